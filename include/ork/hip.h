@@ -1,0 +1,24 @@
+/* ork/hip.h -- MI355X-specific extensions (no reference counterpart). Part of <ork_npu.h>.
+ *
+ * The reference API takes host pointers and returns when C is on the host. A decode loop on a
+ * discrete GPU wants A and C to stay in HBM: allocate them here and pass them to the ordinary run
+ * entry points, which then launch in place (no copies). With async mode on, a run whose A and C are
+ * both device buffers returns right after the launch; ork_npu_sync() waits. */
+#ifndef ORK_HIP_H
+#define ORK_HIP_H
+
+/* Device (HBM) buffer owned by the context, usable in place as A or C. NULL on failure/offline. */
+void        *ork_dev_alloc(ork_npu *ctx, size_t size);
+void         ork_dev_free(ork_npu *ctx, void *ptr);
+/* Synchronous copies between host memory and a device buffer. 0 / -1. */
+int          ork_dev_upload(ork_npu *ctx, void *dst_dev, const void *src, size_t n);
+int          ork_dev_download(ork_npu *ctx, void *dst, const void *src_dev, size_t n);
+/* Async mode for device-resident runs (default 0 = every run synchronizes). */
+void         ork_npu_set_async(ork_npu *ctx, int on);
+/* Wait for every launch on the context's stream. 0 / -1. */
+int          ork_npu_sync(ork_npu *ctx);
+/* The context's hipStream_t, for callers that order their own work after a run (or time it). */
+void        *ork_npu_stream(ork_npu *ctx);
+/* Name of the kernel variant the planner picks for (kind of w, M); for diagnostics and profiling. */
+const char  *ork_w_plan_name(ork_npu *ctx, const ork_w *w, int M);
+#endif

@@ -1,0 +1,54 @@
+/* ork/weights.h -- resident weights: pack, load, dump, free, accessors (MI355X build).
+ * Part of <ork_npu.h>. Packs copy B; the resident form lives in HBM in this build's panel layout
+ * (not the reference's NPU tiles). Packs return NULL on bad dims or allocation failure. */
+#ifndef ORK_WEIGHTS_H
+#define ORK_WEIGHTS_H
+
+/* reference include/ork/weights.h:39. B[K][N] row-major fp16. K%32, N%16. */
+ork_w       *ork_f16_mm_pack(ork_npu *ctx, int K, int N, const ork_f16 *B);
+/* reference include/ork/weights.h:47. B[K][N] row-major int8. K%32, N%32. */
+ork_w       *ork_i8_mm_pack(ork_npu *ctx, int K, int N, const int8_t *B);
+/* reference include/ork/weights.h:92. f32[N][K] (n-major); per-output-channel symmetric int8:
+ * mx = max(1e-9, max|w|), q = clamp(rint(w * (127/mx)), -127, 127), bscale_out[n] = mx/127 (nullable). */
+ork_w       *ork_i8_mm_pack_f32(ork_npu *ctx, int K, int N, const float *f32, float *bscale_out);
+
+/* reference include/ork/weights.h:115 */
+enum { ORK_QK_UNIFORM = 0, ORK_QK_CODEBOOK_NF4 = 1 };
+/* reference include/ork/weights.h:116 and :124. "Effective w4a8": int4 codes per output channel
+ * (uniform: scale = mx/7, q in [-7,7]; NF4 codebook with $ORK_NF4, bscale = mx/127), optional imatrix
+ * clip-grid scale search, stochastic rounding with $ORK_SR. The nibbles stay resident (K*N/2 bytes of
+ * HBM) and are inflated to int8 inside the kernels. Runs via ork_i8_mm_run. K%32, N%32. */
+ork_w       *ork_i4a8_mm_pack(ork_npu *ctx, int K, int N, const float *f32, float *bscale_out);
+ork_w       *ork_i4a8_mm_pack_im(ork_npu *ctx, int K, int N, const float *f32, const float *imatrix, float *bscale_out);
+/* reference include/ork/weights.h:125. W4A4: B[K][N] int4 values [-8,7] in int8 containers. K%32, N%64. */
+ork_w       *ork_i4_mm_pack(ork_npu *ctx, int K, int N, const int8_t *B);
+
+/* reference include/ork/weights.h:141. Frees the handle; its device memory is reclaimed at
+ * ork_npu_free (as in the reference, where device buffers go at context teardown). */
+void         ork_w_free(ork_w *w);
+/* reference include/ork/weights.h:149. Frees the handle and its device memory now. */
+void         ork_mm_free(ork_npu *ctx, ork_w *w);
+/* reference include/ork/weights.h:150. Resident device bytes. */
+size_t       ork_w_bytes(const ork_w *w);
+/* reference include/ork/weights.h:154-158 */
+void         ork_w_dims(const ork_w *w, int *K, int *N);
+int          ork_w_quant_kind(const ork_w *w);
+const float *ork_w_bscale(const ork_w *w);
+/* reference include/ork/weights.h:240. Host codes [K][N] of an OFFLINE weight; NULL when resident. */
+const int8_t *ork_w_codes(const ork_w *w);
+
+/* reference include/ork/weights.h:230. O4N1 blob: {u32 'O4N1', u32 version, i32 K, i32 N,
+ * u32 quant_kind} + f32 bscale[N] + nibbles[N][K/2] (low nibble = even k). out=NULL -> size;
+ * 0 if cap is too small or w has no int4 store. */
+size_t       ork_i4a8_w_dump(const ork_w *w, void *out, size_t cap);
+/* reference include/ork/weights.h:255. NULL on a malformed blob or shape mismatch. */
+ork_w       *ork_i4a8_mm_load(ork_npu *ctx, int K, int N, const void *blob, size_t n);
+/* reference include/ork/weights.h:288 and :294. CPU-only pack straight to an O4N1 blob, byte-identical
+ * to ork_i4a8_mm_pack_im + ork_i4a8_w_dump (nf4 explicit, $ORK_SR honoured). qerr =
+ * sqrt(sum imp*(w-q)^2 / sum imp*w^2). Works on an offline context. */
+size_t       ork_i4a8_pack_cpu_blob(ork_npu *ctx, int K, int N, const float *f32, const float *imatrix, int nf4, void *out, size_t cap);
+size_t       ork_i4a8_pack_cpu_blob_qerr(ork_npu *ctx, int K, int N, const float *f32, const float *imatrix, int nf4, void *out, size_t cap, float *qerr_out);
+
+/* reference include/ork/weights.h:345. A[M][K] fp16, C[M][N] fp32 (caller-allocated). 0 / negative. */
+int          ork_f16_mm_run(ork_npu *ctx, ork_w *w, int M, const ork_f16 *A, float *C);
+#endif

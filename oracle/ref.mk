@@ -1,0 +1,30 @@
+# oracle/ref.mk -- compile the reference's own CPU GEMM / int4-quant translation units IN PLACE from
+# the read-only reference tree and link them, with this directory's driver, into _ref/libork_ref.so.
+# Nothing is copied from the reference; objects and the library go to _ref/ (git-ignored; it travels
+# to the GPU box as a built artefact). clang is used because the reference headers need _Float16,
+# which gcc-11 rejects on x86. Flags follow the reference Makefile (-O2), plus section splitting so
+# the linker can drop every function the driver does not reach; -z defs proves nothing is left
+# unresolved (no stand-in symbols are supplied).
+REF     ?= /root/reference
+HERE    := $(dir $(abspath $(lastword $(MAKEFILE_LIST))))
+OUT     := $(HERE)_ref
+CLANG   ?= /opt/rocm/llvm/bin/clang
+CFLAGS  := -O2 -fPIC -std=gnu11 -w -ffp-contract=off -ffunction-sections -fdata-sections \
+           -I$(REF)/include -I$(REF)/src -pthread
+SRCS    := $(REF)/src/npu/core/buf.c $(REF)/src/npu/i4/quant.c
+OBJS    := $(OUT)/buf.o $(OUT)/quant.o $(OUT)/ref_driver.o
+
+$(OUT)/libork_ref.so: $(OBJS)
+	echo '{ global: ref_*; local: *; };' > $(OUT)/ref.map
+	$(CLANG) -shared -fuse-ld=lld -Wl,--gc-sections -Wl,--version-script=$(OUT)/ref.map -Wl,-z,defs \
+	    -o $@ $(OBJS) -lm -pthread
+
+$(OUT)/buf.o: $(REF)/src/npu/core/buf.c
+	mkdir -p $(OUT)
+	$(CLANG) $(CFLAGS) -c $< -o $@
+$(OUT)/quant.o: $(REF)/src/npu/i4/quant.c
+	mkdir -p $(OUT)
+	$(CLANG) $(CFLAGS) -c $< -o $@
+$(OUT)/ref_driver.o: $(HERE)ref_driver.c
+	mkdir -p $(OUT)
+	$(CLANG) $(CFLAGS) -c $< -o $@

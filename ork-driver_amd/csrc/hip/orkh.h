@@ -1,0 +1,103 @@
+/* orkh.h -- the thin C-ABI between the C host library and HIP (gfx950 / MI355X).
+ *
+ * Plain C: no HIP types cross this boundary. Streams are opaque `void *` (a hipStream_t underneath),
+ * device memory is `void *`. Every call returns 0 on success and a negative value on a HIP error,
+ * with the HIP error string available from orkh_last_error().
+ *
+ * Resident weight layout ("panels") shared by every kernel
+ * -------------------------------------------------------
+ * B[K][N] is stored as 1 KiB blocks, block (nb, kb) at byte offset (nb * KB + kb) * 1024, where
+ * nb = n / 16 indexes a 16-column output panel and kb indexes a K-block; KB = Kp / KPB blocks per panel.
+ * Inside a block, lane l (0..63) of a wave owns the 16 bytes at l*16: column n = nb*16 + (l % 16) and
+ * the K-chunk selected by g = l / 16:
+ *   ORKH_I8   int8,   KPB = 64:  bytes i = 0..15 hold k = kb*64 + g*16 + i
+ *   ORKH_F16  fp16,   KPB = 32:  halves i = 0..7 hold k = kb*32 + g*8 + i
+ *   ORKH_I4U / ORKH_NF4 nibbles, KPB = 128: dword d (0..3), byte b (0..3) holds
+ *             k = kb*128 + g*32 + d*8 + b in its low nibble and k + 4 in its high nibble.
+ *             ORKH_I4U nibbles are two's-complement int4 codes; ORKH_NF4 nibbles index a 16-entry
+ *             int8 codebook (lut).
+ * Padding k >= K is zero (code 0; for NF4 the index of the 0 level). One wave-wide 16-byte load per
+ * lane fetches one whole block: the GEMV streams B with perfectly coalesced 1 KiB reads and the same
+ * bytes are already an MFMA B-fragment (v_mfma_*_16x16x{64 i8, 32 f16}: lane%16 = column,
+ * lane/16 = K-group). A and B fragments use the same lane/byte -> k assignment, so the MFMA's
+ * internal k order never matters for the (exact, integer) result.
+ */
+#ifndef ORKH_H
+#define ORKH_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORKH_I8 = 0, ORKH_I4U = 1, ORKH_NF4 = 2, ORKH_F16 = 3 };
+
+typedef struct orkh_dev {
+    int ordinal;
+    int cu_count;         /* multiProcessorCount */
+    int clock_khz;        /* peak shader clock */
+    int mem_clock_khz;
+    int mem_bus_bits;
+    size_t lds_per_block; /* sharedMemPerBlock */
+    size_t hbm_bytes;     /* totalGlobalMem */
+    int l2_bytes;
+    char arch[64];        /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    char name[256];
+} orkh_dev;
+
+/* ---- runtime ---- */
+int         orkh_device_count(void);
+int         orkh_init(int ordinal, orkh_dev *out, void **stream_out);
+void        orkh_stream_destroy(void *stream);
+const char *orkh_last_error(void);
+void       *orkh_malloc(size_t n);                 /* device memory (HBM); NULL on failure */
+int         orkh_free(void *p);
+void       *orkh_host_alloc(size_t n);             /* pinned, device-mapped host memory */
+int         orkh_host_free(void *p);
+int         orkh_h2d(void *dst, const void *src, size_t n, void *stream);   /* async; direction inferred */
+int         orkh_d2h(void *dst, const void *src, size_t n, void *stream);   /* async */
+int         orkh_d2d(void *dst, const void *src, size_t n, void *stream);   /* async */
+int         orkh_sync(void *stream);
+int         orkh_device_sync(void);
+/* 1 if p is device (or device-mapped) memory known to the HIP runtime, 0 if plain host memory. */
+int         orkh_ptr_is_device(const void *p);
+
+/* ---- matmul launch ---- */
+enum { ORKH_ALGO_STREAM = 0, ORKH_ALGO_TILED = 1 };
+
+/* One C[M][N] = A[M][K] x B[K][N] launch on resident panels. A is row-major with row stride lda
+ * elements (int8 for the integer kinds, fp16 for ORKH_F16); C is row-major int32 (integer kinds) or
+ * fp32 (ORKH_F16) with row stride ldc elements. All pointers are device pointers; A and B must be
+ * 16-byte aligned and lda*elem a multiple of 16 bytes. */
+typedef struct orkh_mm {
+    int kind;
+    int M, K, N;
+    int KB;               /* K-blocks per panel (Kp / KPB) */
+    const void *A;
+    int lda;
+    const void *B;
+    void *C;
+    int ldc;
+    uint32_t lut[4];      /* ORKH_NF4 codebook, entry e in byte e%4 of lut[e/4] */
+} orkh_mm;
+
+/* Launch plan chosen by the host planner (ork-driver_amd/csrc/host/plan.c). */
+typedef struct orkh_plan {
+    int algo;             /* ORKH_ALGO_STREAM | ORKH_ALGO_TILED */
+    /* STREAM: grid (N/16, ksplit), wpg waves per workgroup, each wave kbw K-blocks of one panel,
+     * mt = ceil(M/16) row tiles (1..4). ksplit > 1 writes partials to ws and adds a reduce pass. */
+    int mt, wpg, kbw, kbs, ksplit;
+    /* TILED: bm x bn output tile per 256-thread workgroup, K staged through LDS. */
+    int bm, bn;
+    void *ws;             /* split-K partials, >= ksplit*M*N*4 bytes (device) */
+} orkh_plan;
+
+int orkh_mm_launch(const orkh_mm *p, const orkh_plan *plan, void *stream);
+/* Names of the compiled kernel variants, for diagnostics ("stream_i8_mt1_w4", ...). */
+const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *plan);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

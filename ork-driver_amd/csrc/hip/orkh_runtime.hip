@@ -1,0 +1,135 @@
+// orkh_runtime.hip -- device, memory and stream half of the thin C-ABI HIP layer (see orkh.h).
+//
+// Replaces the reference's L1 substrate for the matmul path: orki_bcreate / MEM_CREATE+MAP
+// (src/npu/core/buf.c:47-80) become hipMalloc, orki_bsync cache maintenance becomes async copies on
+// the context's stream, and the DRM submit ioctl (src/npu/core/submit.c:270-296) becomes a kernel
+// launch on that stream (orkh_kernels.hip).
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "orkh.h"
+
+static thread_local char g_err[256];
+
+static int fail(hipError_t e, const char *what) {
+    snprintf(g_err, sizeof g_err, "%s: %s", what, hipGetErrorString(e));
+    return -1;
+}
+#define CK(call, what)                                  \
+    do {                                                \
+        hipError_t e_ = (call);                         \
+        if (e_ != hipSuccess) return fail(e_, what);    \
+    } while (0)
+
+extern "C" {
+
+const char *orkh_last_error(void) { return g_err; }
+
+int orkh_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int orkh_init(int ordinal, orkh_dev *out, void **stream_out) {
+    int n = 0;
+    CK(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    if (ordinal < 0 || ordinal >= n) {
+        snprintf(g_err, sizeof g_err, "device %d not present (%d visible)", ordinal, n);
+        return -1;
+    }
+    CK(hipSetDevice(ordinal), "hipSetDevice");
+    hipDeviceProp_t p;
+    CK(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
+    if (out) {
+        memset(out, 0, sizeof *out);
+        out->ordinal = ordinal;
+        out->cu_count = p.multiProcessorCount;
+        out->clock_khz = p.clockRate;
+        out->mem_clock_khz = p.memoryClockRate;
+        out->mem_bus_bits = p.memoryBusWidth;
+        out->lds_per_block = p.sharedMemPerBlock;
+        out->hbm_bytes = p.totalGlobalMem;
+        out->l2_bytes = p.l2CacheSize;
+        snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+        snprintf(out->name, sizeof out->name, "%s", p.name);
+    }
+    if (stream_out) {
+        hipStream_t s;
+        // Default priority on purpose: one in-order stream per context.
+        CK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+        *stream_out = (void *)s;
+    }
+    return 0;
+}
+
+void orkh_stream_destroy(void *stream) {
+    if (stream) (void)hipStreamDestroy((hipStream_t)stream);
+}
+
+void *orkh_malloc(size_t n) {
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, n ? n : 1);
+    if (e != hipSuccess) { fail(e, "hipMalloc"); return nullptr; }
+    return p;
+}
+
+int orkh_free(void *p) {
+    if (!p) return 0;
+    CK(hipFree(p), "hipFree");
+    return 0;
+}
+
+void *orkh_host_alloc(size_t n) {
+    void *p = nullptr;
+    hipError_t e = hipHostMalloc(&p, n ? n : 1, hipHostMallocMapped | hipHostMallocPortable);
+    if (e != hipSuccess) { fail(e, "hipHostMalloc"); return nullptr; }
+    return p;
+}
+
+int orkh_host_free(void *p) {
+    if (!p) return 0;
+    CK(hipHostFree(p), "hipHostFree");
+    return 0;
+}
+
+int orkh_h2d(void *dst, const void *src, size_t n, void *stream) {
+    if (!n) return 0;
+    CK(hipMemcpyAsync(dst, src, n, hipMemcpyDefault, (hipStream_t)stream), "hipMemcpyAsync H2D");
+    return 0;
+}
+
+int orkh_d2h(void *dst, const void *src, size_t n, void *stream) {
+    if (!n) return 0;
+    CK(hipMemcpyAsync(dst, src, n, hipMemcpyDefault, (hipStream_t)stream), "hipMemcpyAsync D2H");
+    return 0;
+}
+
+int orkh_d2d(void *dst, const void *src, size_t n, void *stream) {
+    if (!n) return 0;
+    CK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)stream), "hipMemcpyAsync D2D");
+    return 0;
+}
+
+int orkh_sync(void *stream) {
+    CK(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    return 0;
+}
+
+int orkh_device_sync(void) {
+    CK(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    return 0;
+}
+
+int orkh_ptr_is_device(const void *p) {
+    if (!p) return 0;
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();  // plain host memory reports an error here; clear it
+        return 0;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+}  // extern "C"

@@ -1,0 +1,280 @@
+/* context.c -- context lifecycle, buffer registries, diagnostics, worker pool.
+ *
+ * Reference roles: ork_npu_init / ork_npu_init_offline (src/npu/core/sched.c:41-117, :137-145),
+ * ork_npu_free (src/npu/core/device.c:239-300), introspection (src/npu/core/device.c:315-321, :377-385),
+ * ork_dma_alloc / ork_dma_free / orki_dma_find (src/npu/core/buf.c:271-280, :298), ork_parallel_for
+ * (src/npu/core/sched.c:192). On MI355X the context opens one HIP device, creates one in-order stream
+ * and owns every device allocation made through it. */
+#define _GNU_SOURCE
+#include <stdarg.h>
+#include <stdatomic.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#include "internal.h"
+
+static atomic_long g_io_fail;
+
+void orki_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    fputs("[ork] ", stderr);
+    vfprintf(stderr, fmt, ap);
+    fputc('\n', stderr);
+    va_end(ap);
+}
+
+void orki_hip_fail(const char *what) {
+    atomic_fetch_add(&g_io_fail, 1);
+    orki_err("HIP failure in %s: %s", what, orkh_last_error());
+}
+
+long ork_io_failures(void) { return atomic_load(&g_io_fail); }
+
+const char *ork_npu_version(void) { return ORK_NPU_VERSION "+mi355x"; }
+uint32_t ork_pack_format_version(void) { return ORK_PACK_FORMAT_VERSION; }
+
+/* ---- worker pool ------------------------------------------------------------------------------ */
+struct pf_job { void (*fn)(int, int, void *); void *arg; int lo, hi; };
+static void *pf_run(void *p) {
+    struct pf_job *j = p;
+    j->fn(j->lo, j->hi, j->arg);
+    return NULL;
+}
+
+void orki_parallel_for(int n, void (*fn)(int lo, int hi, void *arg), void *arg) {
+    if (n <= 0) return;
+    long nc = sysconf(_SC_NPROCESSORS_ONLN);
+    const char *e = getenv("ORK_PACK_THREADS");
+    if (e && atoi(e) > 0) nc = atoi(e);
+    int nt = (int)(nc < 1 ? 1 : nc > 64 ? 64 : nc);
+    if (nt > n) nt = n;
+    if (nt <= 1) { fn(0, n, arg); return; }
+    pthread_t th[64];
+    struct pf_job jobs[64];
+    int joined[64] = {0};
+    for (int t = 0; t < nt; t++) {
+        jobs[t] = (struct pf_job){fn, arg, (int)((long)n * t / nt), (int)((long)n * (t + 1) / nt)};
+        if (t == 0) continue;
+        if (pthread_create(&th[t], NULL, pf_run, &jobs[t]) == 0) joined[t] = 1;
+        else fn(jobs[t].lo, jobs[t].hi, arg); /* no thread: run the chunk here */
+    }
+    fn(jobs[0].lo, jobs[0].hi, arg);
+    for (int t = 1; t < nt; t++)
+        if (joined[t]) pthread_join(th[t], NULL);
+}
+
+/* ---- lifecycle --------------------------------------------------------------------------------- */
+static ork_npu *ctx_new(void) {
+    ork_npu *c = calloc(1, sizeof *c);
+    if (!c) return NULL;
+    pthread_mutex_init(&c->mu, NULL);
+    return c;
+}
+
+ork_npu *ork_npu_init(void) {
+    if (orkh_device_count() < 1) {
+        orki_err("ork_npu_init: no HIP device visible");
+        return NULL;
+    }
+    int ord = 0;
+    const char *e = getenv("ORK_HIP_DEVICE");
+    if (e) ord = atoi(e);
+    ork_npu *c = ctx_new();
+    if (!c) return NULL;
+    if (orkh_init(ord, &c->dev, &c->stream) != 0) {
+        orki_err("ork_npu_init: %s", orkh_last_error());
+        pthread_mutex_destroy(&c->mu);
+        free(c);
+        return NULL;
+    }
+    /* "gfx950:sramecc+:xnack-" -> "gfx950" */
+    size_t i = 0;
+    while (c->dev.arch[i] && c->dev.arch[i] != ':' && i + 1 < sizeof c->soc) { c->soc[i] = c->dev.arch[i]; i++; }
+    c->soc[i] = 0;
+    c->cores = c->dev.cu_count;
+    c->core_budget = c->cores;
+    if (strcmp(c->soc, "gfx950") != 0)
+        orki_err("ork_npu_init: device is %s, kernels are built for gfx950 only", c->soc);
+    return c;
+}
+
+ork_npu *ork_npu_init_offline(const char *soc_id) {
+    static const struct { const char *id; int cores; } known[] = {
+        {"gfx950", 256}, {"mi355x", 256}, {"rk3588", 3}, {"rk3576", 2}};
+    int hit = -1;
+    for (int i = 0; soc_id && i < (int)(sizeof known / sizeof known[0]); i++)
+        if (!strcmp(soc_id, known[i].id)) hit = i;
+    if (hit < 0) {
+        orki_err("ERROR: ork_npu_init_offline: unknown SoC id \"%s\"", soc_id ? soc_id : "(null)");
+        return NULL;
+    }
+    ork_npu *c = ctx_new();
+    if (!c) return NULL;
+    c->offline = 1;
+    snprintf(c->soc, sizeof c->soc, "%s", known[hit].id);
+    c->cores = known[hit].cores;
+    c->core_budget = c->cores;
+    return c;
+}
+
+void ork_npu_free(ork_npu *c) {
+    if (!c) return;
+    if (!c->offline) {
+        if (c->stream) (void)orkh_sync(c->stream);
+        orkh_free(c->sA.p);
+        orkh_free(c->sC.p);
+        orkh_free(c->sW.p);
+        for (int i = 0; i < c->dma_n; i++) orkh_host_free(c->dma[i].p);
+        for (int i = 0; i < c->devb_n; i++) orkh_free(c->devb[i].p);
+        for (int i = 0; i < c->orphan_n; i++) orkh_free(c->orphan[i]);
+        orkh_stream_destroy(c->stream);
+    }
+    free(c->devb);
+    free(c->orphan);
+    pthread_mutex_destroy(&c->mu);
+    free(c);
+}
+
+const char *ork_npu_soc(const ork_npu *c) { return c ? c->soc : NULL; }
+const char *ork_npu_soc_id(ork_npu *c) { return c ? c->soc : NULL; }
+int ork_npu_cores(const ork_npu *c) { return c ? c->cores : 0; }
+int ork_npu_validated(const ork_npu *c) { return c && !strcmp(c->soc, "gfx950"); }
+void ork_npu_set_core_budget(ork_npu *c, int n) {
+    if (!c) return;
+    c->core_budget = (n > 0 && n <= c->cores) ? n : c->cores;
+}
+
+int orki_need_device(const ork_npu *c, const char *who) {
+    if (!c) { orki_err("%s: NULL context", who); return -1; }
+    if (c->offline) {
+        orki_err("%s: offline context has no device (this build has no CPU fallback)", who);
+        return -1;
+    }
+    return 0;
+}
+
+/* ---- staging / registries ---------------------------------------------------------------------- */
+void *orki_stage(ork_npu *c, struct ork_buf *b, size_t n) {
+    if (b->n >= n && b->p) return b->p;
+    size_t want = n < 65536 ? 65536 : n;
+    want = (want + 4095) & ~(size_t)4095;
+    if (b->p) {
+        if (orkh_sync(c->stream) != 0) orki_hip_fail("stage sync");
+        orkh_free(b->p);
+    }
+    b->p = orkh_malloc(want);
+    b->n = b->p ? want : 0;
+    if (!b->p) orki_hip_fail("staging alloc");
+    return b->p;
+}
+
+void *ork_dma_alloc(ork_npu *c, size_t size) {
+    if (!c || c->offline || !size) return NULL;
+    pthread_mutex_lock(&c->mu);
+    void *p = NULL;
+    if (c->dma_n < ORK_DMA_MAX) {
+        p = orkh_host_alloc(size);
+        if (p) c->dma[c->dma_n++] = (struct ork_buf){p, size};
+        else orki_hip_fail("ork_dma_alloc");
+    }
+    pthread_mutex_unlock(&c->mu);
+    return p;
+}
+
+void ork_dma_free(ork_npu *c, void *ptr) {
+    if (!c || !ptr) return;
+    pthread_mutex_lock(&c->mu);
+    for (int i = 0; i < c->dma_n; i++)
+        if (c->dma[i].p == ptr) {
+            (void)orkh_sync(c->stream);
+            orkh_host_free(ptr);
+            c->dma[i] = c->dma[--c->dma_n];
+            break;
+        }
+    pthread_mutex_unlock(&c->mu);
+}
+
+int orki_dma_find(ork_npu *c, const void *p) {
+    for (int i = 0; i < c->dma_n; i++) {
+        const char *b = c->dma[i].p;
+        if ((const char *)p >= b && (const char *)p < b + c->dma[i].n) return 1;
+    }
+    return 0;
+}
+
+void *ork_dev_alloc(ork_npu *c, size_t size) {
+    if (!c || c->offline || !size) return NULL;
+    void *p = orkh_malloc(size);
+    if (!p) { orki_hip_fail("ork_dev_alloc"); return NULL; }
+    pthread_mutex_lock(&c->mu);
+    if (c->devb_n == c->devb_cap) {
+        int nc = c->devb_cap ? 2 * c->devb_cap : 16;
+        struct ork_buf *nb = realloc(c->devb, (size_t)nc * sizeof *nb);
+        if (!nb) { pthread_mutex_unlock(&c->mu); orkh_free(p); return NULL; }
+        c->devb = nb;
+        c->devb_cap = nc;
+    }
+    c->devb[c->devb_n++] = (struct ork_buf){p, size};
+    pthread_mutex_unlock(&c->mu);
+    return p;
+}
+
+void ork_dev_free(ork_npu *c, void *ptr) {
+    if (!c || !ptr) return;
+    pthread_mutex_lock(&c->mu);
+    for (int i = 0; i < c->devb_n; i++)
+        if (c->devb[i].p == ptr) {
+            (void)orkh_sync(c->stream);
+            orkh_free(ptr);
+            c->devb[i] = c->devb[--c->devb_n];
+            break;
+        }
+    pthread_mutex_unlock(&c->mu);
+}
+
+int orki_dev_find(ork_npu *c, const void *p, size_t n) {
+    for (int i = 0; i < c->devb_n; i++) {
+        const char *b = c->devb[i].p;
+        if ((const char *)p >= b && (const char *)p + n <= b + c->devb[i].n) return 1;
+    }
+    return 0;
+}
+
+int ork_dev_upload(ork_npu *c, void *dst, const void *src, size_t n) {
+    if (orki_need_device(c, "ork_dev_upload")) return -1;
+    if (orkh_h2d(dst, src, n, c->stream) || orkh_sync(c->stream)) { orki_hip_fail("ork_dev_upload"); return -1; }
+    return 0;
+}
+
+int ork_dev_download(ork_npu *c, void *dst, const void *src, size_t n) {
+    if (orki_need_device(c, "ork_dev_download")) return -1;
+    if (orkh_d2h(dst, src, n, c->stream) || orkh_sync(c->stream)) { orki_hip_fail("ork_dev_download"); return -1; }
+    return 0;
+}
+
+void ork_npu_set_async(ork_npu *c, int on) { if (c) c->async = on ? 1 : 0; }
+
+int ork_npu_sync(ork_npu *c) {
+    if (orki_need_device(c, "ork_npu_sync")) return -1;
+    if (orkh_sync(c->stream)) { orki_hip_fail("ork_npu_sync"); return -1; }
+    return 0;
+}
+
+void *ork_npu_stream(ork_npu *c) { return (c && !c->offline) ? c->stream : NULL; }
+
+void orki_orphan(ork_npu *c, void *dptr) {
+    if (!c || !dptr) return;
+    pthread_mutex_lock(&c->mu);
+    if (c->orphan_n == c->orphan_cap) {
+        int nc = c->orphan_cap ? 2 * c->orphan_cap : 16;
+        void **no = realloc(c->orphan, (size_t)nc * sizeof *no);
+        if (!no) { pthread_mutex_unlock(&c->mu); (void)orkh_sync(c->stream); orkh_free(dptr); return; }
+        c->orphan = no;
+        c->orphan_cap = nc;
+    }
+    c->orphan[c->orphan_n++] = dptr;
+    pthread_mutex_unlock(&c->mu);
+}

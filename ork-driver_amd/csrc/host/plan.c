@@ -1,0 +1,72 @@
+/* plan.c -- the MI355X matmul planner: which kernel, what grid, how K is split.
+ *
+ * Replaces the reference's K-split / N-tile / M-tile / core-count policy (orki_int8_ks, orki_budget,
+ * orki_run_loop_chunk, the mg_max*64 M-tile: src/npu.c:131-160, :1598-1610, :1693-1694;
+ * orki_f16_ks, src/npu/f16/regcmd.c:120-125). The NPU needed K cut into 1024-wide slices, N into
+ * 8192-wide outputs and M into CBUF-sized row groups, each a separate submit with a host int32
+ * accumulate. On MI355X every shape is one launch (plus a reduce pass when K is split across
+ * workgroups); the planner only decides how to fill 256 CUs:
+ *   M <= 64  stream: one 16-column panel per workgroup, waves split K, runs of 8 (4 for int4) 1 KiB
+ *            blocks per wave so ~8 KiB per wave is in flight; K is split across workgroups only when
+ *            the panels alone give fewer than ~4 waves per CU.
+ *   M >  64  tiled: the BM x BN tile (128x96, 128x128 or 64x64) with the fewest tile-rounds of work
+ *            per CU, larger tile on ties. */
+#include <stdlib.h>
+#include <string.h>
+
+#include "internal.h"
+
+static int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes) {
+    (void)K;
+    memset(q, 0, sizeof *q);
+    *ws_bytes = 0;
+    const int cu = (c && c->cores > 0) ? c->cores : 256;
+    const int NB = N / 16;
+    int stream = M <= 64;
+    const char *force = getenv("ORK_PLAN");
+    if (force && !strcmp(force, "tiled")) stream = 0;
+    if (force && !strcmp(force, "stream") && M <= 64) stream = 1;
+
+    if (stream) {
+        q->algo = ORKH_ALGO_STREAM;
+        q->mt = cdiv(M, 16);
+        const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 4 : 8;
+        const int need = cdiv(KB, kbw_target); /* waves per panel at the target run length */
+        const int wpg = need <= 4 ? 4 : 8;
+        int ksplit = cdiv(need, wpg);
+        const int ks_fill = cdiv(4 * cu, NB * wpg); /* enough workgroups to give ~4 waves per CU */
+        if (ks_fill > ksplit) ksplit = ks_fill;
+        const int ks_max = cdiv(KB, wpg) > 0 ? cdiv(KB, wpg) : 1; /* every wave keeps >= 1 block */
+        if (ksplit > ks_max) ksplit = ks_max;
+        if (ksplit < 1) ksplit = 1;
+        const int kbs = cdiv(KB, ksplit);
+        ksplit = cdiv(KB, kbs);
+        q->wpg = wpg;
+        q->kbs = kbs;
+        q->kbw = cdiv(kbs, wpg);
+        q->ksplit = ksplit;
+        if (ksplit > 1) *ws_bytes = (size_t)ksplit * M * N * 4;
+        return 0;
+    }
+
+    static const int cfg[][2] = {{128, 96}, {128, 128}, {64, 64}};
+    long best = -1;
+    int bi = 0;
+    for (int i = 0; i < 3; i++) {
+        const int bm = cfg[i][0], bn = cfg[i][1];
+        const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);
+        const long rounds = (tiles + cu - 1) / cu;
+        const long cost = rounds * bm * bn;
+        if (best < 0 || cost < best || (cost == best && bm * bn > cfg[bi][0] * cfg[bi][1])) {
+            best = cost;
+            bi = i;
+        }
+    }
+    q->algo = ORKH_ALGO_TILED;
+    q->bm = cfg[bi][0];
+    q->bn = cfg[bi][1];
+    q->ksplit = 1;
+    return 0;
+}

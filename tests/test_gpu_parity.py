@@ -1,0 +1,352 @@
+"""GPU parity: the HIP path through the C-ABI vs the CPU oracle and the reference's own goldens.
+
+Bar: bit-exact int32 for every integer path (int8, i4a8 uniform/NF4, W4A4); fp16 within 2e-3 relative
+error (per element, floored at 0.1% of the output range) of an fp64-accumulated reference, and
+bit-exact where the reference's known-answer inputs make every fp32 partial sum exact.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import goldens as G
+import oracle as O
+import ork
+
+pytestmark = pytest.mark.gpu
+
+FP16_TOL = 2e-3  # north_star: max relative error of fp16 -> fp32 results vs fp64 accumulation
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------------------------------------- int8
+I8_SHAPES = [  # (M, K, N): stream and tiled paths, K tails (K%64 == 32), N tails vs the tile width
+    (1, 32, 32), (1, 96, 64), (1, 2048, 6144), (2, 2048, 6144), (15, 160, 96), (16, 2048, 6144),
+    (17, 1024, 128), (33, 2080, 224), (64, 4096, 512), (65, 512, 96), (100, 96, 1568), (128, 2048, 2048),
+    (200, 1056, 416), (512, 2048, 6144), (300, 3072, 4096), (1, 12288, 64), (7, 10752, 160)]
+
+
+@pytest.mark.parametrize("M,K,N", I8_SHAPES)
+def test_i8_random_vs_oracle(npu, M, K, N):
+    _say("i8", M, K, N)
+    rng = _rng(M * 7 + K + N)
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    w = npu.pack_i8(B)
+    assert w
+    rc, C = npu.run_i8(w, A)
+    assert rc == 0
+    assert np.array_equal(C, O.gemm_i32(A, B)), npu.plan_name(w, M)
+    ork.free(w)
+
+
+@pytest.mark.parametrize("M", [1, 16, 64, 512])
+def test_i8_forced_algorithms_agree(npu, M):
+    """The stream and tiled kernels give the same exact result on the same weight."""
+    _say("i8 forced", M)
+    rng = _rng(M)
+    K, N = 1024, 768
+    B = rng.integers(-127, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    w = npu.pack_i8(B)
+    ref = O.gemm_i32(A, B)
+    for algo in (["stream", "tiled"] if M <= 64 else ["tiled"]):
+        os.environ["ORK_PLAN"] = algo
+        try:
+            rc, C = npu.run_i8(w, A)
+        finally:
+            del os.environ["ORK_PLAN"]
+        assert rc == 0 and np.array_equal(C, ref), algo
+    ork.free(w)
+
+
+@pytest.mark.parametrize("idx", range(7))
+def test_quant_c_goldens_on_gpu(npu, idx):
+    """examples/quant.c end to end: ork_i8_mm_pack + ork_i8_mm_run, FNV-64 of C == the reference golden."""
+    for M, K, N, Aq, Bq, gold, hm in G.quant_c_cases(select={idx}):
+        _say("quant.c", M, K, N)
+        w = npu.pack_i8(Bq)
+        rc, C = npu.run_i8(w, Aq)
+        assert rc == 0 and G.chained_hash(C, hm) == gold, (M, K, N)
+        ork.free(w)
+
+
+@pytest.mark.parametrize("shape", range(7))
+def test_chain_prefill_goldens_on_gpu(npu, shape):
+    for M, K, N, A, B, gold, hm in G.tm_chain_cases({shape}):
+        _say("chain_prefill", M, K, N)
+        w = npu.pack_i8(B)
+        rc, C = npu.run_i8(w, A)
+        assert rc == 0 and G.chained_hash(C, hm) == gold, (M, K, N)
+        ork.free(w)
+
+
+def test_check_i8_goldens_on_gpu(npu):
+    for M, K, N, A, B, gold, hm in G.tm_check_i8_cases():
+        _say("check_i8", M, K, N)
+        w = npu.pack_i8(B)
+        h = O.FNV_OFFSET
+        for m in hm:  # the same resident weight run at M = 1, 1, 4, M (test_matmul.c:53-56)
+            rc, C = npu.run_i8(w, A[:m])
+            assert rc == 0
+            h = O.fnv64(C, h)
+        assert h == gold, (M, K, N)
+        ork.free(w)
+
+
+def test_i8_pack_f32_bscale_and_codes(npu):
+    """ork_i8_mm_pack_f32: bscale bit-exact and the resident codes equal the oracle's (via C = I x B)."""
+    rng = _rng(5)
+    K, N = 2048, 512
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    W[3, :] = 0.0  # all-zero channel: mx = 1e-9 floor, codes all 0
+    w, bs = npu.pack_i8_f32(W)
+    codes, bs_ref = O.pack_i8_f32(W)
+    assert np.array_equal(bs, bs_ref)
+    A = np.zeros((64, K), np.int8)
+    for i in range(64):
+        A[i, i * 32] = 1  # row i selects k = 32*i
+    rc, C = npu.run_i8(w, A)
+    assert rc == 0 and np.array_equal(C, codes[::32, :].astype(np.int32))
+    A2 = rng.integers(-127, 128, size=(8, K), dtype=np.int8)
+    rc, C2 = npu.run_i8(w, A2)
+    assert rc == 0 and np.array_equal(C2, O.gemm_i32(A2, codes))
+    ork.free(w)
+
+
+# -------------------------------------------------------------------------------------------- W4A8
+def _i4a8_case(npu, K, N, M, nf4, imatrix, sr, seed):
+    rng = _rng(seed)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    im = rng.uniform(0.5, 2.0, K).astype(np.float32) if imatrix else None
+    env = {"ORK_NF4": nf4, "ORK_SR": sr}
+    for k, v in env.items():
+        if v:
+            os.environ[k] = "1"
+    try:
+        w, bs = npu.pack_i4a8(W, im)
+    finally:
+        for k in env:
+            os.environ.pop(k, None)
+    bs_ref, nib_ref, codes = O.pack_i4a8(W, im, nf4=nf4, sr=sr)
+    return W, im, w, bs, bs_ref, codes, rng
+
+
+@pytest.mark.parametrize("nf4", [0, 1])
+@pytest.mark.parametrize("imatrix", [0, 1])
+@pytest.mark.parametrize("M", [1, 5, 16, 64, 130])
+def test_i4a8_vs_oracle(npu, nf4, imatrix, M):
+    _say("i4a8", nf4, imatrix, M)
+    K, N = 1024, 256
+    W, im, w, bs, bs_ref, codes, rng = _i4a8_case(npu, K, N, M, nf4, imatrix, 0, 100 + M)
+    assert w and np.array_equal(bs, bs_ref)
+    assert ork.lib().ork_w_quant_kind(w) == (1 if nf4 else 0)
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    rc, C = npu.run_i8(w, A)
+    assert rc == 0 and np.array_equal(C, O.gemm_i32(A, codes)), npu.plan_name(w, M)
+    # O4N1 round trip: dump == the oracle's blob bytes, load runs bit-identically, re-dump identical
+    blob = ork.dump_i4a8(w)
+    assert np.array_equal(blob, O.i4a8_blob(W, im, nf4=nf4))
+    w2 = npu.load_i4a8(K, N, blob)
+    rc2, C2 = npu.run_i8(w2, A)
+    assert rc2 == 0 and np.array_equal(C2, C)
+    assert np.array_equal(ork.dump_i4a8(w2), blob)
+    ork.free(w)
+    ork.free(w2)
+
+
+def test_i4a8_stochastic_rounding(npu):
+    K, N, M = 512, 128, 8
+    W, im, w, bs, bs_ref, codes, rng = _i4a8_case(npu, K, N, M, 0, 0, 1, 9)
+    assert np.array_equal(bs, bs_ref)
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    rc, C = npu.run_i8(w, A)
+    assert rc == 0 and np.array_equal(C, O.gemm_i32(A, codes))
+    ork.free(w)
+
+
+# -------------------------------------------------------------------------------------------- W4A4
+I4_SHAPES = [  # examples/i4.c:95-136
+    (1, 64, 64), (4, 128, 128), (2, 256, 64), (1, 12288, 64), (3, 2048, 256), (8, 512, 256), (16, 512, 64),
+    (16, 2048, 64), (16, 2048, 256), (128, 512, 256), (256, 512, 256), (128, 512, 512), (20, 2048, 256),
+    (100, 512, 512), (4, 2048, 256), (32, 1024, 128), (64, 512, 256)]
+
+
+@pytest.mark.parametrize("M,K,N", I4_SHAPES)
+def test_w4a4_i4c_shapes(npu, M, K, N):
+    _say("w4a4", M, K, N)
+    A, B = O.gen_i4_test(M, K, N)
+    w = npu.pack_i4(B)
+    assert w
+    rc, C = npu.run_i4(w, A)
+    assert rc == 0 and np.array_equal(C, O.gemm_i32(A, B)), npu.plan_name(w, M)
+    ork.free(w)
+
+
+def test_w4a4_sattest(npu):
+    """examples/i4.c:37-58: one output cell is exactly 32767, reached without saturation."""
+    M, K, N = 16, 2048, 256
+    A, B = O.gen_i4_sattest(M, K, N)
+    w = npu.pack_i4(B)
+    rc, C = npu.run_i4(w, A)
+    assert rc == 0 and C[0, 0] == 32767 and np.array_equal(C, O.gemm_i32(A, B))
+    ork.free(w)
+
+
+def test_w4a4_extremes(npu):
+    """-8 x -8 everywhere: 64*K exactly (int4 range edges, the x16 widening at its limit)."""
+    M, K, N = 70, 4096, 128
+    A = np.full((M, K), -8, np.int8)
+    B = np.full((K, N), -8, np.int8)
+    w = npu.pack_i4(B)
+    rc, C = npu.run_i4(w, A)
+    assert rc == 0 and np.all(C == 64 * K)
+    ork.free(w)
+
+
+# -------------------------------------------------------------------------------------------- fp16
+def test_fp16_goldens_on_gpu(npu):
+    for M, K, N, A, B, gold, hm in G.tm_fp16_cases():
+        _say("fp16 golden", M, K, N)
+        w = npu.pack_f16(B)
+        h = O.FNV_OFFSET
+        for m in hm:
+            rc, C = npu.run_f16(w, A[:m])
+            assert rc == 0
+            h = O.fnv64(C, h)
+        assert h == gold, (M, K, N)
+        ork.free(w)
+
+
+@pytest.mark.parametrize("M", [1, 16, 128, 512])
+def test_fp16_config_tolerance(npu, M):
+    """A ~ N(0,1), B ~ N(0,0.02), K = N = 2048."""
+    _say("fp16", M)
+    rng = _rng(1000 + M)
+    K = N = 2048
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+    w = npu.pack_f16(B)
+    rc, C = npu.run_f16(w, A)
+    assert rc == 0
+    err = O.fp16_err(C, O.gemm_f16_f64acc(A, B))
+    assert err <= FP16_TOL, (err, npu.plan_name(w, M))
+    ork.free(w)
+
+
+@pytest.mark.parametrize("M,K,N", [(3, 96, 48), (65, 160, 112), (1, 4096, 16)])
+def test_fp16_odd_shapes(npu, M, K, N):
+    rng = _rng(M + K + N)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B = rng.standard_normal((K, N)).astype(np.float16)
+    w = npu.pack_f16(B)
+    rc, C = npu.run_f16(w, A)
+    assert rc == 0 and O.fp16_err(C, O.gemm_f16_f64acc(A, B)) <= FP16_TOL
+    ork.free(w)
+
+
+# ------------------------------------------------------------------------------ full-size properties
+def test_m512_full_size_properties(npu):
+    """The metric's M=512 int8 GEMM at full size: exact on sampled rows, and the column checksum
+    sum_m C[m][n] == (sum_m A[m]) . B[:, n] (exact in int64) over every column."""
+    rng = _rng(512)
+    K, N, M = 2048, 6144, 512
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w, _ = npu.pack_i8_f32(W)
+    codes, _ = O.pack_i8_f32(W)
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    rc, C = npu.run_i8(w, A)
+    assert rc == 0
+    rows = np.r_[0:8, 250:262, 504:512]
+    assert np.array_equal(C[rows], O.gemm_i32(A[rows], codes))
+    colsum = A.astype(np.int64).sum(axis=0) @ codes.astype(np.int64)
+    assert np.array_equal(C.astype(np.int64).sum(axis=0), colsum)
+    ork.free(w)
+
+
+def test_w4a4_config4_full(npu):
+    """A int4[256,4096] x B int4[4096,4096], exact."""
+    rng = _rng(44)
+    M, K, N = 256, 4096, 4096
+    A = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    B = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
+    w = npu.pack_i4(B)
+    rc, C = npu.run_i4(w, A)
+    assert rc == 0
+    rows = np.r_[0:16, 120:136, 240:256]
+    assert np.array_equal(C[rows], O.gemm_i32(A[rows], B))
+    colsum = A.astype(np.int64).sum(axis=0) @ B.astype(np.int64)
+    assert np.array_equal(C.astype(np.int64).sum(axis=0), colsum)
+    ork.free(w)
+
+
+# ---------------------------------------------------------------------------- residency / errors
+def test_device_resident_operands_async(npu):
+    L = ork.lib()
+    rng = _rng(77)
+    K, N, M = 2048, 6144, 1
+    B = rng.integers(-127, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    w = npu.pack_i8(B)
+    dA = L.ork_dev_alloc(npu.h, A.nbytes)
+    dC = L.ork_dev_alloc(npu.h, M * N * 4)
+    assert dA and dC
+    assert L.ork_dev_upload(npu.h, dA, ork.ptr(A), A.nbytes) == 0
+    L.ork_npu_set_async(npu.h, 1)
+    for _ in range(3):
+        assert L.ork_i8_mm_run(npu.h, w, M, dA, dC) == 0
+    assert L.ork_npu_sync(npu.h) == 0
+    L.ork_npu_set_async(npu.h, 0)
+    C = np.empty((M, N), np.int32)
+    assert L.ork_dev_download(npu.h, ork.ptr(C), dC, C.nbytes) == 0
+    assert np.array_equal(C, O.gemm_i32(A, B))
+    L.ork_dev_free(npu.h, dA)
+    L.ork_dev_free(npu.h, dC)
+    ork.free(w)
+
+
+def test_dma_buffers(npu):
+    import ctypes as Ct
+
+    L = ork.lib()
+    rng = _rng(78)
+    K, N, M = 512, 256, 4
+    B = rng.integers(-127, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    w = npu.pack_i8(B)
+    pa = L.ork_dma_alloc(npu.h, A.nbytes)
+    pc = L.ork_dma_alloc(npu.h, M * N * 4)
+    Ct.memmove(pa, A.ctypes.data, A.nbytes)
+    assert L.ork_i8_mm_run(npu.h, w, M, pa, pc) == 0
+    C = np.ctypeslib.as_array(Ct.cast(pc, Ct.POINTER(Ct.c_int32)), shape=(M, N)).copy()
+    assert np.array_equal(C, O.gemm_i32(A, B))
+    L.ork_dma_free(npu.h, pa)
+    L.ork_dma_free(npu.h, pc)
+    ork.free(w)
+
+
+def test_run_errors(npu):
+    import ctypes as Ct
+
+    L = ork.lib()
+    B = np.ones((64, 64), np.int8)
+    wi8 = npu.pack_i8(B)
+    wi4 = npu.pack_i4(B)
+    A = np.ones((1, 64), np.int8)
+    C = np.empty((1, 64), np.int32)
+    assert L.ork_i4_mm_run(npu.h, wi8, 1, ork.ptr(A), ork.ptr(C)) == -1   # dtype mismatch
+    assert L.ork_i8_mm_run(npu.h, wi4, 1, ork.ptr(A), ork.ptr(C)) == -1
+    buf = (Ct.c_int8 * 512)()
+    base = Ct.addressof(buf)
+    assert L.ork_i8_mm_run(npu.h, wi8, 1, base, base + 16) == -1          # A/C overlap (test_matmul.c:559-589)
+    assert L.ork_i8_mm_run(npu.h, wi8, 0, ork.ptr(A), ork.ptr(C)) == -1
+    ork.free(wi8)
+    ork.free(wi4)
+    assert L.ork_io_failures() == 0

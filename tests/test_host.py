@@ -1,0 +1,218 @@
+"""Host-side tests of the product library (CPU only, no compute calls on a GPU).
+
+- libork_npu.so loads and exports every function include/*.h declares
+- offline-context surfaces: ork_i4a8_pack_cpu_blob(_qerr) byte-identical to the oracle, offline
+  pack / load keep the oracle's codes, every run on an offline context fails (-1, no CPU fallback)
+- dims gates, O4N1 validation cases, ork_i8_mm_run_cpu vs the oracle
+"""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle as O
+import ork
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = set()
+    for dirpath, _, files in os.walk(os.path.join(ROOT, "include")):
+        for f in files:
+            if f.endswith(".h"):
+                text = open(os.path.join(dirpath, f)).read()
+                text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+                names |= set(re.findall(r"\b(ork_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_exports_every_declared_symbol():
+    declared = _declared_functions()
+    assert len(declared) >= 40
+    L = ork.lib()
+    missing = [n for n in sorted(declared) if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(ork.API) == declared  # the binding covers exactly the declared API
+
+
+def test_version_strings():
+    L = ork.lib()
+    assert L.ork_npu_version().decode() == "1.0.190+mi355x"
+    assert L.ork_pack_format_version() == 1
+
+
+@pytest.fixture
+def off():
+    c = ork.Npu(offline="gfx950")
+    yield c
+    c.close()
+
+
+def test_offline_unknown_soc():
+    assert not ork.lib().ork_npu_init_offline(b"nope")
+
+
+@pytest.mark.parametrize("nf4", [0, 1])
+@pytest.mark.parametrize("imatrix", [0, 1])
+@pytest.mark.parametrize("K,N", [(1024, 256), (1536, 128), (96, 64)])
+def test_cpu_blob_matches_oracle(off, nf4, imatrix, K, N):
+    rng = np.random.default_rng(K + N + nf4 + 10 * imatrix)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    W[0, :5] = [0.0, 1e-12, -1e-12, 0.5, -0.5]
+    im = rng.uniform(0.5, 2.0, K).astype(np.float32) if imatrix else None
+    blob, q = ork.cpu_blob(K, N, W, im, nf4=nf4, ctx=off.h, qerr=True)
+    ref, qref = O.i4a8_blob(W, im, nf4=nf4, want_qerr=True)
+    assert np.array_equal(blob, ref)
+    assert q == qref and 0.0 < q < 1.0
+
+
+def test_cpu_blob_stochastic_rounding(off):
+    rng = np.random.default_rng(3)
+    K, N = 512, 64
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    os.environ["ORK_SR"] = "1"
+    try:
+        for nf4 in (0, 1):
+            blob = ork.cpu_blob(K, N, W, None, nf4=nf4, ctx=off.h)
+            assert np.array_equal(blob, O.i4a8_blob(W, None, nf4=nf4, sr=True))
+            assert not np.array_equal(blob, O.i4a8_blob(W, None, nf4=nf4, sr=False))
+    finally:
+        del os.environ["ORK_SR"]
+
+
+def test_cpu_blob_dims_and_cap(off):
+    W = np.zeros((64, 100), np.float32)
+    assert ork.lib().ork_i4a8_pack_cpu_blob(off.h, 100, 64, ork.ptr(W), None, 0, None, 0) == 0
+    W = np.ones((64, 64), np.float32)
+    need = ork.lib().ork_i4a8_pack_cpu_blob(off.h, 64, 64, ork.ptr(W), None, 0, None, 0)
+    assert need == 20 + 64 * 4 + 64 * 64 // 2  # examples/test_matmul.c:528
+    small = np.zeros(need - 1, np.uint8)
+    assert ork.lib().ork_i4a8_pack_cpu_blob(off.h, 64, 64, ork.ptr(W), None, 0, ork.ptr(small), need - 1) == 0
+
+
+@pytest.mark.parametrize("nf4", [0, 1])
+def test_offline_pack_i4a8_codes_and_dump(off, nf4):
+    rng = np.random.default_rng(21 + nf4)
+    K, N = 512, 96
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    im = rng.uniform(0.5, 2.0, K).astype(np.float32)
+    if nf4:
+        os.environ["ORK_NF4"] = "1"
+    try:
+        w, bs = off.pack_i4a8(W, im)
+    finally:
+        os.environ.pop("ORK_NF4", None)
+    bs_ref, nib_ref, codes_ref = O.pack_i4a8(W, im, nf4=nf4)
+    assert w and np.array_equal(bs, bs_ref)
+    assert np.array_equal(ork.bscale(w, N), bs_ref)
+    assert np.array_equal(ork.codes(w, K, N), codes_ref)
+    assert ork.lib().ork_w_quant_kind(w) == nf4
+    blob = ork.dump_i4a8(w)
+    assert np.array_equal(blob, O.i4a8_blob(W, im, nf4=nf4))
+    # offline load of that blob recovers exactly the same codes (examples/test_offline_load.c:44-77)
+    w2 = off.load_i4a8(K, N, blob)
+    assert np.array_equal(ork.codes(w2, K, N), codes_ref)
+    assert np.array_equal(ork.dump_i4a8(w2), blob)
+    # and a run on an offline context is refused, not computed on the CPU
+    A = np.ones((1, K), np.int8)
+    rc, _ = off.run_i8(w, A)
+    assert rc == -1
+    ork.free(w)
+    ork.free(w2)
+
+
+def test_offline_i4a8_identity_roundtrip(off):
+    """examples/test_offline_load.c:44-77: codes in [-7,7] with one +7 per channel pack to themselves."""
+    rng = np.random.default_rng(4)
+    K, N = 1536, 256
+    codes = rng.integers(-7, 8, size=(K, N), dtype=np.int8)
+    codes[0, :] = 7
+    W = codes.T.astype(np.float32).copy()
+    blob = ork.cpu_blob(K, N, W, None, nf4=0, ctx=off.h)
+    w = off.load_i4a8(K, N, blob)
+    assert np.array_equal(ork.codes(w, K, N), codes)
+    assert np.all(ork.bscale(w, N) == np.float32(1.0))
+    ork.free(w)
+
+
+def test_o4n1_rejections(off):
+    rng = np.random.default_rng(5)
+    K, N = 64, 32
+    W = rng.standard_normal((N, K)).astype(np.float32)
+    blob = ork.cpu_blob(K, N, W, None, ctx=off.h)
+    assert off.load_i4a8(K, N, blob)
+    bad = []
+    b = blob.copy(); b[0] ^= 1; bad.append(("magic", K, N, b))
+    b = blob.copy(); b[4] = 2; bad.append(("version", K, N, b))
+    b = blob.copy(); b[16] = 2; bad.append(("kind", K, N, b))
+    bad.append(("K", 96, N, blob))
+    bad.append(("N", K, 64, blob))
+    bad.append(("short", K, N, blob[:-1]))
+    bad.append(("long", K, N, np.concatenate([blob, np.zeros(1, np.uint8)])))
+    for name, k, n, b in bad:
+        assert not off.load_i4a8(k, n, b), name
+    assert O.o4n1_decode(K, N, blob) is not None
+
+
+def test_offline_pack_i8_f32_codes(off):
+    rng = np.random.default_rng(6)
+    K, N = 2048, 512
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w, bs = off.pack_i8_f32(W)
+    codes, bs_ref = O.pack_i8_f32(W)
+    assert np.array_equal(bs, bs_ref)
+    assert np.array_equal(ork.codes(w, K, N), codes)
+    ork.free(w)
+
+
+def test_dims_gates(off):
+    L = ork.lib()
+    B = np.zeros(64 * 128, np.int8)
+    F = np.zeros(64 * 128, np.float32)
+    H = np.zeros(64 * 128, np.float16)
+    assert not L.ork_i8_mm_pack(off.h, 48, 64, ork.ptr(B))       # K%32
+    assert not L.ork_i8_mm_pack(off.h, 64, 48, ork.ptr(B))       # N%32
+    assert not L.ork_i8_mm_pack_f32(off.h, 64, 16, ork.ptr(F), None)
+    assert not L.ork_i4a8_mm_pack(off.h, 64, 16, ork.ptr(F), None)
+    assert not L.ork_i4_mm_pack(off.h, 64, 32, ork.ptr(B))       # N%64
+    assert not L.ork_f16_mm_pack(off.h, 64, 8, ork.ptr(H))       # N%16
+    w = L.ork_i4_mm_pack(off.h, 64, 64, ork.ptr(B))
+    assert w
+    L.ork_w_free(w)
+
+
+def test_offline_runs_fail(off):
+    L = ork.lib()
+    B = np.ones((64, 64), np.int8)
+    w = off.pack_i8(B)
+    A = np.ones((2, 64), np.int8)
+    Cm = np.zeros((2, 64), np.int32)
+    assert L.ork_i8_mm_run(off.h, w, 2, ork.ptr(A), ork.ptr(Cm)) == -1
+    assert np.all(Cm == 0)
+    assert L.ork_dma_alloc(off.h, 64) is None
+    assert L.ork_dev_alloc(off.h, 64) is None
+    ork.free(w)
+
+
+def test_cpu_gemm_api_matches_oracle():
+    st = O.LCGState(7777)
+    for M, K, N, lo, hi in [(1, 1024, 1024, -8, 7), (32, 1024, 1024, -8, 7), (4, 512, 256, -128, 127), (3, 130, 144, -8, 7)]:
+        A = O.gen_cpu_gemm(st, lo, hi, M * K).reshape(M, K)
+        B = O.gen_cpu_gemm(st, lo, hi, K * N).reshape(K, N)
+        Cm = np.empty((M, N), np.int32)
+        ork.lib().ork_i8_mm_run_cpu(M, K, N, ork.ptr(A), ork.ptr(B), ork.ptr(Cm))
+        assert np.array_equal(Cm, O.gemm_i32(A, B))
+
+
+def test_accessors_null_safe():
+    L = ork.lib()
+    K = C.c_int(5)
+    N = C.c_int(5)
+    L.ork_w_dims(None, C.byref(K), C.byref(N))
+    assert (K.value, N.value) == (0, 0)
+    assert L.ork_w_quant_kind(None) == -1
+    assert L.ork_w_bscale(None) is None
+    assert L.ork_i4a8_w_dump(None, None, 0) == 0
