@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Benchmark of the resident-weight matmul hot path on one MI355X, through the drop-in C-ABI.
+
+Metric: "w8a8 M=1 GEMV HBM GB/s (% peak); M=512 int8 GEMM TOPS (% MFMA peak)".
+Workload (BASELINE config 1 shape): W f32[6144][2048] ~ N(0,0.02) seeded, packed once with
+ork_i8_mm_pack_f32 (per-channel int8); A int8 ~ U[-127,127]; C int32. A step is one ork_i8_mm_run
+call (M=1 for the headline value). The weight is packed into R=48 resident copies (48 x 12.6 MB =
+605 MB > 2 x the 256 MB MALL) and consecutive steps rotate through them, so every step streams its
+weight from HBM. A and C live in HBM (ork_dev_alloc); the steps are captured into one HIP graph and
+timed with HIP events on the library's stream, bracketed by device synchronisation.
+
+Also reported on the same line: the M=512 int8 GEMM (TOPS, % of dense int8 MFMA peak) as "m512",
+the eager (non-graph) launch rate, and the CPU baseline: the reference's own CPU GEMM
+(orki_cpu_gemm_i32, compiled from its sources into oracle/_ref) timed on the host, single-threaded
+as the reference builds it, on a bounded sample of the same workload.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ork-driver_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+K, N = 2048, 6144
+R = 48                          # rotated resident weight copies
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5000.0         # MI355X dense int8 MFMA, TOP/s
+
+
+def algo_bytes(M):
+    return K * N + M * K + 4 * M * N
+
+
+def algo_ops(M):
+    return 2 * M * N * K
+
+
+class Hip:
+    """The few HIP runtime calls the timing needs (graph capture, events), via ctypes."""
+
+    def __init__(self):
+        self.L = C.CDLL("libamdhip64.so")
+        for n in ("hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
+                  "hipEventCreate", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
+                  "hipDeviceSynchronize", "hipGraphExecDestroy", "hipGraphDestroy", "hipEventDestroy"):
+            getattr(self.L, n).restype = C.c_int
+
+    def ck(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    def event(self):
+        e = C.c_void_p()
+        self.ck(self.L.hipEventCreate(C.byref(e)), "hipEventCreate")
+        return e
+
+    def capture(self, stream, fn):
+        g = C.c_void_p()
+        ex = C.c_void_p()
+        self.ck(self.L.hipStreamBeginCapture(C.c_void_p(stream), 0), "hipStreamBeginCapture")
+        fn()
+        self.ck(self.L.hipStreamEndCapture(C.c_void_p(stream), C.byref(g)), "hipStreamEndCapture")
+        self.ck(self.L.hipGraphInstantiate(C.byref(ex), g, None, None, C.c_size_t(0)), "hipGraphInstantiate")
+        return g, ex
+
+    def time_ms(self, stream, launch):
+        e0, e1 = self.event(), self.event()
+        self.ck(self.L.hipDeviceSynchronize(), "sync")
+        self.ck(self.L.hipEventRecord(e0, C.c_void_p(stream)), "record")
+        launch()
+        self.ck(self.L.hipEventRecord(e1, C.c_void_p(stream)), "record")
+        self.ck(self.L.hipEventSynchronize(e1), "event sync")
+        self.ck(self.L.hipDeviceSynchronize(), "sync")
+        ms = C.c_float()
+        self.ck(self.L.hipEventElapsedTime(C.byref(ms), e0, e1), "elapsed")
+        self.L.hipEventDestroy(e0)
+        self.L.hipEventDestroy(e1)
+        return ms.value
+
+
+def measure(npu, hip, ws, M, dA, dC, steps, warmup):
+    """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % R]."""
+    import ork
+
+    L = ork.lib()
+    stream = L.ork_npu_stream(npu.h)
+
+    def run(i):
+        rc = L.ork_i8_mm_run(npu.h, ws[i % len(ws)], M, dA, dC)
+        if rc:
+            raise RuntimeError(f"ork_i8_mm_run rc={rc}")
+
+    # eager: warmup, then steps individually launched (host launch rate included)
+    for i in range(warmup):
+        run(i)
+    eager = hip.time_ms(stream, lambda: [run(i) for i in range(steps)]) / steps
+    # graph: one graph of exactly `steps` launches; warm it, then time one replay
+    g, ex = hip.capture(stream, lambda: [run(i) for i in range(steps)])
+    hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")
+    graph = hip.time_ms(stream, lambda: hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")) / steps
+    hip.L.hipGraphExecDestroy(ex)
+    hip.L.hipGraphDestroy(g)
+    return graph, eager
+
+
+def cpu_baseline(W_codes, A_row, budget_s):
+    """The reference's own CPU GEMM (orki_cpu_gemm_i32 from oracle/_ref) single-threaded on M=1 calls of
+    the same workload, for ~budget_s seconds. Falls back to the oracle restatement if _ref is absent."""
+    import oracle as O
+
+    kind = "reference" if O.ref_available() else "port"
+    fn = O.ref_gemm_i32 if kind == "reference" else O.gemm_i32
+    fn(A_row, W_codes)
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        fn(A_row, W_codes)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(algo_bytes(1) / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{n} M=1 calls of the K=2048,N=6144 int8 GEMM (orki_cpu_gemm_i32 as built, -O2, 1 thread), "
+                      f"{dt * 1e3:.2f} ms/call"}
+
+
+def traffic_from_profiles(kernel_tag):
+    """HBM bytes per launch from committed rocprofv3 --pmc summaries (profiles/*_pmc.json), or None."""
+    p = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        return json.load(open(p)).get("hbm_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2400)
+    ap.add_argument("--warmup", type=int, default=240)
+    ap.add_argument("--m512-steps", type=int, default=480)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the resident-weight matmul has no collective; "
+              "N-sharding across GPUs is described in DESIGN.md but not run). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import ork
+    import oracle as O
+
+    L = ork.lib()
+    hip = Hip()
+    rng = np.random.default_rng(0x6F726B00 + (1 << 8))
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)   # f32[N][K]
+    A512 = rng.integers(-127, 128, size=(512, K), dtype=np.int8)
+    with ork.Npu() as npu:
+        t0 = time.perf_counter()
+        ws = []
+        for _ in range(R):
+            w, bs = npu.pack_i8_f32(W)
+            if not w:
+                raise RuntimeError("ork_i8_mm_pack_f32 failed")
+            ws.append(w)
+        pack_s = (time.perf_counter() - t0) / R
+        codes, bs_ref = O.pack_i8_f32(W)
+        assert np.array_equal(bs, bs_ref)
+        dA = L.ork_dev_alloc(npu.h, A512.nbytes)
+        dC = L.ork_dev_alloc(npu.h, 512 * N * 4)
+        assert dA and dC
+        assert L.ork_dev_upload(npu.h, dA, ork.ptr(A512), A512.nbytes) == 0
+        L.ork_npu_set_async(npu.h, 1)
+        gemv_plan = npu.plan_name(ws[0], 1)
+        gemm_plan = npu.plan_name(ws[0], 512)
+        print(f"[bench] packed {R} x {K}x{N} int8 weights ({pack_s * 1e3:.1f} ms/pack); plans M=1 {gemv_plan}, "
+              f"M=512 {gemm_plan}", file=sys.stderr, flush=True)
+
+        g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup)
+        print(f"[bench] M=1: graph {g1 * 1e3:.2f} us/step, eager {e1 * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+        g512, e512 = measure(npu, hip, ws, 512, dA, dC, args.m512_steps, max(args.warmup // 8, 8))
+        print(f"[bench] M=512: graph {g512 * 1e3:.2f} us/step, eager {e512 * 1e3:.2f} us/step",
+              file=sys.stderr, flush=True)
+
+        # correctness of what was timed: the last M=512 and an M=1 launch vs the oracle
+        L.ork_npu_set_async(npu.h, 0)
+        C512 = np.empty((512, N), np.int32)
+        assert L.ork_dev_download(npu.h, ork.ptr(C512), dC, C512.nbytes) == 0
+        rows = np.r_[0:4, 508:512]
+        assert np.array_equal(C512[rows], O.gemm_i32(A512[rows], codes)), "M=512 result differs from the oracle"
+        assert L.ork_i8_mm_run(npu.h, ws[1], 1, dA, dC) == 0
+        C1 = np.empty((1, N), np.int32)
+        assert L.ork_dev_download(npu.h, ork.ptr(C1), dC, C1.nbytes) == 0
+        assert np.array_equal(C1, O.gemm_i32(A512[:1], codes)), "M=1 result differs from the oracle"
+
+        for w in ws:
+            ork.lib().ork_mm_free(npu.h, w)
+        L.ork_dev_free(npu.h, dA)
+        L.ork_dev_free(npu.h, dC)
+
+    gbs = algo_bytes(1) / (g1 * 1e-3) / 1e9
+    tops = algo_ops(512) / (g512 * 1e-3) / 1e12
+    out = {
+        "metric": "w8a8 M=1 GEMV HBM GB/s (% peak); M=512 int8 GEMM TOPS (% MFMA peak)",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g1, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,0.02) weights, U[-127,127] activations); 48 rotated resident weight copies",
+        "config": {"workload": "w8a8 GEMV ork_i8_mm_run M=1 K=2048 N=6144 (BASELINE config 1)",
+                   "kernel": gemv_plan, "timing": "HIP graph of `steps` launches, HIP events"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_i8_m1")},
+        "eager_value": round(algo_bytes(1) / (e1 * 1e-3) / 1e9, 1),
+        "m512": {"workload": "int8 GEMM ork_i8_mm_run M=512 K=2048 N=6144", "kernel": gemm_plan,
+                 "value": round(tops, 1), "unit": "TOP/s", "ms_per_step": round(g512, 6), "steps": args.m512_steps,
+                 "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                              "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": traffic_from_profiles("gemm_i8_m512")},
+                 "hbm_gbs": round(algo_bytes(512) / (g512 * 1e-3) / 1e9, 1),
+                 "eager_value": round(algo_ops(512) / (e512 * 1e-3) / 1e12, 1)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(codes, A512[:1], args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

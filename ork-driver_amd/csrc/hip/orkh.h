@@ -69,7 +69,9 @@ enum { ORKH_ALGO_STREAM = 0, ORKH_ALGO_TILED = 1 };
 /* One C[M][N] = A[M][K] x B[K][N] launch on resident panels. A is row-major with row stride lda
  * elements (int8 for the integer kinds, fp16 for ORKH_F16); C is row-major int32 (integer kinds) or
  * fp32 (ORKH_F16) with row stride ldc elements. All pointers are device pointers; A and B must be
- * 16-byte aligned and lda*elem a multiple of 16 bytes. */
+ * 16-byte aligned and lda*elem a multiple of 16 bytes. A (M*lda*elem bytes) and the panels are read
+ * through 32-bit buffer offsets, so each must stay below ORKH_MAX_OPERAND_BYTES. */
+#define ORKH_MAX_OPERAND_BYTES 0x80000000u
 typedef struct orkh_mm {
     int kind;
     int M, K, N;

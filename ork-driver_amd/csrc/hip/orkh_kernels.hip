@@ -20,6 +20,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "orkh.h"
 
 namespace {
@@ -100,12 +102,16 @@ template <int KIND> __device__ __forceinline__ typename KT<KIND>::c_t finish(typ
     else return v;
 }
 
-// A chunk load: 16 bytes of row `row` starting at element k, or zero outside [0,M) x [0,K).
-template <int KIND>
-__device__ __forceinline__ v4i load_a(const char *A, int lda_bytes, int row, int k, int M, int K) {
-    v4i a = {0, 0, 0, 0};
-    if (row < M && k < K) a = *(const v4i *)(A + (size_t)row * lda_bytes + (size_t)k * KT<KIND>::ESZ);
-    return a;
+// ------------------------------------------------------------------------------------------------
+// Raw buffer loads: the hardware returns 0 for any byte offset >= num_records, so out-of-range rows,
+// K tails and stages past the end cost no clamping or select instructions, and can never fault.
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+constexpr uint32_t OOB = 0x80000000u;  // an offset past every buffer this path addresses (< 2 GiB)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (v4i)__builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -133,27 +139,45 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) acc[mt] = acc_t{0, 0, 0, 0};
 
-    auto consume = [&](v4i raw, int kb) {
-        v4i op[T::STEPS];
-        decode<KIND>(raw, op, L);
+    // One batch of U blocks: every A chunk (L2-resident, short latency) is requested first, then every
+    // B block (HBM), and only then is anything consumed, so the wave has all its loads in flight at once.
+    // A loads are unconditional from a clamped, always-valid address (row 0, k 0) and the chunks outside
+    // [0,M) x [0,K) are zeroed where they are consumed: a select right after the load would make the
+    // wave wait for it, and buffer loads measured slower on this path.
+    auto batch = [&](int kb, auto U_) {
+        constexpr int U = decltype(U_)::value;
+        v4i av[U][T::STEPS][MT];
 #pragma unroll
-        for (int s = 0; s < T::STEPS; s++) {
-            const int k = kb * T::KPB + a_koff<KIND>(s, g);
+        for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                acc[mt] = mma(load_a<KIND>(A, lda_b, mt * 16 + r16, k, p.M, p.K), op[s], acc[mt]);
+            for (int s = 0; s < T::STEPS; s++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const int row = mt * 16 + r16, k = (kb + u) * T::KPB + a_koff<KIND>(s, g);
+                    const bool ok = row < p.M && k < p.K;
+                    av[u][s][mt] = *(const v4i *)(A + (size_t)(ok ? row : 0) * lda_b + (size_t)(ok ? k : 0) * T::ESZ);
+                }
+        v4i raw[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) raw[u] = __builtin_nontemporal_load(bp + (size_t)(kb + u) * 64);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            v4i op[T::STEPS];
+            decode<KIND>(raw[u], op, L);
+#pragma unroll
+            for (int s = 0; s < T::STEPS; s++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const int row = mt * 16 + r16, k = (kb + u) * T::KPB + a_koff<KIND>(s, g);
+                    const v4i a = (row < p.M && k < p.K) ? av[u][s][mt] : v4i{0, 0, 0, 0};
+                    acc[mt] = mma(a, op[s], acc[mt]);
+                }
         }
     };
 
     int kb = kb0;
-    for (; kb + KU <= kb1; kb += KU) {
-        v4i raw[KU];
-#pragma unroll
-        for (int u = 0; u < KU; u++) raw[u] = __builtin_nontemporal_load(bp + (size_t)(kb + u) * 64);
-#pragma unroll
-        for (int u = 0; u < KU; u++) consume(raw[u], kb + u);
-    }
-    for (; kb < kb1; kb++) consume(__builtin_nontemporal_load(bp + (size_t)kb * 64), kb);
+    for (; kb + KU <= kb1; kb += KU) batch(kb, std::integral_constant<int, KU>{});
+    for (; kb < kb1; kb++) batch(kb, std::integral_constant<int, 1>{});
 
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
@@ -188,23 +212,44 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const c_t *ws, c_t *C, in
     C[(i / N) * ldc + (i % N)] = s;
 }
 
-// ------------------------------------------------------------------------------------------------
-// k_tiled: one 256-thread workgroup (2 x 2 waves) per BM x BN tile, KS panel K-blocks per LDS stage.
-template <int KIND, int BM, int BN, int KS>
-__global__ __launch_bounds__(256) void k_tiled(orkh_mm p, int mtiles) {
+// Dynamic LDS of k_tiled: KG groups x 2 stage buffers of A fragments, or (KG > 1) the 4-wave partial
+// tile parked for the final cross-group sum, whichever is larger.
+template <int KIND, int BM, int BN, int KS, int KG>
+constexpr size_t tiled_lds_bytes() {
+    const size_t stages = (size_t)KG * 2 * (BM / 16) * KS * KT<KIND>::STEPS * 1024;
+    const size_t red = KG > 1 ? (size_t)4 * (BM / 32) * (BN / 32) * 64 * 16 : 0;
+    return stages > red ? stages : red;
+}
+
+// k_tiled: one workgroup per BM x BN output tile, KG groups of 4 waves (2 x 2 over the tile). The
+// groups split K stage by stage (group g takes stages g, g+KG, ...) and sum their partial tiles through
+// LDS at the end; with KG = 2 each SIMD runs two waves, which the MFMA pipe needs to issue near peak.
+// Per stage (KS panel K-blocks) and group:
+//   A fragments (BM rows) are loaded cooperatively and staged through a double-buffered LDS region,
+//   since all four waves read them;
+//   B blocks go straight from HBM/L2 into the registers of the waves that use them (they are already
+//   MFMA fragments in the panel layout), so weights never touch LDS.
+// Both operands run D stages ahead through a ring of register slots (stage t in slot t % D); one
+// barrier per stage. Loads are raw buffer loads: rows >= M, k >= K and stages past the end read 0
+// through the hardware range check (no clamps, no selects, no faults).
+template <int KIND, int BM, int BN, int KS, int D, int KG>
+__global__ __launch_bounds__(256 * KG) void k_tiled(orkh_mm p, int mtiles) {
     using T = KT<KIND>;
     typedef typename T::acc_t acc_t;
     constexpr int MB = BM / 16, NBK = BN / 16;
     constexpr int MTW = MB / 2, NTW = NBK / 2;
     constexpr int AF = MB * KS * T::STEPS;  // A fragments (1 KiB) per stage
-    constexpr int BF = NBK * KS;            // B blocks (1 KiB) per stage
-    constexpr int AV = (AF * 64 + 255) / 256, BV = (BF * 64 + 255) / 256;
-    static_assert(MB % 2 == 0 && NBK % 2 == 0, "tile must split over 2x2 waves");
-    __shared__ v4i lds[2][(AF + BF) * 64];
+    constexpr int AV = AF * 64 / 256;       // A fragment entries per thread per stage
+    constexpr int STG = AF * 64;            // v4i per LDS stage buffer
+    constexpr int KSPAN = KS * T::KPB;      // k per stage
+    static_assert(MB % 2 == 0 && NBK % 2 == 0 && (AF * 64) % 256 == 0, "tile must split over 2x2 waves");
+    extern __shared__ v4i lds_dyn[];  // tiled_lds_bytes<...>(): the stage buffers, or the reduction tile
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int grp = threadIdx.x >> 8;
+    const int tid = threadIdx.x & 255, lane = tid & 63, wv = tid >> 6;
     const int wm = wv & 1, wn = wv >> 1;
-    // XCD-aware order: WG b runs on XCD b%8; give each XCD a contiguous run of tiles, M fastest, so
+    v4i *lds = lds_dyn + grp * 2 * STG;
+    // XCD-aware order: WG b runs on XCD b%8; each XCD gets a contiguous run of tiles, M fastest, so
     // every M-tile that reads a given B column panel shares one L2.
     const int nT = gridDim.x, bid = blockIdx.x;
     const int per = nT / 8, rem = nT % 8, x = bid % 8, j = bid / 8;
@@ -212,49 +257,49 @@ __global__ __launch_bounds__(256) void k_tiled(orkh_mm p, int mtiles) {
     const int m0 = (tile % mtiles) * BM;
     const int nb0 = (tile / mtiles) * NBK;
     const int NBtot = p.N / 16;
-
-    const char *A = (const char *)p.A;
-    const int lda_b = p.lda * T::ESZ;
-    const v4i *Bp = (const v4i *)p.B;
     const Lut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
 
-    v4i ra[AV], rb[BV];
-    auto gload = [&](int st) {
+    const uint32_t lda_b = (uint32_t)p.lda * T::ESZ;
+    const __amdgpu_buffer_rsrc_t Ar = make_rsrc(p.A, (uint32_t)p.M * lda_b);
+    const __amdgpu_buffer_rsrc_t Br = make_rsrc(p.B, (uint32_t)NBtot * p.KB * 1024u);
+
+    // Per-thread constant parts of every load: A entry i -> byte offset at stage 0 and its k within the
+    // stage; B block jn of this wave -> byte offset at stage 0.
+    uint32_t a_off[AV];
+    int a_k[AV];
 #pragma unroll
-        for (int i = 0; i < AV; i++) {
-            const int idx = i * 256 + tid;
-            ra[i] = v4i{0, 0, 0, 0};
-            if (idx < AF * 64) {
-                const int f = idx >> 6, ln = idx & 63;
-                const int mb = f / (KS * T::STEPS), ksub = f % (KS * T::STEPS);
-                const int kbl = ksub / T::STEPS, s = ksub % T::STEPS;
-                const int row = m0 + mb * 16 + (ln & 15);
-                const int k = (st * KS + kbl) * T::KPB + a_koff<KIND>(s, ln >> 4);
-                ra[i] = load_a<KIND>(A, lda_b, row, k, p.M, p.K);
-            }
-        }
+    for (int i = 0; i < AV; i++) {
+        const int idx = i * 256 + tid, f = idx >> 6, ln = idx & 63;
+        const int mb = f / (KS * T::STEPS), ksub = f % (KS * T::STEPS);
+        const int kbl = ksub / T::STEPS, s = ksub % T::STEPS;
+        const int row = m0 + mb * 16 + (ln & 15);
+        a_k[i] = kbl * T::KPB + a_koff<KIND>(s, ln >> 4);
+        a_off[i] = row < p.M ? (uint32_t)row * lda_b + (uint32_t)a_k[i] * T::ESZ : OOB;
+    }
+    uint32_t b_off[NTW];
 #pragma unroll
-        for (int i = 0; i < BV; i++) {
-            const int idx = i * 256 + tid;
-            rb[i] = v4i{0, 0, 0, 0};
-            if (idx < BF * 64) {
-                const int b = idx >> 6, ln = idx & 63;
-                const int nb = nb0 + b / KS, kb = st * KS + b % KS;
-                if (nb < NBtot && kb < p.KB) rb[i] = Bp[((size_t)nb * p.KB + kb) * 64 + ln];
-            }
+    for (int jn = 0; jn < NTW; jn++) {
+        const int nb = nb0 + wn * NTW + jn;
+        b_off[jn] = nb < NBtot ? ((uint32_t)nb * p.KB * 64 + lane) * 16 : OOB;
+    }
+
+    v4i ra[D][AV], rb[D][NTW][KS];
+    // ls = this group's local stage; its global stage is ls * KG + grp.
+    auto gload = [&](int ls, v4i (&xa)[AV], v4i (&xb)[NTW][KS]) {
+        const int st = ls * KG + grp, k0 = st * KSPAN;
+#pragma unroll
+        for (int i = 0; i < AV; i++)
+            xa[i] = bload(Ar, k0 + a_k[i] < p.K ? a_off[i] + (uint32_t)k0 * T::ESZ : OOB);
+#pragma unroll
+        for (int kbl = 0; kbl < KS; kbl++) {
+            const int kb = st * KS + kbl;
+#pragma unroll
+            for (int jn = 0; jn < NTW; jn++) xb[jn][kbl] = bload(Br, kb < p.KB ? b_off[jn] + (uint32_t)kb * 1024u : OOB);
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int buf, const v4i (&xa)[AV]) {
 #pragma unroll
-        for (int i = 0; i < AV; i++) {
-            const int idx = i * 256 + tid;
-            if (idx < AF * 64) lds[buf][idx] = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < BV; i++) {
-            const int idx = i * 256 + tid;
-            if (idx < BF * 64) lds[buf][AF * 64 + idx] = rb[i];
-        }
+        for (int i = 0; i < AV; i++) lds[buf * STG + i * 256 + tid] = xa[i];
     };
 
     acc_t acc[MTW][NTW];
@@ -263,31 +308,59 @@ __global__ __launch_bounds__(256) void k_tiled(orkh_mm p, int mtiles) {
 #pragma unroll
         for (int jn = 0; jn < NTW; jn++) acc[i][jn] = acc_t{0, 0, 0, 0};
 
-    const int nst = (p.KB + KS - 1) / KS;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int st = 0; st < nst; st++) {
-        const int cur = st & 1;
-        if (st + 1 < nst) gload(st + 1);
+    auto compute = [&](int cur, const v4i (&xb)[NTW][KS]) {
+        const v4i *sb = lds + cur * STG;
 #pragma unroll
         for (int kbl = 0; kbl < KS; kbl++) {
             v4i op[NTW][T::STEPS];
 #pragma unroll
-            for (int jn = 0; jn < NTW; jn++)
-                decode<KIND>(lds[cur][AF * 64 + ((wn * NTW + jn) * KS + kbl) * 64 + lane], op[jn], L);
+            for (int jn = 0; jn < NTW; jn++) decode<KIND>(xb[jn][kbl], op[jn], L);
 #pragma unroll
             for (int s = 0; s < T::STEPS; s++) {
 #pragma unroll
                 for (int i = 0; i < MTW; i++) {
-                    const v4i a = lds[cur][(((wm * MTW + i) * KS + kbl) * T::STEPS + s) * 64 + lane];
+                    const v4i a = sb[(((wm * MTW + i) * KS + kbl) * T::STEPS + s) * 64 + lane];
 #pragma unroll
                     for (int jn = 0; jn < NTW; jn++) acc[i][jn] = mma(a, op[jn][s], acc[i][jn]);
                 }
             }
         }
-        if (st + 1 < nst) lstore(cur ^ 1);
+    };
+
+    // Each group's stage count is rounded up to a multiple of D (the extra stages read zeros and add
+    // nothing), so the ring has no branches and every wait is a partial vmcnt.
+    const int nst = (p.KB + KS - 1) / KS;
+    const int nls = ((nst + KG - 1) / KG + D - 1) / D * D;
+#pragma unroll
+    for (int jd = 0; jd < D; jd++) gload(jd, ra[jd], rb[jd]);
+    lstore(0, ra[0]);
+    __syncthreads();
+    for (int s0 = 0; s0 < nls; s0 += D) {
+#pragma unroll
+        for (int jd = 0; jd < D; jd++) {
+            const int ls = s0 + jd;
+            compute(ls & 1, rb[jd]);          // A of stage ls from LDS, B of stage ls from slot jd
+            gload(ls + D, ra[jd], rb[jd]);    // slot jd is free again: refill it D stages ahead
+            lstore((ls + 1) & 1, ra[(jd + 1) % D]);
+            __syncthreads();
+        }
+    }
+
+    if constexpr (KG == 2) {
+        // Every stage buffer is idle after the loop's last barrier: group 1 parks its partial tile in
+        // the LDS, group 0 adds it in.
+        acc_t *red = (acc_t *)lds_dyn;
+        if (grp == 1)
+#pragma unroll
+            for (int i = 0; i < MTW; i++)
+#pragma unroll
+                for (int jn = 0; jn < NTW; jn++) red[((wv * MTW + i) * NTW + jn) * 64 + lane] = acc[i][jn];
         __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int i = 0; i < MTW; i++)
+#pragma unroll
+            for (int jn = 0; jn < NTW; jn++) acc[i][jn] += red[((wv * MTW + i) * NTW + jn) * 64 + lane];
     }
 
     typedef typename T::c_t c_t;
@@ -338,10 +411,20 @@ int launch_stream(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
 
 template <int KIND, int BM, int BN>
 int launch_tiled_v(const orkh_mm *p, hipStream_t s) {
-    constexpr int KS = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 1 : 2;
+    constexpr int KS = 1;
+    constexpr int D = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 3 : 4;
+    constexpr int KG = 2;
+    constexpr size_t lds = tiled_lds_bytes<KIND, BM, BN, KS, KG>();
+    auto kern = k_tiled<KIND, BM, BN, KS, D, KG>;
+    static bool attr = false;  // per instantiation: allow more than the default 64 KiB of dynamic LDS
+    if (!attr) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return -1;
+        attr = true;
+    }
     const int mtiles = (p->M + BM - 1) / BM;
     const int ntiles = (p->N / 16 + BN / 16 - 1) / (BN / 16);
-    hipLaunchKernelGGL((k_tiled<KIND, BM, BN, KS>), dim3(mtiles * ntiles), dim3(256), 0, s, *p, mtiles);
+    hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(256 * KG), lds, s, *p, mtiles);
     return 0;
 }
 

@@ -39,6 +39,10 @@ static int run_common(const char *who, ork_npu *c, ork_w *w, int want_dt, int M,
         return -1;
     }
     const size_t abytes = (size_t)M * K * esz_a, cbytes = (size_t)M * N * 4;
+    if (abytes >= ORKH_MAX_OPERAND_BYTES || w->dbytes >= ORKH_MAX_OPERAND_BYTES) {
+        orki_err("%s: operand too large for 32-bit buffer offsets (A %zu B, weight %zu B)", who, abytes, w->dbytes);
+        return -1;
+    }
     if (orki_check_overlap(who, (uintptr_t)A, (uintptr_t)A + abytes, (uintptr_t)C, (uintptr_t)C + cbytes)) return -1;
 
     const int a_dev = orki_dev_find(c, A, abytes) && ((uintptr_t)A % 16 == 0);
