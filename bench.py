@@ -109,6 +109,24 @@ def measure(npu, hip, ws, M, dA, dC, steps, warmup):
     return graph, eager
 
 
+def copy_calibration(hip, L, reps=96):
+    """Device-to-device copies of K*N bytes (hipMemcpyAsync D2D: the runtime's copy kernel) between
+    rotated buffers, so rocprofv3's FETCH_SIZE / WRITE_SIZE for a kernel of known traffic can be read."""
+    import ork
+
+    nbytes = K * N
+    with ork.Npu() as npu:
+        bufs = [L.ork_dev_alloc(npu.h, nbytes) for _ in range(R)]
+        dst = L.ork_dev_alloc(npu.h, nbytes)
+        stream = L.ork_npu_stream(npu.h)
+        hip.L.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        for i in range(reps):
+            hip.ck(hip.L.hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(bufs[i % R]), nbytes, 3, C.c_void_p(stream)),
+                   "hipMemcpyAsync")
+        hip.ck(hip.L.hipDeviceSynchronize(), "sync")
+        print(f"[bench] copy calibration: {reps} device copies of {nbytes} bytes", file=sys.stderr, flush=True)
+
+
 def cpu_baseline(W_codes, A_row, budget_s):
     """The reference's own CPU GEMM (orki_cpu_gemm_i32 from oracle/_ref) single-threaded on M=1 calls of
     the same workload, for ~budget_s seconds. Falls back to the oracle restatement if _ref is absent."""
@@ -147,6 +165,10 @@ def main():
     ap.add_argument("--m512-steps", type=int, default=480)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["gemv", "m512"], help="profiling: time only one of the two kernels")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="profiling: run device-to-device copies of one weight's bytes (a plain copy kernel of "
+                         "known size) instead of the bench, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the resident-weight matmul has no collective; "
@@ -158,6 +180,9 @@ def main():
 
     L = ork.lib()
     hip = Hip()
+    if args.copy_calibration:
+        copy_calibration(hip, L)
+        return
     rng = np.random.default_rng(0x6F726B00 + (1 << 8))
     W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)   # f32[N][K]
     A512 = rng.integers(-127, 128, size=(512, K), dtype=np.int8)
@@ -182,11 +207,18 @@ def main():
         print(f"[bench] packed {R} x {K}x{N} int8 weights ({pack_s * 1e3:.1f} ms/pack); plans M=1 {gemv_plan}, "
               f"M=512 {gemm_plan}", file=sys.stderr, flush=True)
 
-        g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup)
-        print(f"[bench] M=1: graph {g1 * 1e3:.2f} us/step, eager {e1 * 1e3:.2f} us/step", file=sys.stderr, flush=True)
-        g512, e512 = measure(npu, hip, ws, 512, dA, dC, args.m512_steps, max(args.warmup // 8, 8))
-        print(f"[bench] M=512: graph {g512 * 1e3:.2f} us/step, eager {e512 * 1e3:.2f} us/step",
-              file=sys.stderr, flush=True)
+        g1 = e1 = g512 = e512 = float("nan")
+        if args.only != "m512":
+            g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup)
+            print(f"[bench] M=1: graph {g1 * 1e3:.2f} us/step, eager {e1 * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+        if args.only != "gemv":
+            g512, e512 = measure(npu, hip, ws, 512, dA, dC, args.m512_steps, max(args.warmup // 8, 8))
+            print(f"[bench] M=512: graph {g512 * 1e3:.2f} us/step, eager {e512 * 1e3:.2f} us/step",
+                  file=sys.stderr, flush=True)
+        if args.only:
+            for w in ws:
+                ork.lib().ork_mm_free(npu.h, w)
+            return
 
         # correctness of what was timed: the last M=512 and an M=1 launch vs the oracle
         L.ork_npu_set_async(npu.h, 0)

@@ -28,3 +28,15 @@ $(OUT)/quant.o: $(REF)/src/npu/i4/quant.c
 $(OUT)/ref_driver.o: $(HERE)ref_driver.c
 	mkdir -p $(OUT)
 	$(CLANG) $(CFLAGS) -c $< -o $@
+
+# The reference's own example/test program examples/quant.c, compiled UNMODIFIED from the reference tree
+# against this repository's drop-in header (include/ork_npu.h) and linked to libork_npu.so: a C consumer
+# of the reference API running on the MI355X engine, checked by its own embedded FNV-64 goldens.
+ROOT    := $(abspath $(HERE)..)
+$(OUT)/quant_on_mi355x: $(REF)/examples/quant.c $(ROOT)/ork-driver_amd/libork_npu.so $(wildcard $(ROOT)/include/*.h $(ROOT)/include/ork/*.h)
+	mkdir -p $(OUT)
+	$(CLANG) -O2 -std=gnu11 -w -I$(ROOT)/include $< -o $@ -L$(ROOT)/ork-driver_amd -lork_npu \
+	    -Wl,-rpath,'$$ORIGIN/../../ork-driver_amd' -lm
+
+dropin: $(OUT)/quant_on_mi355x
+.PHONY: dropin
