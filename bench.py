@@ -10,7 +10,8 @@ weight from HBM. A and C live in HBM (ork_dev_alloc); the steps are captured int
 timed with HIP events on the library's stream, bracketed by device synchronisation.
 
 Also reported on the same line: the M=512 int8 GEMM (TOPS, % of dense int8 MFMA peak) as "m512",
-the eager (non-graph) launch rate, and the CPU baseline: the reference's own CPU GEMM
+the eager (non-graph) launch rate, the reference's own calling convention (host A and C, one
+synchronous call per step, PCIe and sync included) as "host_api", and the CPU baseline: the reference's own CPU GEMM
 (orki_cpu_gemm_i32, compiled from its sources into oracle/_ref) timed on the host, single-threaded
 as the reference builds it, on a bounded sample of the same workload.
 """
@@ -231,6 +232,19 @@ def main():
         assert L.ork_dev_download(npu.h, ork.ptr(C1), dC, C1.nbytes) == 0
         assert np.array_equal(C1, O.gemm_i32(A512[:1], codes)), "M=1 result differs from the oracle"
 
+        # the reference's calling convention: host A and C, synchronous (PCIe-inclusive; not `value`)
+        Ah = np.ascontiguousarray(A512[:1])
+        Ch = np.empty((1, N), np.int32)
+        for i in range(20):
+            assert L.ork_i8_mm_run(npu.h, ws[i % R], 1, ork.ptr(Ah), ork.ptr(Ch)) == 0
+        nh = 2000
+        t0 = time.perf_counter()
+        for i in range(nh):
+            L.ork_i8_mm_run(npu.h, ws[i % R], 1, ork.ptr(Ah), ork.ptr(Ch))
+        host_us = (time.perf_counter() - t0) / nh * 1e6
+        assert np.array_equal(Ch, O.gemm_i32(Ah, codes)), "host-pointer M=1 result differs from the oracle"
+        print(f"[bench] M=1 host pointers, synchronous: {host_us:.2f} us/call", file=sys.stderr, flush=True)
+
         for w in ws:
             ork.lib().ork_mm_free(npu.h, w)
         L.ork_dev_free(npu.h, dA)
@@ -256,6 +270,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_i8_m1")},
         "eager_value": round(algo_bytes(1) / (e1 * 1e-3) / 1e9, 1),
+        "host_api": {"value": round(algo_bytes(1) / (host_us * 1e-6) / 1e9, 1), "unit": "GB/s",
+                     "us_per_call": round(host_us, 2),
+                     "note": "ork_i8_mm_run(M=1) with host A and C: H2D of A, launch, D2H of C, stream sync"},
         "m512": {"workload": "int8 GEMM ork_i8_mm_run M=512 K=2048 N=6144", "kernel": gemm_plan,
                  "value": round(tops, 1), "unit": "TOP/s", "ms_per_step": round(g512, 6), "steps": args.m512_steps,
                  "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",

@@ -177,6 +177,8 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
 
     int kb = kb0;
     for (; kb + KU <= kb1; kb += KU) batch(kb, std::integral_constant<int, KU>{});
+    if constexpr (KU > 4)
+        if (kb + 4 <= kb1) { batch(kb, std::integral_constant<int, 4>{}); kb += 4; }
     for (; kb < kb1; kb++) batch(kb, std::integral_constant<int, 1>{});
 
 #pragma unroll
@@ -201,7 +203,11 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
     }
 }
 
-// Fixed-order sum of split-K partials (deterministic for fp32 as well as exact for int32).
+// Fixed-order sum of split-K partials (deterministic for fp32 as well as exact for int32). A separate
+// launch on purpose: combining the partials inside k_stream (last-arriving workgroup reduces) needs a
+// device-scope release/acquire per workgroup, which on gfx950 is an L2 write-back + invalidate
+// (buffer_wbl2 sc1 / buffer_inv sc1) and measured 34-120 us per launch for a 4 us GEMV; a second
+// launch costs ~2 us.
 template <typename c_t>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const c_t *ws, c_t *C, int M, int N, int ldc, int ksplit) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -6,9 +6,9 @@
  * 8192-wide outputs and M into CBUF-sized row groups, each a separate submit with a host int32
  * accumulate. On MI355X every shape is one launch (plus a reduce pass when K is split across
  * workgroups); the planner only decides how to fill 256 CUs:
- *   M <= 64  stream: one 16-column panel per workgroup, waves split K, runs of 8 (4 for int4) 1 KiB
- *            blocks per wave so ~8 KiB per wave is in flight; K is split across workgroups only when
- *            the panels alone give fewer than ~4 waves per CU.
+ *   M <= 64  stream: one 16-column panel per workgroup, waves split K in runs of 1 KiB blocks (8 per
+ *            run for the int8/fp16 GEMV); K is split across workgroups only for long-K, few-panel
+ *            shapes that leave the machine underfilled. ORK_KSPLIT=n forces a split (tests).
  *   M >  64  tiled: the BM x BN tile (128x96, 128x128 or 64x64) with the fewest tile-rounds of work
  *            per CU, larger tile on ties. */
 #include <stdlib.h>
@@ -32,14 +32,24 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
     if (stream) {
         q->algo = ORKH_ALGO_STREAM;
         q->mt = cdiv(M, 16);
-        const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 4 : 8;
+        /* Run length per wave: 8 KiB in flight per wave for the int8/fp16 GEMV (M = 1); more waves with
+         * shorter runs where each block costs more issue (more rows, int4 decode). Measured on the
+         * K=2048, N=6144 panels; the run lengths on either side were within 2-4%. */
+        const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
         const int need = cdiv(KB, kbw_target); /* waves per panel at the target run length */
         const int wpg = need <= 4 ? 4 : 8;
-        int ksplit = cdiv(need, wpg);
-        const int ks_fill = cdiv(4 * cu, NB * wpg); /* enough workgroups to give ~4 waves per CU */
-        if (ks_fill > ksplit) ksplit = ks_fill;
-        const int ks_max = cdiv(KB, wpg) > 0 ? cdiv(KB, wpg) : 1; /* every wave keeps >= 1 block */
-        if (ksplit > ks_max) ksplit = ks_max;
+        /* K is split across workgroups only when the panels leave the machine underfilled (< 4 waves
+         * per CU) AND each wave would otherwise stream more than two runs back to back: the split
+         * costs a second launch (the fixed-order reduce, ~2 us), which a one-run wave never repays. */
+        int ksplit = 1;
+        const int runs = cdiv(cdiv(KB, wpg), kbw_target);
+        if ((long)NB * wpg < 4L * cu && runs > 2) {
+            ksplit = cdiv(4 * cu, NB * wpg);
+            if (ksplit > runs) ksplit = runs; /* every wave keeps a full run */
+        }
+        const char *fks = getenv("ORK_KSPLIT");
+        if (fks && atoi(fks) > 0) ksplit = atoi(fks);
+        if (ksplit > KB) ksplit = KB;
         if (ksplit < 1) ksplit = 1;
         const int kbs = cdiv(KB, ksplit);
         ksplit = cdiv(KB, kbs);

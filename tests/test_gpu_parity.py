@@ -67,6 +67,60 @@ def test_i8_forced_algorithms_agree(npu, M):
     ork.free(w)
 
 
+class _env:
+    """Sets environment variables for the duration of a with-block (the planner reads them per call)."""
+
+    def __init__(self, **kv):
+        self.kv = kv
+
+    def __enter__(self):
+        for k, v in self.kv.items():
+            os.environ[k] = str(v)
+
+    def __exit__(self, *a):
+        for k in self.kv:
+            os.environ.pop(k, None)
+
+
+@pytest.mark.parametrize("ks", [2, 3, 7, 64])
+def test_forced_split_k_all_kinds(npu, ks):
+    """K split across workgroups + the fixed-order reduce: exact for int8 / int4 (uniform and W4A4),
+    within tolerance and run-to-run bit-identical for fp16. ks=64 exceeds the K-blocks of the int4
+    shape and is clamped to one block per workgroup."""
+    _say("split-k", ks)
+    rng = _rng(ks)
+    K, N = 2080, 128  # K % 64 == 32: a K tail in every kind; N % 64 == 0 for the W4A4 pack gate
+    for M in (1, 13, 40):
+        A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+        B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+        w = npu.pack_i8(B)
+        with _env(ORK_PLAN="stream", ORK_KSPLIT=ks):
+            rc, C = npu.run_i8(w, A)
+            KB = -(-K // 64)
+            kbs = -(-KB // min(ks, KB))
+            assert npu.plan_name(w, M).endswith(f"_ks{-(-KB // kbs)}"), npu.plan_name(w, M)
+        assert rc == 0 and np.array_equal(C, O.gemm_i32(A, B)), ("i8", M, npu.plan_name(w, M))
+        ork.free(w)
+
+        A4, B4 = O.gen_i4_test(M, K, N)
+        w = npu.pack_i4(B4)
+        assert w
+        with _env(ORK_PLAN="stream", ORK_KSPLIT=ks):
+            rc, C = npu.run_i4(w, A4)
+        assert rc == 0 and np.array_equal(C, O.gemm_i32(A4, B4)), ("w4a4", M)
+        ork.free(w)
+
+        Ah = rng.standard_normal((M, K)).astype(np.float16)
+        Bh = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+        w = npu.pack_f16(Bh)
+        with _env(ORK_PLAN="stream", ORK_KSPLIT=ks):
+            rc, C1 = npu.run_f16(w, Ah)
+            rc2, C2 = npu.run_f16(w, Ah)
+        assert rc == 0 and rc2 == 0 and np.array_equal(C1, C2), ("f16 determinism", M)
+        assert O.fp16_err(C1, O.gemm_f16_f64acc(Ah, Bh)) <= FP16_TOL, ("f16", M)
+        ork.free(w)
+
+
 @pytest.mark.parametrize("idx", range(7))
 def test_quant_c_goldens_on_gpu(npu, idx):
     """examples/quant.c end to end: ork_i8_mm_pack + ork_i8_mm_run, FNV-64 of C == the reference golden."""

@@ -1,0 +1,229 @@
+"""Pins the oracle's quantisers and codec where no golden vector of the reference covers them (CPU only).
+
+Each check is something the mathematics or the reference's own tests fix independently of the
+oracle's code, chosen so that a plausible slip fails it:
+- int8 per-channel quant (src/npu.c:854-865, src/npu/i8/pack.c:442-453): exact round-half-even ties,
+  the dequantisation error bound, the 1e-9 floor, max|q| = 127, and the reference's own RMS gate
+  (examples/test_matmul.c:280-306)
+- NF4 (src/npu/i4/quant.c:70-90, src/npu/i4/pack.c:57): the int8 codebook, nearest-level by brute
+  force (ties to the upper level), the reference's accuracy gate (examples/test_matmul.c:402-427), and
+  for stochastic rounding the bracket and the hit frequency P(hi) = t
+- imatrix clip search (src/npu/i4/quant.c:26, :130-161): the chosen scale is on the clip grid and is
+  the grid's minimum of the weighted error (brute force in float64, up to float32 near-ties), the
+  NULL path is absmax/7 exactly (examples/test_matmul.c:467-471), and the reference's importance gate
+  (examples/test_matmul.c:430-500)
+- O4N1 (src/npu/i4/pack.c:91-103, :115-122; src/npu/internal.h:584, :597): header bytes, section
+  offsets, the C3 size the reference's test expects (examples/test_matmul.c:528), decode round trip,
+  and qerr = sqrt(sum imp (w - q)^2 / sum imp w^2) recomputed from the decoded blob
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+# int8 codebook of the NF4 levels, rint(level * 127) (src/npu.c:888-892 with src/npu/i4/pack.c:57)
+NF4_LUT = [-127, -88, -67, -50, -36, -23, -12, 0, 10, 20, 31, 43, 56, 71, 92, 127]
+# the 16 normalised NF4 levels, transcribed from src/npu.c:888-892 (checked against the codebook below)
+NF4_LEVELS = np.array([-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+                       -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+                       0.07958029955625534, 0.16093020141124725, 0.24611230194568634, 0.33791524171829224,
+                       0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0])
+CLIP_GRID = [1.0, 0.92, 0.85, 0.78, 0.70, 0.62, 0.55]  # src/npu/i4/quant.c:26
+
+
+# ------------------------------------------------------------------------------------------- int8
+def test_i8_quant_exact_ties_and_floor():
+    K, N = 64, 32
+    W = np.zeros((N, K), np.float32)
+    # channel 1: absmax 127 -> inv = 1.0 exactly, so w itself is rounded: half-even at every tie
+    W[1, :8] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5]
+    # channel 2: absmax 254 -> inv = 0.5 exactly
+    W[2, :3] = [254.0, 5.0, 7.0]
+    # channel 3: a value that rounds past 127 cannot occur; the clamp still bounds -127
+    W[3, :2] = [-127.0, 126.5]
+    codes, bs = O.pack_i8_f32(W)
+    assert list(codes[:8, 1]) == [127, 2, 4, -2, -4, 0, 0, 2]
+    assert list(codes[:3, 2]) == [127, 2, 4]
+    assert list(codes[:2, 3]) == [-127, 126]
+    # the all-zero channel: absmax floored at 1e-9, codes 0, bscale = 1e-9/127 in float32
+    assert np.all(codes[:, 0] == 0) and bs[0] == np.float32(np.float32(1e-9) / np.float32(127.0))
+    assert bs[1] == np.float32(1.0) and bs[2] == np.float32(2.0)
+
+
+def test_i8_quant_bounds_and_gate():
+    rng = np.random.default_rng(5)
+    N, K = 96, 512
+    W = (rng.standard_normal((N, K)) * rng.uniform(0.001, 3.0, (N, 1))).astype(np.float32)
+    codes, bs = O.pack_i8_f32(W)
+    q = codes.T.astype(np.float64)                      # [N][K]
+    mx = np.max(np.abs(W), axis=1).astype(np.float64)
+    assert np.all(np.max(np.abs(codes), axis=0) == 127)  # every channel reaches the grid end
+    assert np.allclose(bs.astype(np.float64), mx / 127.0, rtol=1e-6)
+    err = np.abs(q * bs[:, None].astype(np.float64) - W)
+    assert np.all(err <= 0.5 * bs[:, None] * (1 + 1e-5) + 1e-12)  # nearest grid point, per channel
+
+    # examples/test_matmul.c:280-306: weights and activations (rnd()-128)/64 from the test's LCG,
+    # per-row int8 activations, dequantised int32 GEMM within 3% RMS of the fp64 product
+    st = O.LCGState(12345)
+    M, K, N = 8, 2048, 512
+    Bf = ((O.gen_tm_rnd(st, N * K).astype(np.int32) - 128) / 64.0).astype(np.float32).reshape(N, K)
+    Af = ((O.gen_tm_rnd(st, M * K).astype(np.int32) - 128) / 64.0).astype(np.float32).reshape(M, K)
+    codes, bs = O.pack_i8_f32(Bf)
+    amx = np.maximum(np.max(np.abs(Af), axis=1), np.float32(1e-9)).astype(np.float32)
+    Ai = np.clip(np.rint(Af * (np.float32(127.0) / amx)[:, None]), -127, 127).astype(np.int8)
+    C = O.gemm_i32(Ai, codes)
+    got = (amx / np.float32(127.0))[:, None].astype(np.float64) * bs[None, :] * C
+    ref = Af.astype(np.float64) @ Bf.astype(np.float64).T
+    rms = np.sqrt(np.mean((got - ref) ** 2)) / (np.sqrt(np.mean(ref ** 2)) + 1e-9)
+    assert rms < 0.03
+
+
+# -------------------------------------------------------------------------------------------- NF4
+def test_nf4_codebook():
+    assert list(O.nf4_lut()) == NF4_LUT
+
+
+def test_nf4_nearest_level_brute_force():
+    rng = np.random.default_rng(21)
+    K, N = 1024, 32
+    W = rng.uniform(-1.0, 1.0, (N, K)).astype(np.float32)
+    W[:, 0] = 1.0  # absmax 1 -> normalised weight == w, scale == 1/127
+    bs, nib, codes = O.pack_i4a8(W, nf4=True)
+    assert np.all(bs == np.float32(np.float32(1.0) / np.float32(127.0)))
+    # idx recovered from the nibble store (low nibble = even k)
+    idx = np.empty((N, K), np.int64)
+    idx[:, 0::2] = nib & 0xF
+    idx[:, 1::2] = nib >> 4
+    lut = np.array(NF4_LUT)
+    assert np.array_equal(lut[idx], codes.T.astype(np.int64))
+    # brute force over the 16 levels in float64: the stored index is a nearest level (float32
+    # near-ties excepted)
+    L = NF4_LEVELS
+    assert np.array_equal(np.rint(L * 127).astype(int), lut)
+    d = np.abs(W.astype(np.float64)[:, :, None] - L[None, None, :])
+    chosen = d[np.arange(N)[:, None], np.arange(K)[None, :], idx]
+    assert np.all(chosen <= d.min(axis=2) + 1e-6)
+    # a weight exactly on a level selects that level; a midpoint selects one of its two neighbours
+    Wl = np.zeros((32, 64), np.float32)  # N % 32 == 0 (pack gate); rows 1.. are all-zero channels
+    Wl[0, 0:16] = L.astype(np.float32)
+    Wl[0, 16:31] = ((L[:-1] + L[1:]) / 2).astype(np.float32)
+    _, nibl, _ = O.pack_i4a8(Wl, nf4=True)
+    il = np.empty(64, np.int64)
+    il[0::2] = nibl[0] & 0xF
+    il[1::2] = nibl[0] >> 4
+    assert list(il[0:16]) == list(range(16))
+    assert all(il[16 + i] in (i, i + 1) for i in range(15))
+
+
+def test_nf4_accuracy_gate():
+    """examples/test_matmul.c:402-427: on N(0,1) weights NF4 reconstructs better than uniform int4."""
+    rng = np.random.default_rng(3)
+    K, N = 4096, 256
+    W = rng.standard_normal((N, K)).astype(np.float32)
+    bsu, _, cu = O.pack_i4a8(W, nf4=False)
+    bsn, _, cn = O.pack_i4a8(W, nf4=True)
+    eu = np.sqrt(np.mean((cu.T * bsu[:, None].astype(np.float64) - W) ** 2))
+    en = np.sqrt(np.mean((cn.T * bsn[:, None].astype(np.float64) - W) ** 2))
+    assert en < eu
+
+
+def test_nf4_stochastic_rounding_frequency():
+    """SR picks hi with probability t = (wn - L[lo]) / (L[hi] - L[lo]) and never leaves the bracket."""
+    K = 8192
+    L7, L8 = 0.0, 0.07958029955625534
+    for t in (0.25, 0.7):
+        W = np.full((32, K), np.float32(L7 + t * (L8 - L7)), np.float32)
+        W[:, 0] = 1.0
+        _, nib, _ = O.pack_i4a8(W, nf4=True, sr=True)
+        idx = np.concatenate([(nib & 0xF)[:, 1:], (nib >> 4)], axis=1)
+        assert set(np.unique(idx)) <= {7, 8}
+        frac = float(np.mean(idx == 8))
+        assert abs(frac - t) < 0.01, (t, frac)
+
+
+# ---------------------------------------------------------------------------------- imatrix search
+def _werr64(w, s, im, nf4):
+    if nf4:
+        wn = np.clip(w / (s * 127.0), -1, 1)
+        # the level is chosen on the normalised levels, the value comes from the int8 codebook
+        idx = np.argmin(np.abs(wn[:, None] - NF4_LEVELS[None, :]), axis=1)
+        dq = np.array(NF4_LUT, np.float64)[idx] * s
+    else:
+        dq = np.clip(np.rint(w / s), -7, 7) * s
+    return float(np.sum(im * (w - dq) ** 2))
+
+
+@pytest.mark.parametrize("nf4", [False, True])
+def test_imatrix_clip_is_grid_argmin(nf4):
+    rng = np.random.default_rng(40 + nf4)
+    N, K = 64, 256
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    W[:, ::37] *= 8  # outliers make clipping pay on some channels
+    im = rng.uniform(0.5, 2.0, K).astype(np.float32)
+    bs, _, _ = O.pack_i4a8(W, im, nf4=nf4)
+    div = 127.0 if nf4 else 7.0
+    mx = np.max(np.abs(W), axis=1).astype(np.float64)
+    picked = []
+    for n in range(N):
+        r = bs[n] * div / mx[n]
+        g = int(np.argmin([abs(r - x) for x in CLIP_GRID]))
+        assert abs(r - CLIP_GRID[g]) < 1e-5, (n, r)
+        picked.append(g)
+        errs = [_werr64(W[n].astype(np.float64), mx[n] * x / div, im.astype(np.float64), nf4) for x in CLIP_GRID]
+        assert errs[g] <= min(errs) * (1 + 1e-4), (n, g, errs)
+    assert len(set(picked)) > 1  # the search is exercised, not stuck at absmax
+
+
+def test_imatrix_null_path_and_importance_gate():
+    """examples/test_matmul.c:430-500: with imatrix NULL, bscale == absmax/7 exactly; with important
+    mid-range columns and unimportant outliers the imatrix pack has the lower weighted error."""
+    rng = np.random.default_rng(9)
+    N, K = 128, 2048
+    im = np.where(np.arange(K) < 64, 50.0, 0.01).astype(np.float32)
+    W = (rng.integers(0, 256, (N, K)) - 128).astype(np.float32) / 4096.0
+    W[:, :64] = (rng.integers(0, 256, (N, 64)) - 128).astype(np.float32) / 256.0
+    out = np.arange(K) % 401 == 0
+    out[:64] = False
+    W[:, out] = (rng.choice([-1.0, 1.0], (N, int(out.sum()))) * (6.0 + rng.integers(0, 8, (N, int(out.sum())))))
+    W = W.astype(np.float32)
+    bs0, _, _ = O.pack_i4a8(W, None)
+    mx = np.maximum(np.max(np.abs(W), axis=1), np.float32(1e-9)).astype(np.float32)
+    assert np.array_equal(bs0, (mx / np.float32(7.0)).astype(np.float32))
+    bs1, _, _ = O.pack_i4a8(W, im)
+    e0 = sum(_werr64(W[n].astype(np.float64), float(bs0[n]), im.astype(np.float64), False) for n in range(N))
+    e1 = sum(_werr64(W[n].astype(np.float64), float(bs1[n]), im.astype(np.float64), False) for n in range(N))
+    assert e1 < e0
+
+
+# ------------------------------------------------------------------------------------------- O4N1
+@pytest.mark.parametrize("nf4", [False, True])
+def test_o4n1_layout_and_qerr(nf4):
+    rng = np.random.default_rng(77 + nf4)
+    N, K = 64, 96
+    W = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    im = rng.uniform(0.5, 2.0, K).astype(np.float32)
+    blob, qerr = O.i4a8_blob(W, im, nf4=nf4, want_qerr=True)
+    assert blob.nbytes == 20 + 4 * N + K * N // 2
+    hdr = np.frombuffer(blob[:20].tobytes(), "<u4")
+    assert list(hdr) == [0x4F344E31, 1, K, N, int(nf4)]
+    assert blob[:4].tobytes() == b"1N4O"  # magic 'O4N1' as a little-endian u32
+    bs, nib, codes = O.pack_i4a8(W, im, nf4=nf4)
+    assert blob[20:20 + 4 * N].tobytes() == bs.astype("<f4").tobytes()
+    assert np.array_equal(blob[20 + 4 * N:].reshape(N, K // 2), nib)
+    dec = O.o4n1_decode(K, N, blob)
+    assert dec is not None and np.array_equal(dec[0], bs) and np.array_equal(dec[1], codes)
+    q = codes.T.astype(np.float64) * bs[:, None].astype(np.float64)
+    w = W.astype(np.float64)
+    ref = np.sqrt(np.sum(im * (w - q) ** 2) / np.sum(im * w * w))
+    assert abs(qerr - ref) <= 1e-6 * ref
+    # rejections: magic, version, K, N, kind, size
+    for off, val in ((0, 0x4F344E30), (4, 2), (8, K + 32), (12, N + 32), (16, 2)):
+        bad = blob.copy()
+        bad[off:off + 4] = np.frombuffer(np.array([val], "<u4").tobytes(), np.uint8)
+        assert O.o4n1_decode(K, N, bad) is None, off
+    assert O.o4n1_decode(K, N, blob[:-1]) is None
+
+
+def test_o4n1_c3_size():
+    """examples/test_matmul.c:528: the K=2048, N=6144 blob is 20 + 4N + K*N/2 = 6,316,052 bytes."""
+    assert O.lib().oracle_i4a8_blob(2048, 6144, O._ptr(np.zeros(1, np.float32)), None, 0, 0, None, 0, None) == 6316052
