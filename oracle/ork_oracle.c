@@ -12,7 +12,26 @@
  * scalar branches (the reference says so at each site and its own tests assert it), so only the
  * scalar semantics are restated.
  *
- * Pinning (what checks each function) is listed in oracle/README.md.
+ * What pins each function (tests/test_oracle_golden.py, tests/test_oracle_pins.py):
+ *   oracle_gemm_i32          the reference's FNV-64 goldens (examples/quant.c:72-81, test_matmul.c chains),
+ *                            the reference's own compiled orki_cpu_gemm_i32 (oracle/_ref), brute force
+ *   oracle_gemm_f16_*        test_matmul.c:611-612 goldens (integer-valued inputs: every sum exact)
+ *   oracle_chan_scales_f32, oracle_quant_i8, oracle_pack_i8_f32
+ *                            exact half-even ties, the 1e-9 floor, max|q| = 127, the half-step error
+ *                            bound, the reference's 3% RMS gate (test_matmul.c:280-306)
+ *   oracle_i4_quant_chan     the reference's own compiled orki_i4_quant_chan (oracle/_ref), RN and SR
+ *   oracle_nf4_lut, oracle_nf4_quant_chan (RN)
+ *                            the int8 codebook, nearest level by brute force, the NF4 < uniform gate
+ *                            (test_matmul.c:402-427)
+ *   oracle_nf4_quant_chan (SR)  bracket and P(hi) = t; PARITY UNPINNED for the exact NF4 draw coupling
+ *                            across channels (src/npu.c, which holds the NF4 levels, does not compile
+ *                            on x86, so no compiled reference NF4 exists here)
+ *   oracle_wq_err_chan, oracle_wq_best_absmax
+ *                            grid membership and float64 argmin, NULL path = absmax/7, the importance
+ *                            gate (test_matmul.c:430-500); PARITY UNPINNED for float32 near-ties
+ *   oracle_i4a8_blob, oracle_o4n1_decode
+ *                            header bytes, offsets, size (test_matmul.c:528), round trip, rejections,
+ *                            qerr recomputed in float64
  */
 #include <math.h>
 #include <stdint.h>
