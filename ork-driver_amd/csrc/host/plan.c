@@ -30,7 +30,8 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
     if (force && !strcmp(force, "stream") && M <= 64) stream = 1;
 
     if (stream) {
-        q->algo = ORKH_ALGO_STREAM;
+        /* M = 1 takes the VALU-dot GEMV (same grid and fields); ORK_PLAN=stream keeps the MFMA kernel. */
+        q->algo = (M == 1 && !(force && !strcmp(force, "stream"))) ? ORKH_ALGO_GEMV : ORKH_ALGO_STREAM;
         q->mt = cdiv(M, 16);
         /* Run length per wave: 8 KiB in flight per wave for the int8/fp16 GEMV (M = 1); more waves with
          * shorter runs where each block costs more issue (more rows, int4 decode). Measured on the
