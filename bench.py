@@ -32,6 +32,7 @@ K, N = 2048, 6144
 R = 48                          # rotated resident weight copies
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
 INT8_PEAK_TOPS = 5000.0         # MI355X dense int8 MFMA, TOP/s
+FP16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 MFMA, TFLOP/s
 
 
 def algo_bytes(M):
@@ -85,17 +86,18 @@ class Hip:
         return ms.value
 
 
-def measure(npu, hip, ws, M, dA, dC, steps, warmup):
-    """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % R]."""
+def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run"):
+    """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % len(ws)] through `entry`."""
     import ork
 
     L = ork.lib()
     stream = L.ork_npu_stream(npu.h)
+    fn = getattr(L, entry)
 
     def run(i):
-        rc = L.ork_i8_mm_run(npu.h, ws[i % len(ws)], M, dA, dC)
+        rc = fn(npu.h, ws[i % len(ws)], M, dA, dC)
         if rc:
-            raise RuntimeError(f"ork_i8_mm_run rc={rc}")
+            raise RuntimeError(f"{entry} rc={rc}")
 
     # eager: warmup, then steps individually launched (host launch rate included)
     for i in range(warmup):
@@ -108,6 +110,109 @@ def measure(npu, hip, ws, M, dA, dC, steps, warmup):
     hip.L.hipGraphExecDestroy(ex)
     hip.L.hipGraphDestroy(g)
     return graph, eager
+
+
+def sweep_configs(npu, hip, L, ws_c1, dA, dC):
+    """BASELINE configs 1-4 at their stated shapes, measured like the headline (one HIP graph of
+    rotating resident weights, >= 2x the 256 MB MALL, A and C in HBM): throughput and roofline fraction
+    per config. Each result is spot-checked against the oracle on a few rows."""
+    import ork
+    import oracle as O
+
+    rng = np.random.default_rng(0x6F726B00 + (9 << 8))
+    out = []
+
+    def rec(name, plan, M, ms, nbytes, ops, bound):
+        us = ms * 1e3
+        if bound == "hbm":
+            val, unit, peak = nbytes / (ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS
+        else:
+            val, unit, peak = ops / (ms * 1e-3) / 1e12, "TOP/s" if bound == "mfma_int8" else "TFLOP/s", \
+                (INT8_PEAK_TOPS if bound == "mfma_int8" else FP16_PEAK_TFLOPS)
+        out.append({"config": name, "M": M, "kernel": plan, "us_per_call": round(us, 3), "value": round(val, 1),
+                    "unit": unit, "roofline": {"bound": "hbm" if bound == "hbm" else "mfma", "peak": peak,
+                                               "frac": round(val / peak, 4)}})
+        print(f"[bench] {name} M={M}: {us:.2f} us ({val:.1f} {unit}, {val / peak:.1%} of peak) {plan}",
+              file=sys.stderr, flush=True)
+
+    def steps_for(ms_guess):
+        return max(64, min(2400, int(400.0 / max(ms_guess * 1e3, 1.0))))
+
+    # ---- config 1, M=16 (the headline weights)
+    g, _ = measure(npu, hip, ws_c1, 16, dA, dC, 960, 48)
+    rec("C1 w8a8 K=2048 N=6144", npu.plan_name(ws_c1[0], 16), 16, g, K * N + 16 * K + 4 * 16 * N, 2 * 16 * N * K, "hbm")
+
+    # ---- config 2: fp16, K = N = 2048, M in {1, 16, 128, 512}
+    K2 = N2 = 2048
+    B2 = (rng.standard_normal((K2, N2)) * 0.02).astype(np.float16)
+    A2 = rng.standard_normal((512, K2)).astype(np.float16)
+    ws2 = [npu.pack_f16(B2) for _ in range(64)]   # 64 x 8 MB
+    dA2 = L.ork_dev_alloc(npu.h, A2.nbytes)
+    assert all(ws2) and dA2 and L.ork_dev_upload(npu.h, dA2, ork.ptr(A2), A2.nbytes) == 0
+    for M in (1, 16, 128, 512):
+        n = steps_for(0.006 if M < 512 else 0.012)
+        g, _ = measure(npu, hip, ws2, M, dA2, dC, n, 16, "ork_f16_mm_run")
+        rec("C2 fp16 K=N=2048", npu.plan_name(ws2[0], M), M, g, 2 * M * K2 + 2 * K2 * N2 + 4 * M * N2,
+            2 * M * N2 * K2, "hbm" if M <= 128 else "mfma_fp16")
+    L.ork_npu_set_async(npu.h, 0)
+    C2 = np.empty((4, N2), np.float32)
+    assert L.ork_f16_mm_run(npu.h, ws2[0], 4, dA2, dC) == 0
+    assert L.ork_dev_download(npu.h, ork.ptr(C2), dC, C2.nbytes) == 0
+    assert O.fp16_err(C2, O.gemm_f16_f64acc(A2[:4], B2)) <= 2e-3, "fp16 spot check"
+    L.ork_npu_set_async(npu.h, 1)
+    for w in ws2:
+        L.ork_mm_free(npu.h, w)
+    L.ork_dev_free(npu.h, dA2)
+
+    # ---- config 3: w4a8, K=2048, N=6144, importance vector, uniform and NF4, M in {1, 64}
+    W3 = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    im3 = rng.uniform(0.5, 2.0, K).astype(np.float32)
+    for nf4 in (0, 1):
+        if nf4:
+            os.environ["ORK_NF4"] = "1"
+        try:
+            w0, _ = npu.pack_i4a8(W3, im3)
+        finally:
+            os.environ.pop("ORK_NF4", None)
+        blob = ork.dump_i4a8(w0)
+        ws3 = [w0] + [npu.load_i4a8(K, N, blob) for _ in range(83)]   # 84 x 6.3 MB
+        assert all(ws3)
+        name = "C3 w4a8 %s K=2048 N=6144" % ("nf4" if nf4 else "uniform")
+        for M in (1, 64):
+            g, _ = measure(npu, hip, ws3, M, dA, dC, steps_for(0.003), 32)
+            rec(name, npu.plan_name(ws3[0], M), M, g, K * N // 2 + M * K + 4 * M * N, 2 * M * N * K, "hbm")
+        L.ork_npu_set_async(npu.h, 0)
+        A3 = np.empty((2, K), np.int8)
+        assert L.ork_dev_download(npu.h, ork.ptr(A3), dA, A3.nbytes) == 0
+        C3 = np.empty((2, N), np.int32)
+        assert L.ork_i8_mm_run(npu.h, ws3[-1], 2, dA, dC) == 0
+        assert L.ork_dev_download(npu.h, ork.ptr(C3), dC, C3.nbytes) == 0
+        _, codes3 = O.o4n1_decode(K, N, blob)
+        assert np.array_equal(C3, O.gemm_i32(A3, codes3)), "w4a8 spot check"
+        L.ork_npu_set_async(npu.h, 1)
+        for w in ws3:
+            L.ork_mm_free(npu.h, w)
+
+    # ---- config 4: W4A4, M=256, K=N=4096, values in [-8, 7]
+    K4 = N4 = 4096
+    B4 = rng.integers(-8, 8, size=(K4, N4), dtype=np.int8)
+    A4 = rng.integers(-8, 8, size=(256, K4), dtype=np.int8)
+    ws4 = [npu.pack_i4(B4) for _ in range(64)]   # 64 x 8 MB of nibbles
+    dA4 = L.ork_dev_alloc(npu.h, A4.nbytes)
+    assert all(ws4) and dA4 and L.ork_dev_upload(npu.h, dA4, ork.ptr(A4), A4.nbytes) == 0
+    g, _ = measure(npu, hip, ws4, 256, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run")
+    rec("C4 W4A4 K=N=4096", npu.plan_name(ws4[0], 256), 256, g, 256 * K4 + K4 * N4 // 2 + 4 * 256 * N4,
+        2 * 256 * N4 * K4, "mfma_int8")
+    L.ork_npu_set_async(npu.h, 0)
+    C4 = np.empty((256, N4), np.int32)
+    assert L.ork_dev_download(npu.h, ork.ptr(C4), dC, C4.nbytes) == 0
+    assert np.array_equal(C4[:2], O.gemm_i32(A4[:2], B4)) and np.array_equal(C4[-2:], O.gemm_i32(A4[-2:], B4)), \
+        "W4A4 spot check"
+    L.ork_npu_set_async(npu.h, 1)
+    for w in ws4:
+        L.ork_mm_free(npu.h, w)
+    L.ork_dev_free(npu.h, dA4)
+    return out
 
 
 def copy_calibration(hip, L, reps=96):
@@ -166,6 +271,7 @@ def main():
     ap.add_argument("--m512-steps", type=int, default=480)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the sweep over BASELINE configs 1-4")
     ap.add_argument("--only", choices=["gemv", "m512"], help="profiling: time only one of the two kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling: run device-to-device copies of one weight's bytes (a plain copy kernel of "
@@ -245,6 +351,12 @@ def main():
         assert np.array_equal(Ch, O.gemm_i32(Ah, codes)), "host-pointer M=1 result differs from the oracle"
         print(f"[bench] M=1 host pointers, synchronous: {host_us:.2f} us/call", file=sys.stderr, flush=True)
 
+        configs = None
+        if not args.no_configs:
+            L.ork_npu_set_async(npu.h, 1)
+            configs = sweep_configs(npu, hip, L, ws, dA, dC)
+            L.ork_npu_set_async(npu.h, 0)
+
         for w in ws:
             ork.lib().ork_mm_free(npu.h, w)
         L.ork_dev_free(npu.h, dA)
@@ -280,6 +392,8 @@ def main():
                  "hbm_gbs": round(algo_bytes(512) / (g512 * 1e-3) / 1e9, 1),
                  "eager_value": round(algo_ops(512) / (e512 * 1e-3) / 1e12, 1)},
     }
+    if configs is not None:
+        out["configs"] = configs
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(codes, A512[:1], args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -347,8 +347,11 @@ constexpr size_t tiled_lds_bytes() {
 // Both operands run D stages ahead through a ring of register slots (stage t in slot t % D); one
 // barrier per stage. Loads are raw buffer loads: rows >= M, k >= K and stages past the end read 0
 // through the hardware range check (no clamps, no selects, no faults).
+// Split K (shapes with too few tiles to fill the CUs): the grid holds ntiles x ksplit workgroups; the
+// one mapped to (tile, ks) covers K-blocks [ks*kbs, ks*kbs + kbs) and writes its partial tile to ws,
+// summed afterwards by k_splitk_reduce in fixed order.
 template <int KIND, int BM, int BN, int KS, int D, int KG>
-__global__ __launch_bounds__(256 * KG) void k_tiled(orkh_mm p, int mtiles) {
+__global__ __launch_bounds__(256 * KG) void k_tiled(orkh_mm p, int mtiles, int ntiles_all, int kbs, void *ws) {
     using T = KT<KIND>;
     typedef typename T::acc_t acc_t;
     constexpr int MB = BM / 16, NBK = BN / 16;
@@ -368,11 +371,14 @@ __global__ __launch_bounds__(256 * KG) void k_tiled(orkh_mm p, int mtiles) {
     // every M-tile that reads a given B column panel shares one L2.
     const int nT = gridDim.x, bid = blockIdx.x;
     const int per = nT / 8, rem = nT % 8, x = bid % 8, j = bid / 8;
-    const int tile = (x < rem) ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    const int tl = (x < rem) ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    const int ks = tl / ntiles_all, tile = tl % ntiles_all;   // each XCD's run: one K range, M fastest
     const int m0 = (tile % mtiles) * BM;
     const int nb0 = (tile / mtiles) * NBK;
     const int NBtot = p.N / 16;
     const Lut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
+    const int kb_lo = ks * kbs, kb_hi = min(kb_lo + kbs, p.KB);   // this workgroup's K-blocks
+    const int k_hi = min(kb_hi * T::KPB, p.K);
 
     const uint32_t lda_b = (uint32_t)p.lda * T::ESZ;
     const __amdgpu_buffer_rsrc_t Ar = make_rsrc(p.A, (uint32_t)p.M * lda_b);
@@ -401,15 +407,15 @@ __global__ __launch_bounds__(256 * KG) void k_tiled(orkh_mm p, int mtiles) {
     v4i ra[D][AV], rb[D][NTW][KS];
     // ls = this group's local stage; its global stage is ls * KG + grp.
     auto gload = [&](int ls, v4i (&xa)[AV], v4i (&xb)[NTW][KS]) {
-        const int st = ls * KG + grp, k0 = st * KSPAN;
+        const int st = ls * KG + grp, k0 = kb_lo * T::KPB + st * KSPAN;
 #pragma unroll
         for (int i = 0; i < AV; i++)
-            xa[i] = bload(Ar, k0 + a_k[i] < p.K ? a_off[i] + (uint32_t)k0 * T::ESZ : OOB);
+            xa[i] = bload(Ar, k0 + a_k[i] < k_hi ? a_off[i] + (uint32_t)k0 * T::ESZ : OOB);
 #pragma unroll
         for (int kbl = 0; kbl < KS; kbl++) {
-            const int kb = st * KS + kbl;
+            const int kb = kb_lo + st * KS + kbl;
 #pragma unroll
-            for (int jn = 0; jn < NTW; jn++) xb[jn][kbl] = bload(Br, kb < p.KB ? b_off[jn] + (uint32_t)kb * 1024u : OOB);
+            for (int jn = 0; jn < NTW; jn++) xb[jn][kbl] = bload(Br, kb < kb_hi ? b_off[jn] + (uint32_t)kb * 1024u : OOB);
         }
     };
     auto lstore = [&](int buf, const v4i (&xa)[AV]) {
@@ -444,7 +450,7 @@ __global__ __launch_bounds__(256 * KG) void k_tiled(orkh_mm p, int mtiles) {
 
     // Each group's stage count is rounded up to a multiple of D (the extra stages read zeros and add
     // nothing), so the ring has no branches and every wait is a partial vmcnt.
-    const int nst = (p.KB + KS - 1) / KS;
+    const int nst = (kb_hi - kb_lo + KS - 1) / KS;
     const int nls = ((nst + KG - 1) / KG + D - 1) / D * D;
 #pragma unroll
     for (int jd = 0; jd < D; jd++) gload(jd, ra[jd], rb[jd]);
@@ -479,7 +485,9 @@ __global__ __launch_bounds__(256 * KG) void k_tiled(orkh_mm p, int mtiles) {
     }
 
     typedef typename T::c_t c_t;
-    c_t *C = (c_t *)p.C;
+    const bool split = gridDim.x > ntiles_all;
+    c_t *C = split ? (c_t *)ws + (size_t)ks * p.M * p.N : (c_t *)p.C;
+    const size_t ldc = split ? (size_t)p.N : (size_t)p.ldc;
 #pragma unroll
     for (int i = 0; i < MTW; i++)
 #pragma unroll
@@ -490,7 +498,7 @@ __global__ __launch_bounds__(256 * KG) void k_tiled(orkh_mm p, int mtiles) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + (wm * MTW + i) * 16 + (lane >> 4) * 4 + r;
-                if (m < p.M) C[(size_t)m * p.ldc + n] = finish<KIND>(acc[i][jn][r]);
+                if (m < p.M) C[(size_t)m * ldc + n] = finish<KIND>(acc[i][jn][r]);
             }
         }
 }
@@ -545,7 +553,7 @@ int launch_stream(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
 }
 
 template <int KIND, int BM, int BN>
-int launch_tiled_v(const orkh_mm *p, hipStream_t s) {
+int launch_tiled_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int KS = 1;
     constexpr int D = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 3 : 4;
     constexpr int KG = 2;
@@ -559,15 +567,23 @@ int launch_tiled_v(const orkh_mm *p, hipStream_t s) {
     }
     const int mtiles = (p->M + BM - 1) / BM;
     const int ntiles = (p->N / 16 + BN / 16 - 1) / (BN / 16);
-    hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(256 * KG), lds, s, *p, mtiles);
+    const int ksplit = q->ksplit > 1 ? q->ksplit : 1;
+    const int kbs = ksplit > 1 ? q->kbs : p->KB;
+    hipLaunchKernelGGL(kern, dim3(mtiles * ntiles * ksplit), dim3(256 * KG), lds, s, *p, mtiles, mtiles * ntiles, kbs,
+                       q->ws);
     return 0;
 }
 
 template <int KIND>
 int launch_tiled(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
-    if (q->bm == 128 && q->bn == 96) return launch_tiled_v<KIND, 128, 96>(p, s);
-    if (q->bm == 128 && q->bn == 128) return launch_tiled_v<KIND, 128, 128>(p, s);
-    if (q->bm == 64 && q->bn == 64) return launch_tiled_v<KIND, 64, 64>(p, s);
+    if (q->ksplit > 1 && (!q->ws || (long)q->ksplit * q->kbs < p->KB)) {
+        snprintf(g_lerr, sizeof g_lerr, "tiled plan: ksplit=%d kbs=%d does not cover KB=%d or has no ws", q->ksplit,
+                 q->kbs, p->KB);
+        return -2;
+    }
+    if (q->bm == 128 && q->bn == 96) return launch_tiled_v<KIND, 128, 96>(p, q, s);
+    if (q->bm == 128 && q->bn == 128) return launch_tiled_v<KIND, 128, 128>(p, q, s);
+    if (q->bm == 64 && q->bn == 64) return launch_tiled_v<KIND, 64, 64>(p, q, s);
     snprintf(g_lerr, sizeof g_lerr, "tiled plan: %dx%d unsupported", q->bm, q->bn);
     return -2;
 }
@@ -620,6 +636,16 @@ extern "C" int orkh_mm_launch(const orkh_mm *p, const orkh_plan *q, void *stream
         case ORKH_F16: rc = launch_tiled<ORKH_F16>(p, q, s); break;
         default: rc = -2;
         }
+        if (rc == 0 && q->ksplit > 1) {
+            const size_t MN = (size_t)p->M * p->N;
+            dim3 grid((unsigned)((MN + 255) / 256)), block(256);
+            if (p->kind == ORKH_F16)
+                hipLaunchKernelGGL(k_splitk_reduce<float>, grid, block, 0, s, (const float *)q->ws, (float *)p->C,
+                                   p->M, p->N, p->ldc, q->ksplit);
+            else
+                hipLaunchKernelGGL(k_splitk_reduce<int32_t>, grid, block, 0, s, (const int32_t *)q->ws,
+                                   (int32_t *)p->C, p->M, p->N, p->ldc, q->ksplit);
+        }
     }
     if (rc) return rc;
     hipError_t e = hipGetLastError();
@@ -638,6 +664,8 @@ extern "C" const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *q) {
         snprintf(b, sizeof b, "gemv_%s_w%d_kbw%d_ks%d", k, q->wpg, q->kbw, q->ksplit);
     else if (q->algo == ORKH_ALGO_STREAM)
         snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d", k, q->mt, q->wpg, q->kbw, q->ksplit);
+    else if (q->ksplit > 1)
+        snprintf(b, sizeof b, "tiled_%s_%dx%d_ks%d", k, q->bm, q->bn, q->ksplit);
     else
         snprintf(b, sizeof b, "tiled_%s_%dx%d", k, q->bm, q->bn);
     return b;

@@ -9,8 +9,8 @@
  *   M <= 64  stream: one 16-column panel per workgroup, waves split K in runs of 1 KiB blocks (8 per
  *            run for the int8/fp16 GEMV); K is split across workgroups only for long-K, few-panel
  *            shapes that leave the machine underfilled. ORK_KSPLIT=n forces a split (tests).
- *   M >  64  tiled: the BM x BN tile (128x96, 128x128 or 64x64) with the fewest tile-rounds of work
- *            per CU, larger tile on ties. */
+ *   M >  64  tiled: the BM x BN tile (128x96, 128x128 or 64x64) and K split with the least modelled
+ *            time (operand bytes per workgroup-round, plus partials and a reduce launch when split). */
 #include <stdlib.h>
 #include <string.h>
 
@@ -62,22 +62,38 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
         return 0;
     }
 
+    /* Tiled: each CU pulls its tiles' A and B rows through L2 at a roughly fixed rate, so the time of a
+     * round of workgroups is about the operand bytes one workgroup loads. K is split across
+     * workgroups when that cuts the per-workgroup bytes by more than the partial sums and the extra
+     * reduce launch (~2 us) cost. Model units: us at ~48 KB/us per CU (measured order of magnitude),
+     * 5 TB/s for the partials' HBM round trip. */
     static const int cfg[][2] = {{128, 96}, {128, 128}, {64, 64}};
-    long best = -1;
-    int bi = 0;
+    const int bpk = 64;                                                  /* B bytes per column per K-block, every kind */
+    const int apk = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 128 : 64; /* A bytes per row per K-block */
+    const char *fks = getenv("ORK_KSPLIT");
+    int ks_force = fks ? atoi(fks) : 0;
+    if (ks_force > 0) ks_force = cdiv(KB, cdiv(KB, ks_force < KB ? ks_force : KB)); /* as a split can realise it */
+    double best = -1;
     for (int i = 0; i < 3; i++) {
         const int bm = cfg[i][0], bn = cfg[i][1];
         const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);
-        const long rounds = (tiles + cu - 1) / cu;
-        const long cost = rounds * bm * bn;
-        if (best < 0 || cost < best || (cost == best && bm * bn > cfg[bi][0] * cfg[bi][1])) {
-            best = cost;
-            bi = i;
+        for (int ks = ks_force > 0 ? ks_force : 1; ks <= (ks_force > 0 ? ks_force : 8); ks++) {
+            const int kbs = cdiv(KB, ks);
+            if (ks_force <= 0 && (cdiv(KB, kbs) != ks || (ks > 1 && kbs < 4))) continue;
+            const long wgs = tiles * ks;
+            const long rounds = (wgs + cu - 1) / cu;
+            double t = rounds * (double)(bm * apk + bn * bpk) * kbs / 48e3;
+            if (ks > 1) t += 2.0 + 2.0 * ks * (double)M * N * 4 / 5e6;
+            if (best < 0 || t < best - 1e-9) {
+                best = t;
+                q->bm = bm;
+                q->bn = bn;
+                q->ksplit = ks;
+                q->kbs = kbs;
+            }
         }
     }
     q->algo = ORKH_ALGO_TILED;
-    q->bm = cfg[bi][0];
-    q->bn = cfg[bi][1];
-    q->ksplit = 1;
+    if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
     return 0;
 }

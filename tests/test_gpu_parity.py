@@ -121,6 +121,38 @@ def test_forced_split_k_all_kinds(npu, ks):
         ork.free(w)
 
 
+@pytest.mark.parametrize("ks", [2, 3, 8])
+def test_forced_tiled_split_k(npu, ks):
+    """The tiled kernel with K split across workgroups (partials + fixed-order reduce): exact for int8 and
+    int4, within tolerance and run-to-run identical for fp16; M and N tails included."""
+    _say("tiled split-k", ks)
+    rng = _rng(50 + ks)
+    M, K, N = 200, 2080, 192
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    w = npu.pack_i8(B)
+    with _env(ORK_PLAN="tiled", ORK_KSPLIT=ks):
+        rc, C = npu.run_i8(w, A)
+        assert "_ks" in npu.plan_name(w, M), npu.plan_name(w, M)
+    assert rc == 0 and np.array_equal(C, O.gemm_i32(A, B)), ("i8", npu.plan_name(w, M))
+    ork.free(w)
+    A4, B4 = O.gen_i4_test(M, K, N)
+    w = npu.pack_i4(B4)
+    with _env(ORK_PLAN="tiled", ORK_KSPLIT=ks):
+        rc, C = npu.run_i4(w, A4)
+    assert rc == 0 and np.array_equal(C, O.gemm_i32(A4, B4)), "w4a4"
+    ork.free(w)
+    Ah = rng.standard_normal((M, K)).astype(np.float16)
+    Bh = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+    w = npu.pack_f16(Bh)
+    with _env(ORK_PLAN="tiled", ORK_KSPLIT=ks):
+        rc, C1 = npu.run_f16(w, Ah)
+        rc2, C2 = npu.run_f16(w, Ah)
+    assert rc == 0 and rc2 == 0 and np.array_equal(C1, C2)
+    assert O.fp16_err(C1, O.gemm_f16_f64acc(Ah, Bh)) <= FP16_TOL
+    ork.free(w)
+
+
 @pytest.mark.parametrize("idx", range(7))
 def test_quant_c_goldens_on_gpu(npu, idx):
     """examples/quant.c end to end: ork_i8_mm_pack + ork_i8_mm_run, FNV-64 of C == the reference golden."""
