@@ -215,6 +215,31 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
     return out
 
 
+def measure_chain(npu, hip, L, ws, dA, dC, S, steps):
+    """ms per ork_i8_mm_run_chain call of S M=1 GEMVs (the multi-matmul submit), graph-timed like
+    measure(): call i runs weights ws[(i*S + j) % len(ws)], one shared activation row, S output rows."""
+    import ork
+
+    stream = L.ork_npu_stream(npu.h)
+    nsets = len(ws) // S
+    sets = [ork.tasks(ork.TaskI8, [(ws[(k * S + j) % len(ws)], 1, dA, dC + j * N * 4, 0) for j in range(S)])
+            for k in range(nsets)]
+
+    def run(i):
+        rc = L.ork_i8_mm_run_chain(npu.h, S, sets[i % nsets])
+        if rc:
+            raise RuntimeError(f"ork_i8_mm_run_chain rc={rc}")
+
+    for i in range(2 * nsets):
+        run(i)
+    g, ex = hip.capture(stream, lambda: [run(i) for i in range(steps)])
+    hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")
+    ms = hip.time_ms(stream, lambda: hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")) / steps
+    hip.L.hipGraphExecDestroy(ex)
+    hip.L.hipGraphDestroy(g)
+    return ms
+
+
 def copy_calibration(hip, L, reps=96):
     """Device-to-device copies of K*N bytes (hipMemcpyAsync D2D: the runtime's copy kernel) between
     rotated buffers, so rocprofv3's FETCH_SIZE / WRITE_SIZE for a kernel of known traffic can be read."""
@@ -351,6 +376,18 @@ def main():
         assert np.array_equal(Ch, O.gemm_i32(Ah, codes)), "host-pointer M=1 result differs from the oracle"
         print(f"[bench] M=1 host pointers, synchronous: {host_us:.2f} us/call", file=sys.stderr, flush=True)
 
+        # the multi-matmul submit: 8 GEMVs of the same shape per call, one grouped launch
+        L.ork_npu_set_async(npu.h, 1)
+        S8 = 8
+        chain_ms = measure_chain(npu, hip, L, ws, dA, dC, S8, 300)
+        L.ork_npu_set_async(npu.h, 0)
+        Cch = np.empty((S8, N), np.int32)
+        assert L.ork_dev_download(npu.h, ork.ptr(Cch), dC, Cch.nbytes) == 0
+        assert np.array_equal(Cch, np.repeat(O.gemm_i32(A512[:1], codes), S8, axis=0)), "chain result differs"
+        chain_gbs = S8 * algo_bytes(1) / (chain_ms * 1e-3) / 1e9
+        print(f"[bench] ork_i8_mm_run_chain of {S8} M=1 GEMVs: {chain_ms * 1e3:.2f} us/call "
+              f"({chain_gbs:.0f} GB/s aggregate)", file=sys.stderr, flush=True)
+
         configs = None
         if not args.no_configs:
             L.ork_npu_set_async(npu.h, 1)
@@ -382,6 +419,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_i8_m1")},
         "eager_value": round(algo_bytes(1) / (e1 * 1e-3) / 1e9, 1),
+        "chain8": {"value": round(chain_gbs, 1), "unit": "GB/s", "us_per_call": round(chain_ms * 1e3, 3),
+                   "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
+                   "note": "ork_i8_mm_run_chain: 8 M=1 GEMVs of the same shape (distinct resident weights) per call, "
+                           "one grouped launch; A and C in HBM; HIP graph of 300 calls"},
         "host_api": {"value": round(algo_bytes(1) / (host_us * 1e-6) / 1e9, 1), "unit": "GB/s",
                      "us_per_call": round(host_us, 2),
                      "note": "ork_i8_mm_run(M=1) with host A and C: H2D of A, launch, D2H of C, stream sync"},

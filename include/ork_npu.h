@@ -7,8 +7,9 @@
  *   C[M,N] (int32) = A[M,K] (int8)  x B[K,N] (int8 / int4 / NF4 codes)   ork_i8_mm_run, ork_i4_mm_run
  *   C[M,N] (fp32)  = A[M,K] (fp16)  x B[K,N] (fp16)                      ork_f16_mm_run
  *
- * Only the resident-weight matmul subset is provided (context, DMA buffers, pack/load/dump, run);
- * ork/hip.h adds device-resident operands for callers that keep A and C in HBM.
+ * Only the resident-weight matmul subset is provided (context, DMA buffers, pack/load/dump, run, and
+ * the multi-matmul submit of ork/chain.h); ork/hip.h adds device-resident operands for callers that
+ * keep A and C in HBM.
  */
 #ifndef ORK_NPU_H
 #define ORK_NPU_H
@@ -32,6 +33,7 @@ typedef struct ork_w ork_w;         /* resident packed weights for one B[K,N]  -
 #include "ork/dma.h"
 #include "ork/weights.h"
 #include "ork/run.h"
+#include "ork/chain.h"
 #include "ork/hip.h"
 
 #ifdef __cplusplus

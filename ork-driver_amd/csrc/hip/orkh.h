@@ -58,6 +58,8 @@ int         orkh_host_free(void *p);
 int         orkh_h2d(void *dst, const void *src, size_t n, void *stream);   /* async; direction inferred */
 int         orkh_d2h(void *dst, const void *src, size_t n, void *stream);   /* async */
 int         orkh_d2d(void *dst, const void *src, size_t n, void *stream);   /* async */
+/* async strided copy: rows x width bytes, row pitches dpitch / spitch */
+int         orkh_d2h_2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t rows, void *stream);
 int         orkh_sync(void *stream);
 int         orkh_device_sync(void);
 /* 1 if p is device (or device-mapped) memory known to the HIP runtime, 0 if plain host memory. */
@@ -97,6 +99,22 @@ typedef struct orkh_plan {
 } orkh_plan;
 
 int orkh_mm_launch(const orkh_mm *p, const orkh_plan *plan, void *stream);
+
+/* Grouped M = 1 launch (multi-matmul submit): n independent GEMVs of one kind (p.kind equal, p.M == 1)
+ * in one launch. Task i covers workgroups [t[i].wg0, t[i].wg0 + p.N/16), wg0 ascending from 0 with no
+ * gaps; each workgroup runs wpg waves over the whole K of one panel, kbw K-blocks per wave
+ * (kbw * wpg >= p.KB). */
+#define ORKH_GROUP_MAX 16
+typedef struct orkh_gtask {
+    orkh_mm p;
+    int kbw;
+    int wg0;
+} orkh_gtask;
+typedef struct orkh_group {
+    int n;
+    orkh_gtask t[ORKH_GROUP_MAX];
+} orkh_group;
+int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream);
 /* Names of the compiled kernel variants, for diagnostics ("stream_i8_mt1_w4", ...). */
 const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *plan);
 

@@ -227,19 +227,19 @@ template <int LANE> __device__ __forceinline__ int row_bcast(int x) {
 }
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
+// One panel (nb) x one K range (ks) of a GEMV: the body shared by k_gemv and k_gemv_group.
 template <int KIND, int WPG, int KU>
-__global__ __launch_bounds__(WPG * 64) void k_gemv(orkh_mm p, int kbw, int kbs, int ksplit, void *ws) {
+__device__ __forceinline__ void gemv_panel(const orkh_mm &p, int nb, int ks, int kbw, int kbs, int ksplit, void *ws,
+                                           typename KT<KIND>::c_t (*red)[16]) {
     using T = KT<KIND>;
     typedef typename T::c_t c_t;
     constexpr int W = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 8 : 4;  // activation dwords per group per block
     constexpr int BPL = 16 / W;                                         // blocks per activation load
     constexpr int KPBB = T::KPB * T::ESZ;                               // activation bytes per block
     static_assert(KU % BPL == 0, "a full batch must cover whole activation loads");
-    __shared__ c_t red[WPG][16];
 
     // the wave index is wave-uniform: keep it (and every bound derived from it) in SGPRs
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = lane >> 4, i = lane & 15;
-    const int nb = blockIdx.x, ks = blockIdx.y;
     const int kb_hi = min(ks * kbs + kbs, p.KB);
     const int kb0 = ks * kbs + w * kbw;
     const int kb1 = min(kb0 + kbw, kb_hi);
@@ -310,6 +310,23 @@ __global__ __launch_bounds__(WPG * 64) void k_gemv(orkh_mm p, int kbw, int kbs, 
         if (ksplit == 1) ((c_t *)p.C)[n] = finish<KIND>(s);
         else ((c_t *)ws)[(size_t)ks * p.N + n] = finish<KIND>(s);
     }
+}
+
+template <int KIND, int WPG, int KU>
+__global__ __launch_bounds__(WPG * 64) void k_gemv(orkh_mm p, int kbw, int kbs, int ksplit, void *ws) {
+    __shared__ typename KT<KIND>::c_t red[WPG][16];
+    gemv_panel<KIND, WPG, KU>(p, blockIdx.x, blockIdx.y, kbw, kbs, ksplit, ws, red);
+}
+
+// k_gemv_group: up to ORKH_GROUP_MAX independent M = 1 GEMVs of one kind in a single launch (the
+// multi-matmul submit). Task t owns workgroups [t.wg0, t.wg0 + N/16), one panel each, whole K.
+template <int KIND, int WPG, int KU>
+__global__ __launch_bounds__(WPG * 64) void k_gemv_group(orkh_group g) {
+    __shared__ typename KT<KIND>::c_t red[WPG][16];
+    int t = g.n - 1;
+    while (t > 0 && (int)blockIdx.x < g.t[t].wg0) t--;
+    const orkh_gtask &tk = g.t[t];
+    gemv_panel<KIND, WPG, KU>(tk.p, (int)blockIdx.x - tk.wg0, 0, tk.kbw, tk.p.KB, 1, nullptr, red);
 }
 
 // Fixed-order sum of split-K partials (deterministic for fp32 as well as exact for int32). A separate
@@ -648,6 +665,43 @@ extern "C" int orkh_mm_launch(const orkh_mm *p, const orkh_plan *q, void *stream
         }
     }
     if (rc) return rc;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_lerr, sizeof g_lerr, "launch: %s", hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (g->n < 1 || g->n > ORKH_GROUP_MAX) {
+        snprintf(g_lerr, sizeof g_lerr, "group: n=%d", g->n);
+        return -2;
+    }
+    int wgs = 0;
+    for (int i = 0; i < g->n; i++) {
+        const orkh_mm &p = g->t[i].p;
+        if (p.kind != g->t[0].p.kind || p.M != 1 || g->t[i].wg0 != wgs || (long)g->t[i].kbw * wpg < p.KB) {
+            snprintf(g_lerr, sizeof g_lerr, "group: task %d inconsistent (kind %d M %d wg0 %d kbw %d)", i, p.kind, p.M,
+                     g->t[i].wg0, g->t[i].kbw);
+            return -2;
+        }
+        wgs += p.N / 16;
+    }
+    dim3 grid(wgs), block(wpg * 64);
+#define ORKH_GROUP_CASE(KIND, KU)                                                                    \
+    if (wpg == 4) hipLaunchKernelGGL((k_gemv_group<KIND, 4, KU>), grid, block, 0, s, *g);            \
+    else if (wpg == 8) hipLaunchKernelGGL((k_gemv_group<KIND, 8, KU>), grid, block, 0, s, *g);       \
+    else { snprintf(g_lerr, sizeof g_lerr, "group: wpg=%d unsupported", wpg); return -2; }
+    switch (g->t[0].p.kind) {
+    case ORKH_I8: ORKH_GROUP_CASE(ORKH_I8, 8) break;
+    case ORKH_I4U: ORKH_GROUP_CASE(ORKH_I4U, 4) break;
+    case ORKH_NF4: ORKH_GROUP_CASE(ORKH_NF4, 4) break;
+    case ORKH_F16: ORKH_GROUP_CASE(ORKH_F16, 8) break;
+    default: snprintf(g_lerr, sizeof g_lerr, "group: kind %d", g->t[0].p.kind); return -2;
+    }
+#undef ORKH_GROUP_CASE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_lerr, sizeof g_lerr, "launch: %s", hipGetErrorString(e));

@@ -106,6 +106,13 @@ int orkh_d2h(void *dst, const void *src, size_t n, void *stream) {
     return 0;
 }
 
+int orkh_d2h_2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t rows, void *stream) {
+    if (!width || !rows) return 0;
+    CK(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, rows, hipMemcpyDefault, (hipStream_t)stream),
+       "hipMemcpy2DAsync D2H");
+    return 0;
+}
+
 int orkh_d2d(void *dst, const void *src, size_t n, void *stream) {
     if (!n) return 0;
     CK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)stream), "hipMemcpyAsync D2D");

@@ -51,6 +51,11 @@ API = {
     "ork_i8_mm_run": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "ork_i4_mm_run": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "ork_i8_mm_run_cpu": (None, [C.c_int, C.c_int, C.c_int, _P, _P, _P]),
+    "ork_i8_mm_run_chain": (C.c_int, [_P, C.c_int, _P]),
+    "ork_i8_mm_run_stream": (C.c_int, [_P, C.c_int, _P]),
+    "ork_i4_mm_run_chain": (C.c_int, [_P, C.c_int, _P]),
+    "ork_i4_mm_run_stream": (C.c_int, [_P, C.c_int, _P]),
+    "ork_f16_mm_run_stream": (C.c_int, [_P, C.c_int, _P]),
     "ork_dev_alloc": (_P, [_P, C.c_size_t]),
     "ork_dev_free": (None, [_P, _P]),
     "ork_dev_upload": (C.c_int, [_P, _P, _P, C.c_size_t]),
@@ -60,6 +65,34 @@ API = {
     "ork_npu_stream": (_P, [_P]),
     "ork_w_plan_name": (C.c_char_p, [_P, _P, C.c_int]),
 }
+
+
+
+class TaskI8(C.Structure):
+    """ork_mm_task_i8 (include/ork/chain.h)"""
+    _fields_ = [("w", _P), ("M", C.c_int), ("A", _P), ("C", _P), ("cstride", C.c_int)]
+
+
+class TaskI4(C.Structure):
+    """ork_mm_task_i4 / ork_mm_task_f16 (same layout: w, M, A, C)"""
+    _fields_ = [("w", _P), ("M", C.c_int), ("A", _P), ("C", _P)]
+
+
+TaskF16 = TaskI4
+
+
+def tasks(cls, rows):
+    """A ctypes array of task structs from tuples (w, M, A, C[, cstride]); A and C are arrays or ints."""
+    arr = (cls * len(rows))()
+    for i, r in enumerate(rows):
+        arr[i].w = r[0]
+        arr[i].M = r[1]
+        arr[i].A = ptr(r[2])
+        arr[i].C = ptr(r[3])
+        if len(r) > 4:
+            arr[i].cstride = r[4]
+    return arr
+
 
 _lib = None
 

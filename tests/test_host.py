@@ -207,6 +207,26 @@ def test_cpu_gemm_api_matches_oracle():
         assert np.array_equal(Cm, O.gemm_i32(A, B))
 
 
+def test_chain_argument_checks_offline(off):
+    """ork/chain.h: bad arguments are -2 before anything else; an offline context cannot run (-1,
+    no CPU fallback in this build)."""
+    L = ork.lib()
+    B = np.zeros((64, 64), np.int8)
+    w = L.ork_i8_mm_pack(off.h, 64, 64, ork.ptr(B))
+    A = np.zeros((1, 64), np.int8)
+    Cb = np.zeros((1, 64), np.int32)
+    t = ork.tasks(ork.TaskI8, [(w, 1, A, Cb)])
+    assert L.ork_i8_mm_run_chain(off.h, 0, t) == -2
+    assert L.ork_i8_mm_run_chain(off.h, 1025, t) == -2
+    assert L.ork_i8_mm_run_chain(off.h, 1, None) == -2
+    assert L.ork_i8_mm_run_chain(None, 1, t) == -1
+    assert L.ork_i8_mm_run_stream(None, 1, t) == -2
+    assert L.ork_i8_mm_run_chain(off.h, 1, t) == -1
+    assert L.ork_i4_mm_run_stream(off.h, 0, ork.tasks(ork.TaskI4, [(w, 1, A, Cb)])) == -2
+    assert L.ork_f16_mm_run_stream(off.h, 0, ork.tasks(ork.TaskF16, [(w, 1, A, Cb)])) == -2
+    ork.free(w)
+
+
 def test_accessors_null_safe():
     L = ork.lib()
     K = C.c_int(5)
