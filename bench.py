@@ -297,7 +297,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the sweep over BASELINE configs 1-4")
-    ap.add_argument("--only", choices=["gemv", "m512"], help="profiling: time only one of the two kernels")
+    ap.add_argument("--only", choices=["gemv", "m512", "chain"], help="profiling: time only one kernel")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling: run device-to-device copies of one weight's bytes (a plain copy kernel of "
                          "known size) instead of the bench, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -340,7 +340,13 @@ def main():
               f"M=512 {gemm_plan}", file=sys.stderr, flush=True)
 
         g1 = e1 = g512 = e512 = float("nan")
-        if args.only != "m512":
+        if args.only == "chain":
+            ms = measure_chain(npu, hip, L, ws, dA, dC, 8, 300)
+            print(f"[bench] chain of 8: {ms * 1e3:.2f} us/call", file=sys.stderr, flush=True)
+            for w in ws:
+                ork.lib().ork_mm_free(npu.h, w)
+            return
+        if args.only not in ("m512",):
             g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup)
             print(f"[bench] M=1: graph {g1 * 1e3:.2f} us/step, eager {e1 * 1e3:.2f} us/step", file=sys.stderr, flush=True)
         if args.only != "gemv":
@@ -420,7 +426,7 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_i8_m1")},
         "eager_value": round(algo_bytes(1) / (e1 * 1e-3) / 1e9, 1),
         "chain8": {"value": round(chain_gbs, 1), "unit": "GB/s", "us_per_call": round(chain_ms * 1e3, 3),
-                   "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
+                   "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("chain8_i8_m1"),
                    "note": "ork_i8_mm_run_chain: 8 M=1 GEMVs of the same shape (distinct resident weights) per call, "
                            "one grouped launch; A and C in HBM; HIP graph of 300 calls"},
         "host_api": {"value": round(algo_bytes(1) / (host_us * 1e-6) / 1e9, 1), "unit": "GB/s",
