@@ -1,0 +1,488 @@
+// q3_ops.hip -- the non-matmul operators of the Qwen3-shaped decoder harness, for gfx950.
+//
+// The reference runs these on the host CPU between NPU matmuls (examples/bench.c:74-78 rmsnorm / rope /
+// silu, :83-90 the int8 activation round trip, :115-127 flash-style GQA attention; examples/layer.c:21-30,
+// examples/decode.c:21-26; the per-row activation quantisation of examples/quant.c:34-37). Here they are
+// small fused kernels on the library's stream, so activations never leave HBM between the matmuls:
+//   k_norm_quant      [embedding lookup | residual add of a matmul result] + RMSNorm + per-row int8 quant
+//   k_qkv_post        q/k/v dequant + per-head RMSNorm (Qwen3 q_norm / k_norm) + RoPE + KV-cache append
+//   k_attn_part       causal GQA attention over one 64-key chunk: running max, sum and P.V per query head
+//   k_attn_quant      combine the chunks (log-sum-exp) + per-row int8 quant of the attention output
+//   k_swiglu_quant    gate/up dequant + silu(g) * u + per-row int8 quant
+//   k_argmax          greedy sampling: dequantised logits -> one 64-bit atomic max per workgroup
+// Decode reads its position and its input token from device memory (st[], best), so one captured HIP
+// graph per decode step replays unchanged. Compiled with -ffp-contract=off: every product and sum is
+// rounded as the reference's C code rounds it (no fused multiply-add).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "q3_ops.h"
+
+namespace {
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+// Block-wide sum / max (blockDim a multiple of 64, at most 1024). red[] holds 16 floats. The result
+// reaches every thread; the waves' partials are added in wave order.
+__device__ inline float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += red[i];
+    return s;
+}
+__device__ inline float block_max(float v, float *red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) m = fmaxf(m, red[i]);
+    return m;
+}
+
+// Rows live in registers: thread i holds elements i, i + blockDim, ... (E of them, E a compile-time
+// bound), so every global load of a row is issued before the first arithmetic that needs it.
+template <int E, typename T>
+__device__ inline void load_row(T (&v)[E], const T *__restrict__ src, int n) {
+#pragma unroll
+    for (int k = 0; k < E; k++) {
+        const int i = threadIdx.x + k * blockDim.x;
+        v[k] = i < n ? src[i] : T(0);
+    }
+}
+
+// Per-row symmetric int8 (examples/quant.c:34-37): s = max|x| / 127 (1 when the row is zero),
+// q = clamp(rint(x / s), -127, 127). x * (1/s) is within 2 ulp of the correctly rounded x / s, so it
+// rounds to the same integer unless it lies within 1e-4 of a half-way point (|x / s| <= 127.5, where
+// 2 ulp < 1.6e-5); there the exact quotient decides.
+template <int E>
+__device__ inline void quant_regs(const float (&y)[E], int n, int8_t *__restrict__ q, float *s_out, float *red) {
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < E; k++)
+        if (threadIdx.x + k * blockDim.x < (unsigned)n) mx = fmaxf(mx, fabsf(y[k]));
+    mx = block_max(mx, red);
+    const float s = mx > 0.f ? mx / 127.0f : 1.0f;
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < E; k++) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < n) {
+            float r = y[k] * inv;
+            if (fabsf(r - floorf(r) - 0.5f) < 1e-4f) r = y[k] / s;
+            r = fminf(fmaxf(rintf(r), -127.f), 127.f);
+            q[i] = (int8_t)(int)r;
+        }
+    }
+    if (threadIdx.x == 0) *s_out = s;
+}
+
+// Token of a greedy-sampling key (see k_argmax): low 32 bits hold ~index.
+__device__ inline int key_token(unsigned long long k) { return (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)); }
+
+template <int E>
+__global__ __launch_bounds__(512) void k_norm_quant(q3_nq p) {
+    __shared__ float red[16];
+    const int t = blockIdx.x, H = p.H;
+    float *__restrict__ xr = p.x + (size_t)t * H;
+    float v[E], nw[E];
+    int tok = 0;
+    if (p.emb) {
+        tok = p.tok ? p.tok[t] : key_token(*p.best);
+        if (tok < 0 || tok >= p.V) tok = 0; // an unset key; the host validates tokens it uploads
+        const __half *__restrict__ e = p.emb + (size_t)tok * H;
+#pragma unroll
+        for (int k = 0; k < E; k++) {
+            const int i = threadIdx.x + k * blockDim.x;
+            v[k] = i < H ? __half2float(e[i]) : 0.f;
+        }
+    } else {
+        load_row(v, (const float *)xr, H);
+    }
+    if (p.acc) { // residual add of the previous projection: x += (c * a_scale) * w_scale
+        int32_t c[E];
+        float w[E];
+        load_row(c, p.acc + (size_t)t * H, H);
+        load_row(w, p.acc_ws, H);
+        const float as = p.acc_as[t];
+#pragma unroll
+        for (int k = 0; k < E; k++) v[k] = v[k] + ((float)c[k] * as) * w[k];
+    }
+    load_row(nw, p.nw, H);
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < E; k++) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < H) xr[i] = v[k];
+        ss += v[k] * v[k];
+    }
+    ss = block_sum(ss, red); // its barriers also order every read of *best before the clear below
+    if (p.emb && threadIdx.x == 0) {
+        if (p.tok) {
+            p.toks[p.st[0] + t] = tok;
+            if (t == 0 && p.best) *p.best = 0ull;
+        } else { // decode: this row is the next position
+            const int pos = p.st[1];
+            p.toks[pos] = tok;
+            p.st[0] = pos;
+            p.st[1] = pos + 1;
+            *p.best = 0ull;
+        }
+    }
+    const float r = 1.0f / sqrtf(ss / (float)H + p.eps);
+#pragma unroll
+    for (int k = 0; k < E; k++) v[k] = (v[k] * r) * nw[k];
+    quant_regs(v, H, p.a8 + (size_t)t * H, p.as + t, red);
+}
+
+__global__ __launch_bounds__(256) void k_qkv_post(q3_qkv p) {
+    __shared__ float v[Q3_MAX_HD];
+    __shared__ float red[16];
+    const int HD = p.HD, half = HD >> 1, d = threadIdx.x;
+    const int h = blockIdx.x, t = blockIdx.y;
+    const int QD = p.NH * HD, KVD = p.NKV * HD;
+    const int pos = p.st[0] + t;
+    if (pos >= p.max_ctx) return; // the host refuses such a step; never write past the cache
+    const bool kv = h >= p.NH;
+    const int g = h - p.NH;
+    const int32_t *__restrict__ c = kv ? p.ck + (size_t)t * KVD + g * HD : p.cq + (size_t)t * QD + h * HD;
+    const float *__restrict__ ws = kv ? p.wsk + g * HD : p.wsq + h * HD;
+    const float *__restrict__ nw = kv ? p.kn : p.qn;
+    // every load first
+    const int i = d < half ? d : d - half;
+    const int32_t cd = c[d];
+    const float wd = ws[d], nwd = nw[d], as = p.as[t];
+    const float cs = p.rcos[(size_t)pos * half + i], sn = p.rsin[(size_t)pos * half + i];
+    int32_t cvd = 0;
+    float wvd = 0.f;
+    if (kv) {
+        cvd = p.cv[(size_t)t * KVD + g * HD + d];
+        wvd = p.wsv[g * HD + d];
+    }
+    const float x = ((float)cd * as) * wd;
+    const float ss = block_sum(x * x, red);
+    const float r = 1.0f / sqrtf(ss / (float)HD + p.eps);
+    v[d] = (x * r) * nwd;
+    __syncthreads();
+    // NeoX rotate-halves (examples/bench.c:76): pairs (i, i + HD/2) at angle pos * theta^(-2i/HD)
+    const float a = v[i], b = v[i + half];
+    const float o = d < half ? a * cs - b * sn : a * sn + b * cs;
+    if (kv) {
+        p.kc[(size_t)pos * KVD + g * HD + d] = o;
+        p.vc[(size_t)pos * KVD + g * HD + d] = ((float)cvd * as) * wvd;
+    } else {
+        p.q[(size_t)t * QD + h * HD + d] = o;
+    }
+}
+
+// One workgroup per (kv head, sub-group of GW query heads, 64-key chunk, query row), GW * HD <= 256
+// threads: thread (g, d) = query head g of the sub-group, dimension d. Every global load is issued up
+// front and unconditionally (rows past the chunk's last key repeat that key; their probabilities are
+// zero): the chunk's K rows go to LDS as float4, each thread's V column stays in registers. Wave g scores
+// head g's keys one per lane, so the chunk's softmax statistics are two wave reductions.
+template <int GW>
+__global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
+    extern __shared__ float sm[];
+    const int HD = p.HD, G = p.NH / p.NKV, KVD = p.NKV * HD, QD = p.NH * HD;
+    const int nsub = G / GW;
+    const int kvh = blockIdx.x / nsub, h0 = kvh * G + (blockIdx.x - kvh * nsub) * GW; // first query head
+    const int s = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+    const int g = tid / HD, d = tid - g * HD;
+    const int L = min(p.st[0] + t + 1, p.max_ctx); // causal: keys 0 .. pos (never past the cache)
+    const int j0 = s * Q3_CHUNK;
+    const int n = min(Q3_CHUNK, L - j0);
+    float *out = p.part + (((size_t)t * p.NH + h0 + g) * p.S + s) * (HD + 2);
+    if (n <= 0) { // whole workgroup: this chunk is beyond the row's keys
+        out[d] = 0.f;
+        if (d == 0) {
+            out[HD] = -INFINITY;
+            out[HD + 1] = 0.f;
+        }
+        return;
+    }
+    const int KS = HD + 4; // LDS row stride: 16-byte rows, 8 consecutive lanes of a float4 read hit distinct banks
+    float *Ks = sm;
+    float *qs = Ks + Q3_CHUNK * KS;
+    float *P = qs + GW * HD;
+    float *ml = P + GW * Q3_CHUNK; // [GW][2]: max, sum
+    const float *__restrict__ kb = p.kc + (size_t)j0 * KVD + kvh * HD;
+    const float *__restrict__ vb = p.vc + (size_t)j0 * KVD + kvh * HD + d;
+    float vv[Q3_CHUNK];
+#pragma unroll
+    for (int j = 0; j < Q3_CHUNK; j++) vv[j] = vb[(size_t)min(j, n - 1) * KVD];
+    // the chunk's Q3_CHUNK * HD / 4 float4s are exactly Q3_CHUNK / 4 / GW per thread (blockDim = GW * HD)
+    const int HD4 = HD >> 2;
+    constexpr int KR = Q3_CHUNK / 4 / GW;
+    float4 kreg[KR];
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int f = tid + k * blockDim.x, j = f / HD4, c4 = f - j * HD4;
+        kreg[k] = *(const float4 *)(kb + (size_t)min(j, n - 1) * KVD + 4 * c4);
+    }
+    qs[tid] = p.q[(size_t)t * QD + h0 * HD + tid];
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int f = tid + k * blockDim.x, j = f / HD4, c4 = f - j * HD4;
+        *(float4 *)(Ks + j * KS + 4 * c4) = kreg[k];
+    }
+    __syncthreads();
+    if (tid < GW * Q3_CHUNK) {
+        const int gg = tid >> 6, j = tid & 63;
+        const float4 *qr = (const float4 *)(qs + gg * HD), *kr = (const float4 *)(Ks + j * KS);
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        for (int e = 0; e < HD4; e++) {
+            const float4 qv = qr[e], kv = kr[e];
+            a0 += qv.x * kv.x;
+            a1 += qv.y * kv.y;
+            a2 += qv.z * kv.z;
+            a3 += qv.w * kv.w;
+        }
+        const float sc = j < n ? ((a0 + a1) + (a2 + a3)) * p.scale : -INFINITY;
+        const float m = wave_max(sc);
+        const float pj = j < n ? expf(sc - m) : 0.f;
+        const float l = wave_sum(pj);
+        P[gg * Q3_CHUNK + j] = pj;
+        if (j == 0) {
+            ml[2 * gg] = m;
+            ml[2 * gg + 1] = l;
+        }
+    }
+    __syncthreads();
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < Q3_CHUNK; j++) acc += P[g * Q3_CHUNK + j] * vv[j];
+    out[d] = acc;
+    if (d == 0) {
+        out[HD] = ml[2 * g];
+        out[HD + 1] = ml[2 * g + 1];
+    }
+}
+
+// Combine the chunks of every head (log-sum-exp weights), then quantise the row.
+template <int E>
+__global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
+    extern __shared__ float sm[];
+    __shared__ float red[16];
+    const int HD = p.HD, NH = p.NH, S = p.S, QD = NH * HD, t = blockIdx.x;
+    const float *__restrict__ part = p.part + (size_t)t * NH * S * (HD + 2);
+    float *w = sm, *ls = sm + NH * S, *inv = ls + NH * S;
+    for (int i = threadIdx.x; i < NH * S; i += blockDim.x) {
+        w[i] = part[(size_t)i * (HD + 2) + HD];
+        ls[i] = part[(size_t)i * (HD + 2) + HD + 1];
+    }
+    __syncthreads();
+    for (int h = threadIdx.x; h < NH; h += blockDim.x) {
+        float mx = -INFINITY;
+        for (int s = 0; s < S; s++) mx = fmaxf(mx, w[h * S + s]);
+        float den = 0.f;
+        for (int s = 0; s < S; s++) {
+            const float m = w[h * S + s];
+            const float e = m == -INFINITY ? 0.f : expf(m - mx);
+            w[h * S + s] = e;
+            den += ls[h * S + s] * e;
+        }
+        inv[h] = den > 0.f ? 1.0f / den : 0.f;
+    }
+    __syncthreads();
+    float y[E];
+#pragma unroll
+    for (int k = 0; k < E; k++) {
+        const int i = threadIdx.x + k * blockDim.x;
+        float num = 0.f;
+        if (i < QD) {
+            const int h = i / HD, d = i - h * HD;
+            const float *ph = part + (size_t)h * S * (HD + 2) + d;
+#pragma unroll 8
+            for (int s = 0; s < S; s++) num += ph[(size_t)s * (HD + 2)] * w[h * S + s];
+            num = num * inv[h];
+        }
+        y[k] = num;
+    }
+    quant_regs(y, QD, p.a8 + (size_t)t * QD, p.as + t, red);
+}
+
+template <int E>
+__global__ __launch_bounds__(1024) void k_swiglu_quant(q3_glu p) {
+    __shared__ float red[16];
+    const int F = p.F, t = blockIdx.x;
+    int32_t cg[E], cu[E];
+    float wg[E], wu[E], y[E];
+    load_row(cg, p.cg + (size_t)t * F, F);
+    load_row(cu, p.cu + (size_t)t * F, F);
+    load_row(wg, p.wsg, F);
+    load_row(wu, p.wsu, F);
+    const float as = p.as_in[t];
+#pragma unroll
+    for (int k = 0; k < E; k++) {
+        const float gv = ((float)cg[k] * as) * wg[k];
+        const float uv = ((float)cu[k] * as) * wu[k];
+        y[k] = (gv / (1.0f + expf(-gv))) * uv;
+    }
+    quant_regs(y, F, p.a8 + (size_t)t * F, p.as_out + t, red);
+}
+
+// Order-preserving map of a float to 32 bits (larger float -> larger unsigned).
+__device__ inline unsigned ord_bits(float v) {
+    const unsigned u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__global__ void k_argmax(q3_amax p) {
+    __shared__ unsigned long long red[16];
+    const float as = *p.as;
+    unsigned long long best = 0ull;
+    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < p.V; n += gridDim.x * blockDim.x) {
+        const float v = ((float)p.c[n] * as) * p.ws[n];
+        // ties resolve to the smaller index (the first maximum), as a sequential scan does
+        const unsigned long long k = ((unsigned long long)ord_bits(v) << 32) | (0xFFFFFFFFu - (unsigned)n);
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long x = __shfl_xor(best, o, 64);
+        best = x > best ? x : best;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < (int)(blockDim.x >> 6); i++) best = red[i] > best ? red[i] : best;
+        atomicMax(p.best, best);
+    }
+}
+
+inline int launch_ok() { return hipGetLastError() == hipSuccess ? 0 : -1; }
+
+} // namespace
+
+extern "C" {
+
+// Register-row templates: E elements per thread, the smallest power of two that covers the row.
+#define Q3_ROW_DISPATCH(KERNEL, THREADS, N, GRID, LDS, STREAM, ARG)                                           \
+    do {                                                                                                      \
+        const int e_ = ((N) + (THREADS)-1) / (THREADS);                                                       \
+        if (e_ <= 1) hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(THREADS), LDS, STREAM, ARG);                     \
+        else if (e_ <= 2) hipLaunchKernelGGL(KERNEL<2>, GRID, dim3(THREADS), LDS, STREAM, ARG);                \
+        else if (e_ <= 4) hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(THREADS), LDS, STREAM, ARG);                \
+        else if (e_ <= 8) hipLaunchKernelGGL(KERNEL<8>, GRID, dim3(THREADS), LDS, STREAM, ARG);                \
+        else if (e_ <= 16) hipLaunchKernelGGL(KERNEL<16>, GRID, dim3(THREADS), LDS, STREAM, ARG);              \
+        else return -2;                                                                                       \
+    } while (0)
+
+int q3k_norm_quant(const q3_nq *p, void *stream) {
+    if (p->M < 1 || p->H < 64 || p->H > 512 * 16 || (p->emb && !p->tok && p->M != 1)) return -2;
+    Q3_ROW_DISPATCH(k_norm_quant, 512, p->H, dim3(p->M), 0, (hipStream_t)stream, *p);
+    return launch_ok();
+}
+
+int q3k_qkv_post(const q3_qkv *p, void *stream) {
+    if (p->M < 1 || p->HD < 64 || p->HD > Q3_MAX_HD || p->HD % 64) return -2;
+    hipLaunchKernelGGL(k_qkv_post, dim3(p->NH + p->NKV, p->M), dim3(p->HD), 0, (hipStream_t)stream, *p);
+    return launch_ok();
+}
+
+int q3k_attn_part(const q3_att *p, void *stream) {
+    const int G = p->NKV > 0 ? p->NH / p->NKV : 0;
+    if (p->M < 1 || G < 1 || G * p->NKV != p->NH || p->HD % 64 || p->HD > Q3_MAX_HD || p->HD < Q3_CHUNK ||
+        p->S < 1 || (long)p->S * Q3_CHUNK < p->max_ctx)
+        return -2;
+    int GW = 256 / p->HD; // query heads per workgroup: the largest divisor of G with GW * HD <= 256
+    if (GW > G) GW = G;
+    while (G % GW) GW--;
+    const size_t lds = Q3_ATT_LDS(GW, p->HD);
+    if (lds > 64 * 1024) return -2;
+    const dim3 grid(p->NKV * (G / GW), p->S, p->M), block(GW * p->HD);
+    if (GW == 1) hipLaunchKernelGGL(k_attn_part<1>, grid, block, lds, (hipStream_t)stream, *p);
+    else if (GW == 2) hipLaunchKernelGGL(k_attn_part<2>, grid, block, lds, (hipStream_t)stream, *p);
+    else if (GW == 4) hipLaunchKernelGGL(k_attn_part<4>, grid, block, lds, (hipStream_t)stream, *p);
+    else return -2;
+    return launch_ok();
+}
+
+int q3k_attn_quant(const q3_aq *p, void *stream) {
+    const size_t lds = (size_t)(2 * p->NH * p->S + p->NH) * sizeof(float);
+    if (p->M < 1 || p->NH * p->HD > 1024 * 16 || lds > 32 * 1024) return -2;
+    Q3_ROW_DISPATCH(k_attn_quant, 1024, p->NH * p->HD, dim3(p->M), lds, (hipStream_t)stream, *p);
+    return launch_ok();
+}
+
+int q3k_swiglu_quant(const q3_glu *p, void *stream) {
+    if (p->M < 1 || p->F > 1024 * 16) return -2;
+    Q3_ROW_DISPATCH(k_swiglu_quant, 1024, p->F, dim3(p->M), 0, (hipStream_t)stream, *p);
+    return launch_ok();
+}
+
+int q3k_argmax(const q3_amax *p, void *stream) {
+    if (p->V < 1) return -2;
+    int grid = (p->V + 1023) / 1024;
+    if (grid > 512) grid = 512;
+    hipLaunchKernelGGL(k_argmax, dim3(grid), dim3(256), 0, (hipStream_t)stream, *p);
+    return launch_ok();
+}
+
+// ---- HIP graphs for the decode step ----------------------------------------------------------------------
+int q3g_begin(void *stream) {
+    return hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal) == hipSuccess ? 0 : -1;
+}
+
+int q3g_end(void *stream, void **exec) {
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture((hipStream_t)stream, &g) != hipSuccess || !g) return -1;
+    hipGraphExec_t e = nullptr;
+    const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (rc != hipSuccess) return -1;
+    *exec = e;
+    return 0;
+}
+
+int q3g_launch(void *exec, void *stream) {
+    return hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream) == hipSuccess ? 0 : -1;
+}
+
+void q3g_destroy(void *exec) {
+    if (exec) (void)hipGraphExecDestroy((hipGraphExec_t)exec);
+}
+
+int q3g_sync(void *stream) { return hipStreamSynchronize((hipStream_t)stream) == hipSuccess ? 0 : -1; }
+
+// Event-timed region on the stream: q3t_begin records a start event, q3t_end a stop event, waits for it
+// and returns the elapsed milliseconds (negative on error).
+int q3t_begin(void *stream, void **ev) {
+    hipEvent_t e[2];
+    if (hipEventCreate(&e[0]) != hipSuccess) return -1;
+    if (hipEventCreate(&e[1]) != hipSuccess) { (void)hipEventDestroy(e[0]); return -1; }
+    if (hipEventRecord(e[0], (hipStream_t)stream) != hipSuccess) {
+        (void)hipEventDestroy(e[0]);
+        (void)hipEventDestroy(e[1]);
+        return -1;
+    }
+    ev[0] = e[0];
+    ev[1] = e[1];
+    return 0;
+}
+
+double q3t_end(void *stream, void **ev) {
+    hipEvent_t e0 = (hipEvent_t)ev[0], e1 = (hipEvent_t)ev[1];
+    float ms = -1.f;
+    if (hipEventRecord(e1, (hipStream_t)stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+        ms = -1.f;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return ms;
+}
+
+} // extern "C"
