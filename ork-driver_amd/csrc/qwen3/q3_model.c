@@ -161,7 +161,7 @@ static int lin_dims(const q3_cfg *c, int layer, int which, int *K, int *N) {
 static int cfg_ok(const q3_cfg *c) {
     if (!c || c->layers < 1 || c->hidden < 64 || c->heads < 1 || c->kv_heads < 1 || c->heads % c->kv_heads ||
         c->head_dim < Q3_CHUNK || c->head_dim > Q3_MAX_HD || c->head_dim % 64 || c->ffn < 32 || c->vocab < 32 ||
-        c->max_ctx < 1 || c->max_rows < 1 || c->max_rows > c->max_ctx)
+        c->max_ctx < 1 || c->max_ctx > Q3_MAX_S * Q3_CHUNK || c->max_rows < 1 || c->max_rows > c->max_ctx)
         return 0;
     if (Q3_ATT_LDS(256 / c->head_dim, c->head_dim) > 65536) return 0;
     /* the matmul API's dimension rules: K % 32, N % 32 */
@@ -416,11 +416,27 @@ static int pass(q3_model *m, int M, int decode) {
                                  {Ly->l[Q3_WK].w, M, m->a8x, m->ck, 0},
                                  {Ly->l[Q3_WV].w, M, m->a8x, m->cv, 0}};
         CK(ork_i8_mm_run_chain(m->ctx, 3, qkv));
-        const q3_qkv qp = {M, NH, NKV, HD, c->max_ctx, m->cq, m->ck, m->cv, m->asx,
-                           Ly->l[Q3_WQ].ws, Ly->l[Q3_WK].ws, Ly->l[Q3_WV].ws, Ly->qn, Ly->kn, c->eps,
-                           m->rcos, m->rsin, m->st, m->q, Ly->kc, Ly->vc};
-        CK(q3k_qkv_post(&qp, s));
-        const q3_att at = {M, NH, NKV, HD, m->S, c->max_ctx, m->q, Ly->kc, Ly->vc, m->st, 1.0f / sqrtf((float)HD), m->part};
+        q3_att at = {.M = M, .NH = NH, .NKV = NKV, .HD = HD, .S = m->S, .max_ctx = c->max_ctx, .q = m->q,
+                     .kc = Ly->kc, .vc = Ly->vc, .st = m->st, .scale = 1.0f / sqrtf((float)HD), .part = m->part};
+        if (M == 1) { /* one row: attention does the q/k/v post-processing itself */
+            at.cq = m->cq;
+            at.ck = m->ck;
+            at.cv = m->cv;
+            at.as = m->asx;
+            at.wsq = Ly->l[Q3_WQ].ws;
+            at.wsk = Ly->l[Q3_WK].ws;
+            at.wsv = Ly->l[Q3_WV].ws;
+            at.qn = Ly->qn;
+            at.kn = Ly->kn;
+            at.eps = c->eps;
+            at.rcos = m->rcos;
+            at.rsin = m->rsin;
+        } else {
+            const q3_qkv qp = {M, NH, NKV, HD, c->max_ctx, m->cq, m->ck, m->cv, m->asx,
+                               Ly->l[Q3_WQ].ws, Ly->l[Q3_WK].ws, Ly->l[Q3_WV].ws, Ly->qn, Ly->kn, c->eps,
+                               m->rcos, m->rsin, m->st, m->q, Ly->kc, Ly->vc};
+            CK(q3k_qkv_post(&qp, s));
+        }
         CK(q3k_attn_part(&at, s));
         const q3_aq aq = {M, NH, HD, m->S, m->part, m->a8att, m->asatt};
         CK(q3k_attn_quant(&aq, s));

@@ -18,6 +18,7 @@ typedef uint16_t q3_half;
 
 #define Q3_CHUNK 64   /* keys per attention workgroup */
 #define Q3_MAX_HD 256 /* head_dim bound of k_qkv_post / k_attn_part */
+#define Q3_MAX_S 16   /* key chunks per row: max_ctx <= 1024 */
 
 /* st[] decode state: st[0] position of row 0 of the current pass, st[1] next free position.
  * best: greedy-sampling key, (order-preserving bits of the logit << 32) | (0xFFFFFFFF - token). */
@@ -54,11 +55,16 @@ typedef struct q3_qkv { /* q/k/v dequant -> per-head RMSNorm -> RoPE -> q rows, 
 
 typedef struct q3_att { /* grid (NKV * query-head sub-groups, S, M): 64-key chunk partials */
     int M, NH, NKV, HD, S, max_ctx;
-    const float *q;
-    const float *kc, *vc;
+    const float *q; /* [M][NH*HD] rotated queries (unfused) */
+    float *kc, *vc; /* this layer's cache; the fused form appends the new row */
     const int *st;
     float scale;
     float *part; /* [M][NH][S][HD + 2]: P.V, then max and sum */
+    /* fused form (M = 1, cq != NULL): the q/k/v matmul results and what k_qkv_post takes */
+    const int32_t *cq, *ck, *cv;
+    const float *as, *wsq, *wsk, *wsv, *qn, *kn;
+    float eps;
+    const float *rcos, *rsin;
 } q3_att;
 
 typedef struct q3_aq { /* chunk combine -> int8 rows */
@@ -86,7 +92,7 @@ typedef struct q3_amax { /* greedy sampling over one row of logits */
 } q3_amax;
 
 /* LDS bytes of k_attn_part for a workgroup of G query heads (launches above 64 KiB are refused). */
-#define Q3_ATT_LDS(G, HD) ((size_t)(Q3_CHUNK * ((HD) + 4) + (G) * (HD) + (G) * Q3_CHUNK + 2 * (G)) * 4)
+#define Q3_ATT_LDS(G, HD) ((size_t)(Q3_CHUNK * ((HD) + 4) + 2 * (G) * (HD) + (G) * Q3_CHUNK + 2 * (G) + 2 * (HD)) * 4)
 
 int q3k_norm_quant(const q3_nq *p, void *stream);
 int q3k_qkv_post(const q3_qkv *p, void *stream);

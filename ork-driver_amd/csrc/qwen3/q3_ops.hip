@@ -193,15 +193,21 @@ __global__ __launch_bounds__(256) void k_qkv_post(q3_qkv p) {
 // front and unconditionally (rows past the chunk's last key repeat that key; their probabilities are
 // zero): the chunk's K rows go to LDS as float4, each thread's V column stays in registers. Wave g scores
 // head g's keys one per lane, so the chunk's softmax statistics are two wave reductions.
-template <int GW>
+// FUSED (one query row, decode): the workgroup also does k_qkv_post's work for itself -- dequantises,
+// normalises and rotates its query heads from the q/k/v matmul results, and the workgroup whose chunk
+// holds the current position builds that position's K/V row (appending it to the cache) -- which saves
+// a launch and a round trip through HBM per layer.
+template <int GW, bool FUSED>
 __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
     extern __shared__ float sm[];
-    const int HD = p.HD, G = p.NH / p.NKV, KVD = p.NKV * HD, QD = p.NH * HD;
-    const int nsub = G / GW;
-    const int kvh = blockIdx.x / nsub, h0 = kvh * G + (blockIdx.x - kvh * nsub) * GW; // first query head
+    __shared__ float red[32];
+    const int HD = p.HD, half = HD >> 1, G = p.NH / p.NKV, KVD = p.NKV * HD, QD = p.NH * HD;
+    const int nsub = G / GW, sub = blockIdx.x % nsub;
+    const int kvh = blockIdx.x / nsub, h0 = kvh * G + sub * GW; // first query head
     const int s = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int g = tid / HD, d = tid - g * HD;
-    const int L = min(p.st[0] + t + 1, p.max_ctx); // causal: keys 0 .. pos (never past the cache)
+    const int pos = p.st[0] + t;
+    const int L = min(pos + 1, p.max_ctx); // causal: keys 0 .. pos (never past the cache)
     const int j0 = s * Q3_CHUNK;
     const int n = min(Q3_CHUNK, L - j0);
     float *out = p.part + (((size_t)t * p.NH + h0 + g) * p.S + s) * (HD + 2);
@@ -218,6 +224,7 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
     float *qs = Ks + Q3_CHUNK * KS;
     float *P = qs + GW * HD;
     float *ml = P + GW * Q3_CHUNK; // [GW][2]: max, sum
+    float *xs = ml + 2 * GW;       // FUSED: [GW][HD] normalised q, then [HD] k and [HD] v of the new row
     const float *__restrict__ kb = p.kc + (size_t)j0 * KVD + kvh * HD;
     const float *__restrict__ vb = p.vc + (size_t)j0 * KVD + kvh * HD + d;
     float vv[Q3_CHUNK];
@@ -232,11 +239,70 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
         const int f = tid + k * blockDim.x, j = f / HD4, c4 = f - j * HD4;
         kreg[k] = *(const float4 *)(kb + (size_t)min(j, n - 1) * KVD + 4 * c4);
     }
-    qs[tid] = p.q[(size_t)t * QD + h0 * HD + tid];
+    const bool own = FUSED && pos - j0 < Q3_CHUNK; // this chunk holds the new row (row n - 1)
+    int32_t cqd = 0, ckd = 0, cvd = 0;
+    float wq = 0.f, wk = 0.f, wv = 0.f, qn = 0.f, kn = 0.f, as = 0.f, cs = 0.f, sn = 0.f;
+    const int ri = d < half ? d : d - half;
+    if (FUSED) {
+        const int h = h0 + g;
+        cqd = p.cq[h * HD + d];
+        wq = p.wsq[h * HD + d];
+        qn = p.qn[d];
+        as = p.as[0];
+        cs = p.rcos[(size_t)pos * half + ri];
+        sn = p.rsin[(size_t)pos * half + ri];
+        if (own) {
+            ckd = p.ck[kvh * HD + d];
+            cvd = p.cv[kvh * HD + d];
+            wk = p.wsk[kvh * HD + d];
+            wv = p.wsv[kvh * HD + d];
+            kn = p.kn[d];
+        }
+    } else {
+        qs[tid] = p.q[(size_t)t * QD + h0 * HD + tid];
+    }
 #pragma unroll
     for (int k = 0; k < KR; k++) {
         const int f = tid + k * blockDim.x, j = f / HD4, c4 = f - j * HD4;
         *(float4 *)(Ks + j * KS + 4 * c4) = kreg[k];
+    }
+    const int jn = n - 1;
+    if (FUSED) {
+        // per-head RMSNorm of q (and of the new k row): sums of squares over head g's HD threads
+        const float xq = ((float)cqd * as) * wq;
+        const float xk = ((float)ckd * as) * wk;
+        const float a = wave_sum(xq * xq), b = wave_sum(xk * xk);
+        const int w = tid >> 6, wph = HD >> 6;
+        if ((tid & 63) == 0) {
+            red[2 * w] = a;
+            red[2 * w + 1] = b;
+        }
+        __syncthreads();
+        float sq = 0.f, sk = 0.f;
+        for (int i = 0; i < wph; i++) {
+            sq += red[2 * (g * wph + i)];
+            sk += red[2 * (g * wph + i) + 1];
+        }
+        const float rq = 1.0f / sqrtf(sq / (float)HD + p.eps);
+        const float rk = 1.0f / sqrtf(sk / (float)HD + p.eps);
+        xs[tid] = (xq * rq) * qn;
+        float *kx = xs + GW * HD, *vx = kx + HD;
+        if (own && g == 0) kx[d] = (xk * rk) * kn;
+        __syncthreads();
+        // NeoX rotate-halves (examples/bench.c:76)
+        const float qa = xs[g * HD + ri], qb = xs[g * HD + ri + half];
+        qs[tid] = d < half ? qa * cs - qb * sn : qa * sn + qb * cs;
+        if (own && g == 0) {
+            const float ka = kx[ri], kbv = kx[ri + half];
+            const float ko = d < half ? ka * cs - kbv * sn : ka * sn + kbv * cs;
+            const float vo = ((float)cvd * as) * wv;
+            Ks[jn * KS + d] = ko;
+            vx[d] = vo;
+            if (sub == 0) { // one workgroup per kv head appends the row
+                p.kc[(size_t)pos * KVD + kvh * HD + d] = ko;
+                p.vc[(size_t)pos * KVD + kvh * HD + d] = vo;
+            }
+        }
     }
     __syncthreads();
     if (tid < GW * Q3_CHUNK) {
@@ -261,9 +327,13 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
         }
     }
     __syncthreads();
+    // in the chunk that holds the new row, rows jn.. of vv were loaded before that row existed (the cache
+    // there is unwritten, possibly not even finite): the new V row replaces jn, zeros the rest
+    const float vnew = own ? xs[GW * HD + HD + d] : 0.f;
     float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < Q3_CHUNK; j++) acc += P[g * Q3_CHUNK + j] * vv[j];
+    for (int j = 0; j < Q3_CHUNK; j++)
+        acc += P[g * Q3_CHUNK + j] * ((own && j >= jn) ? (j == jn ? vnew : 0.f) : vv[j]);
     out[d] = acc;
     if (d == 0) {
         out[HD] = ml[2 * g];
@@ -271,7 +341,8 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
     }
 }
 
-// Combine the chunks of every head (log-sum-exp weights), then quantise the row.
+// Combine the chunks of every head (log-sum-exp weights), then quantise the row. Each thread's partial
+// sums are loaded before the chunk weights are known, so the kernel pays one round trip to memory.
 template <int E>
 __global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
     extern __shared__ float sm[];
@@ -279,6 +350,15 @@ __global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
     const int HD = p.HD, NH = p.NH, S = p.S, QD = NH * HD, t = blockIdx.x;
     const float *__restrict__ part = p.part + (size_t)t * NH * S * (HD + 2);
     float *w = sm, *ls = sm + NH * S, *inv = ls + NH * S;
+    float acc[E][Q3_MAX_S];
+#pragma unroll
+    for (int k = 0; k < E; k++) {
+        const int i = min((int)(threadIdx.x + k * blockDim.x), QD - 1);
+        const int h = i / HD, d = i - h * HD;
+        const float *ph = part + (size_t)h * S * (HD + 2) + d;
+#pragma unroll
+        for (int s = 0; s < Q3_MAX_S; s++) acc[k][s] = s < S ? ph[(size_t)s * (HD + 2)] : 0.f;
+    }
     for (int i = threadIdx.x; i < NH * S; i += blockDim.x) {
         w[i] = part[(size_t)i * (HD + 2) + HD];
         ls[i] = part[(size_t)i * (HD + 2) + HD + 1];
@@ -301,15 +381,12 @@ __global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
 #pragma unroll
     for (int k = 0; k < E; k++) {
         const int i = threadIdx.x + k * blockDim.x;
+        const int h = min(i, QD - 1) / HD;
         float num = 0.f;
-        if (i < QD) {
-            const int h = i / HD, d = i - h * HD;
-            const float *ph = part + (size_t)h * S * (HD + 2) + d;
-#pragma unroll 8
-            for (int s = 0; s < S; s++) num += ph[(size_t)s * (HD + 2)] * w[h * S + s];
-            num = num * inv[h];
-        }
-        y[k] = num;
+#pragma unroll
+        for (int s = 0; s < Q3_MAX_S; s++)
+            if (s < S) num += acc[k][s] * w[h * S + s];
+        y[k] = i < QD ? num * inv[h] : 0.f;
     }
     quant_regs(y, QD, p.a8 + (size_t)t * QD, p.as + t, red);
 }
@@ -369,14 +446,17 @@ inline int launch_ok() { return hipGetLastError() == hipSuccess ? 0 : -1; }
 
 extern "C" {
 
-// Register-row templates: E elements per thread, the smallest power of two that covers the row.
+// Register-row templates: E elements per thread, the smallest instantiated width that covers the row.
 #define Q3_ROW_DISPATCH(KERNEL, THREADS, N, GRID, LDS, STREAM, ARG)                                           \
     do {                                                                                                      \
         const int e_ = ((N) + (THREADS)-1) / (THREADS);                                                       \
         if (e_ <= 1) hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(THREADS), LDS, STREAM, ARG);                     \
         else if (e_ <= 2) hipLaunchKernelGGL(KERNEL<2>, GRID, dim3(THREADS), LDS, STREAM, ARG);                \
+        else if (e_ <= 3) hipLaunchKernelGGL(KERNEL<3>, GRID, dim3(THREADS), LDS, STREAM, ARG);                \
         else if (e_ <= 4) hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(THREADS), LDS, STREAM, ARG);                \
+        else if (e_ <= 6) hipLaunchKernelGGL(KERNEL<6>, GRID, dim3(THREADS), LDS, STREAM, ARG);                \
         else if (e_ <= 8) hipLaunchKernelGGL(KERNEL<8>, GRID, dim3(THREADS), LDS, STREAM, ARG);                \
+        else if (e_ <= 12) hipLaunchKernelGGL(KERNEL<12>, GRID, dim3(THREADS), LDS, STREAM, ARG);              \
         else if (e_ <= 16) hipLaunchKernelGGL(KERNEL<16>, GRID, dim3(THREADS), LDS, STREAM, ARG);              \
         else return -2;                                                                                       \
     } while (0)
@@ -396,7 +476,7 @@ int q3k_qkv_post(const q3_qkv *p, void *stream) {
 int q3k_attn_part(const q3_att *p, void *stream) {
     const int G = p->NKV > 0 ? p->NH / p->NKV : 0;
     if (p->M < 1 || G < 1 || G * p->NKV != p->NH || p->HD % 64 || p->HD > Q3_MAX_HD || p->HD < Q3_CHUNK ||
-        p->S < 1 || (long)p->S * Q3_CHUNK < p->max_ctx)
+        p->S < 1 || (long)p->S * Q3_CHUNK < p->max_ctx || (p->cq && p->M != 1) || (!p->cq && !p->q))
         return -2;
     int GW = 256 / p->HD; // query heads per workgroup: the largest divisor of G with GW * HD <= 256
     if (GW > G) GW = G;
@@ -404,16 +484,26 @@ int q3k_attn_part(const q3_att *p, void *stream) {
     const size_t lds = Q3_ATT_LDS(GW, p->HD);
     if (lds > 64 * 1024) return -2;
     const dim3 grid(p->NKV * (G / GW), p->S, p->M), block(GW * p->HD);
-    if (GW == 1) hipLaunchKernelGGL(k_attn_part<1>, grid, block, lds, (hipStream_t)stream, *p);
-    else if (GW == 2) hipLaunchKernelGGL(k_attn_part<2>, grid, block, lds, (hipStream_t)stream, *p);
-    else if (GW == 4) hipLaunchKernelGGL(k_attn_part<4>, grid, block, lds, (hipStream_t)stream, *p);
-    else return -2;
+    const hipStream_t st = (hipStream_t)stream;
+    const bool fused = p->cq != nullptr;
+    if (GW == 1) {
+        if (fused) hipLaunchKernelGGL((k_attn_part<1, true>), grid, block, lds, st, *p);
+        else hipLaunchKernelGGL((k_attn_part<1, false>), grid, block, lds, st, *p);
+    } else if (GW == 2) {
+        if (fused) hipLaunchKernelGGL((k_attn_part<2, true>), grid, block, lds, st, *p);
+        else hipLaunchKernelGGL((k_attn_part<2, false>), grid, block, lds, st, *p);
+    } else if (GW == 4) {
+        if (fused) hipLaunchKernelGGL((k_attn_part<4, true>), grid, block, lds, st, *p);
+        else hipLaunchKernelGGL((k_attn_part<4, false>), grid, block, lds, st, *p);
+    } else {
+        return -2;
+    }
     return launch_ok();
 }
 
 int q3k_attn_quant(const q3_aq *p, void *stream) {
     const size_t lds = (size_t)(2 * p->NH * p->S + p->NH) * sizeof(float);
-    if (p->M < 1 || p->NH * p->HD > 1024 * 16 || lds > 32 * 1024) return -2;
+    if (p->M < 1 || p->NH * p->HD > 1024 * 16 || p->S > Q3_MAX_S || lds > 32 * 1024) return -2;
     Q3_ROW_DISPATCH(k_attn_quant, 1024, p->NH * p->HD, dim3(p->M), lds, (hipStream_t)stream, *p);
     return launch_ok();
 }
