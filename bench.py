@@ -349,7 +349,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the sweep over BASELINE configs 1-4")
     ap.add_argument("--no-decoder", action="store_true", help="skip BASELINE config 5 (the Qwen3-shaped decoder)")
-    ap.add_argument("--only", choices=["gemv", "m512", "chain"], help="profiling: time only one kernel")
+    ap.add_argument("--only", choices=["gemv", "m512", "chain", "decoder"],
+                    help="profiling: time only one kernel (decoder: only BASELINE config 5, w8a8)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling: run device-to-device copies of one weight's bytes (a plain copy kernel of "
                          "known size) instead of the bench, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -366,6 +367,10 @@ def main():
     hip = Hip()
     if args.copy_calibration:
         copy_calibration(hip, L)
+        return
+    if args.only == "decoder":
+        with ork.Npu() as npu:
+            print(json.dumps(measure_decoder(npu, 0)), flush=True)
         return
     rng = np.random.default_rng(0x6F726B00 + (1 << 8))
     W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)   # f32[N][K]

@@ -37,6 +37,50 @@ const float *ork_w_bscale(const ork_w *w);
 /* reference include/ork/weights.h:240. Host codes [K][N] of an OFFLINE weight; NULL when resident. */
 const int8_t *ork_w_codes(const ork_w *w);
 
+/* Persisted weights (.orkpack). Reference include/ork/weights.h:159-193: every ork_w_dump /
+ * ork_*_w_dump_cpu blob starts with this one-page header and every ork_*_mm_load refuses a blob that
+ * lacks it or whose stamp disagrees with this build. The payload after it is this build's resident
+ * panel layout, so capid names gfx950 and that geometry: packs tiled for another chip are refused. */
+#define ORK_PACK_MAGIC      0x4b50414fu /* "OAPK" */
+#define ORK_PACK_HDR_BYTES  4096u
+typedef struct {
+    uint32_t magic;     /* ORK_PACK_MAGIC */
+    uint32_t fmt;       /* ork_pack_format_version() at dump time */
+    uint32_t capid;     /* identity of the layout's caps: SoC + panel geometry + rule */
+    uint32_t dtype;     /* ORK_DT_* of the packed weight */
+    int32_t  K, N;
+    uint32_t hdr_bytes; /* == ORK_PACK_HDR_BYTES */
+    uint32_t flags;     /* reserved, 0 */
+    char     soc[16];   /* SoC id at dump time, for the diagnostic */
+} ork_pack_hdr;         /* zero-padded to ORK_PACK_HDR_BYTES */
+/* Load refusal causes, reference include/ork/weights.h:189-193 (loaders return NULL and log the cause). */
+#define ORK_PACKERR_SHORT     (-1) /* blob smaller than the header */
+#define ORK_PACKERR_UNSTAMPED (-2) /* no magic */
+#define ORK_PACKERR_FORMAT    (-3) /* different pack format */
+#define ORK_PACKERR_CAPS      (-4) /* built for other caps (another chip's tile layout) */
+#define ORK_PACKERR_SHAPE     (-5) /* header disagrees with the requested dtype/K/N */
+/* reference include/ork/weights.h:194 */
+size_t       ork_pack_hdr_bytes(void);
+/* reference include/ork/weights.h:198. Header + the resident panels (int8 / fp16 / W4A4 nibbles; an i4a8
+ * weight dumps the int8 codes it multiplies with, dtype I8). out=NULL -> size; 0 if cap is too small. */
+size_t       ork_w_dump(const ork_w *w, void *out, size_t cap);
+/* reference include/ork/weights.h:203. The bytes of ork_i8_mm_pack + ork_w_dump, tiled on the host. K%32, N%32. */
+size_t       ork_i8_w_dump_cpu(ork_npu *ctx, int K, int N, const int8_t *B, void *out, size_t cap);
+/* reference include/ork/weights.h:206. 0: the panel layout has no separate full-K copy to persist. */
+size_t       ork_i8_w_dump_bf_cpu(ork_npu *ctx, int K, int N, const int8_t *B, void *out, size_t cap);
+/* reference include/ork/weights.h:212. W4A4 twin of ork_i8_w_dump_cpu. K%32, N%64. */
+size_t       ork_i4_w_dump_cpu(ork_npu *ctx, int K, int N, const int8_t *B, void *out, size_t cap);
+/* reference include/ork/weights.h:219, :222, :265. NULL on a refused
+ * header or a payload of the wrong size. On an offline context the int8 / W4A4 loaders recover the codes
+ * (ork_w_codes); fp16 needs a device. */
+ork_w       *ork_f16_mm_load(ork_npu *ctx, int K, int N, const void *blob, size_t n);
+ork_w       *ork_i8_mm_load(ork_npu *ctx, int K, int N, const void *blob, size_t n);
+ork_w       *ork_i4_mm_load(ork_npu *ctx, int K, int N, const void *blob, size_t n);
+/* reference include/ork/weights.h:220, :17. NULL: no dma-buf import in this build
+ * (the reference's "import unavailable"; callers fall back to the plain loader). */
+ork_w       *ork_f16_mm_load_import(ork_npu *ctx, int K, int N, const void *blob, size_t n);
+ork_w       *ork_i8_mm_load_import(ork_npu *ctx, int K, int N, const void *blob, size_t n);
+
 /* reference include/ork/weights.h:230. O4N1 blob: {u32 'O4N1', u32 version, i32 K, i32 N,
  * u32 quant_kind} + f32 bscale[N] + nibbles[N][K/2] (low nibble = even k). out=NULL -> size;
  * 0 if cap is too small or w has no int4 store. */

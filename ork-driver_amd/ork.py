@@ -44,6 +44,16 @@ API = {
     "ork_w_bscale": (_P, [_P]),
     "ork_w_codes": (_P, [_P]),
     "ork_i4a8_w_dump": (C.c_size_t, [_P, _P, C.c_size_t]),
+    "ork_pack_hdr_bytes": (C.c_size_t, []),
+    "ork_w_dump": (C.c_size_t, [_P, _P, C.c_size_t]),
+    "ork_i8_w_dump_cpu": (C.c_size_t, [_P, C.c_int, C.c_int, _P, _P, C.c_size_t]),
+    "ork_i8_w_dump_bf_cpu": (C.c_size_t, [_P, C.c_int, C.c_int, _P, _P, C.c_size_t]),
+    "ork_i4_w_dump_cpu": (C.c_size_t, [_P, C.c_int, C.c_int, _P, _P, C.c_size_t]),
+    "ork_i8_mm_load": (_P, [_P, C.c_int, C.c_int, _P, C.c_size_t]),
+    "ork_i4_mm_load": (_P, [_P, C.c_int, C.c_int, _P, C.c_size_t]),
+    "ork_f16_mm_load": (_P, [_P, C.c_int, C.c_int, _P, C.c_size_t]),
+    "ork_i8_mm_load_import": (_P, [_P, C.c_int, C.c_int, _P, C.c_size_t]),
+    "ork_f16_mm_load_import": (_P, [_P, C.c_int, C.c_int, _P, C.c_size_t]),
     "ork_i4a8_mm_load": (_P, [_P, C.c_int, C.c_int, _P, C.c_size_t]),
     "ork_i4a8_pack_cpu_blob": (C.c_size_t, [_P, C.c_int, C.c_int, _P, _P, C.c_int, _P, C.c_size_t]),
     "ork_i4a8_pack_cpu_blob_qerr": (C.c_size_t, [_P, C.c_int, C.c_int, _P, _P, C.c_int, _P, C.c_size_t, _P]),
@@ -233,6 +243,30 @@ def dump_i4a8(w):
     out = np.zeros(need, np.uint8)
     got = L.ork_i4a8_w_dump(w, ptr(out), need)
     assert got == need
+    return out
+
+
+def dump(w):
+    """ork_w_dump: the 4 KiB OAPK header + the resident panels, or None."""
+    L = lib()
+    need = L.ork_w_dump(w, None, 0)
+    if not need:
+        return None
+    out = np.zeros(need, np.uint8)
+    assert L.ork_w_dump(w, ptr(out), need) == need
+    return out
+
+
+def dump_cpu(ctx, B_kn, w4a4=False):
+    """ork_i8_w_dump_cpu / ork_i4_w_dump_cpu of B[K][N], or None."""
+    B = np.ascontiguousarray(B_kn, np.int8)
+    K, N = B.shape
+    fn = lib().ork_i4_w_dump_cpu if w4a4 else lib().ork_i8_w_dump_cpu
+    need = fn(ctx, K, N, ptr(B), None, 0)
+    if not need:
+        return None
+    out = np.zeros(need, np.uint8)
+    assert fn(ctx, K, N, ptr(B), ptr(out), need) == need
     return out
 
 
