@@ -23,6 +23,21 @@ ork_w       *ork_i4a8_mm_pack_im(ork_npu *ctx, int K, int N, const float *f32, c
 /* reference include/ork/weights.h:125. W4A4: B[K][N] int4 values [-8,7] in int8 containers. K%32, N%64. */
 ork_w       *ork_i4_mm_pack(ork_npu *ctx, int K, int N, const int8_t *B);
 
+/* Grouped scales. reference include/ork/weights.h:126-128: int4 weights whose scales are per (K-group of
+ * G, channel), for ork_i4_mm_run_grouped. K%32, N%64, G%32, K%G, G <= 10752. */
+ork_w       *ork_i4_mm_pack_grouped(ork_npu *ctx, int K, int N, const int8_t *B, int G);
+/* reference include/ork/weights.h:129-132: set the group size of an int4 or int8 weight (K%G; G <= 0 clears
+ * it). 0, or -1 if w is neither. */
+int          ork_w_set_group(ork_w *w, int G);
+/* reference include/ork/weights.h:231-235: a W4A4 pack (ork_w_dump / ork_i4_w_dump_cpu of an int4 weight)
+ * loaded as an int8-computed weight with group size G (0: none); scales come from the caller. */
+ork_w       *ork_i4a8_mm_load_tiled(ork_npu *c, int K, int N, const void *blob, size_t n, int G);
+/* reference include/ork/weights.h:250-253: C f32[M][N] from int8 A, per-(row, group) aScale[m*(K/G)+g] and
+ * per-(group, channel) bScale[g*N+n]; the int32 partial of each K-group is scaled and summed in ascending g,
+ * bit-identical to the reference's CPU accumulate. G % 32 on the device (else -3). */
+int          ork_i8_mm_run_grouped(ork_npu *c, ork_w *w, int M, const int8_t *A, const float *aScale,
+                                   const float *bScale, float *C);
+
 /* reference include/ork/weights.h:141. Frees the handle; its device memory is reclaimed at
  * ork_npu_free (as in the reference, where device buffers go at context teardown). */
 void         ork_w_free(ork_w *w);

@@ -62,6 +62,8 @@ def lib():
         L.oracle_gen_i4_sattest.argtypes = [C.c_int, C.c_int, C.c_int, _P, _P]
         L.oracle_gen_cpu_gemm.argtypes = [_P, C.c_int, C.c_int, _P, C.c_size_t]
         L.oracle_gen_tm_gauss.argtypes = [_P, _P, C.c_size_t]
+        L.oracle_gemm_grouped.argtypes = [C.c_int] * 4 + [_P] * 5
+        L.oracle_gemm_grouped.restype = C.c_int
         _lib = L
     return _lib
 
@@ -80,6 +82,8 @@ def ref():
         R.ref_gemm_i32.argtypes = [C.c_int, C.c_int, C.c_int, _P, _P, _P]
         R.ref_i4_quant_chan.argtypes = [_P, C.c_int, C.c_float, C.c_int, _P, _P, _P]
         R.ref_i4_expand_chan_to_i8.argtypes = [_P, C.c_int, _P]
+        R.ref_gemm_grouped.argtypes = [C.c_int] * 4 + [_P] * 5
+        R.ref_gemm_grouped.restype = C.c_int
         _ref = R
     return _ref
 
@@ -113,6 +117,28 @@ def ref_gemm_i32(A, B):
     Cm = np.empty((M, N), dtype=np.int32)
     ref().ref_gemm_i32(M, K, N, _ptr(A), _ptr(B), _ptr(Cm))
     return Cm
+
+
+def _grouped(fn, A, codes, aS, bS, G):
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(codes, np.int8)
+    aS = np.ascontiguousarray(aS, np.float32)
+    bS = np.ascontiguousarray(bS, np.float32)
+    M, K = A.shape
+    N = B.shape[1]
+    Cm = np.empty((M, N), np.float32)
+    assert fn(M, K, N, G, _ptr(A), _ptr(B), _ptr(aS), _ptr(bS), _ptr(Cm)) == 0
+    return Cm
+
+
+def gemm_grouped(A, codes_kn, aScale, bScale, G):
+    """ork_{i4,i8}_mm_run_grouped arithmetic (src/npu/core/buf.c:501-520): C f32 [M][N]; aScale [M][K/G],
+    bScale [K/G][N]."""
+    return _grouped(lib().oracle_gemm_grouped, A, codes_kn, aScale, bScale, G)
+
+
+def ref_gemm_grouped(A, codes_kn, aScale, bScale, G):
+    return _grouped(ref().ref_gemm_grouped, A, codes_kn, aScale, bScale, G)
 
 
 def chan_scales_f32(f32_nk):

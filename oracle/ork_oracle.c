@@ -32,6 +32,8 @@
  *   oracle_i4a8_blob, oracle_o4n1_decode
  *                            header bytes, offsets, size (test_matmul.c:528), round trip, rejections,
  *                            qerr recomputed in float64
+ *   oracle_gemm_grouped      the reference's own compiled orki_cpu_gemm_grouped (oracle/_ref), bit for bit;
+ *                            a numpy float32 restatement; G = K reduces to one scaled int32 GEMM
  */
 #include <math.h>
 #include <stdint.h>
@@ -77,6 +79,28 @@ ORACLE_API void oracle_gemm_i32_naive(int M, int K, int N, const int8_t *A, cons
 
 /* ------------------------------------------------------------------------------------------ */
 /* Per-channel int8 scales: src/npu.c:854-865.  mx = max(1e-9, max|w|); inv = 127/mx; bscale = mx/127 */
+/* src/npu/core/buf.c:501-520 orki_cpu_gemm_grouped: per K-group int32 partials (exact), each scaled as
+ * ((float)acc * aScale[m*Sk+g]) * bScale[g*N+n] and added to C in ascending g, from 0.0f. */
+ORACLE_API int oracle_gemm_grouped(int M, int K, int N, int G, const int8_t *A, const int8_t *codes_kn,
+                                   const float *aScale, const float *bScale, float *C) {
+    if (M < 1 || K < 1 || N < 1 || G < 1 || K % G) return -1;
+    const int Sk = K / G;
+    int32_t *acc = malloc((size_t)N * sizeof *acc);
+    if (!acc) return -1;
+    for (int m = 0; m < M; m++) {
+        float *cr = C + (size_t)m * N;
+        for (int n = 0; n < N; n++) cr[n] = 0.0f;
+        for (int g = 0; g < Sk; g++) {
+            const float as = aScale[(size_t)m * Sk + g];
+            const float *bs = bScale + (size_t)g * N;
+            oracle_gemm_i32(1, G, N, A + (size_t)m * K + (size_t)g * G, codes_kn + (size_t)g * G * N, acc);
+            for (int n = 0; n < N; n++) cr[n] += (float)acc[n] * as * bs[n];
+        }
+    }
+    free(acc);
+    return 0;
+}
+
 ORACLE_API void oracle_chan_scales_f32(const float *f32, int K, int N, float *inv, float *bscale) {
     for (int n = 0; n < N; n++) {
         const float *fr = f32 + (size_t)n * K;

@@ -127,6 +127,7 @@ void ork_npu_free(ork_npu *c) {
         orkh_free(c->sA.p);
         orkh_free(c->sC.p);
         orkh_free(c->sW.p);
+        orkh_free(c->sS.p);
         for (int i = 0; i < c->dma_n; i++) orkh_host_free(c->dma[i].p);
         for (int i = 0; i < c->devb_n; i++) orkh_free(c->devb[i].p);
         for (int i = 0; i < c->orphan_n; i++) orkh_free(c->orphan[i]);

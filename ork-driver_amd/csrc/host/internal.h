@@ -26,8 +26,8 @@ struct ork_npu {
     orkh_dev dev;
     void *stream;
     int async;
-    /* device staging for host-side A / C and split-K partials, grown on demand */
-    struct ork_buf sA, sC, sW;
+    /* device staging for host-side A / C, split-K / grouped partials and grouped-run scales, grown on demand */
+    struct ork_buf sA, sC, sW, sS;
     /* ork_dma_alloc (pinned host) and ork_dev_alloc (HBM) registries */
     struct ork_buf dma[ORK_DMA_MAX];
     int dma_n;
@@ -51,6 +51,7 @@ struct ork_w {
     float *bscale;         /* i4a8: per-channel scale [N] (NULL for other weights) */
     int8_t *codes;         /* offline weights only: codes [K][N] for ork_w_codes */
     uint32_t lut[4];       /* NF4 int8 codebook, packed 4 entries per word */
+    int gsize;             /* K-group size for the grouped runs (0: per-channel weight) */
     ork_npu *ctx;
 };
 

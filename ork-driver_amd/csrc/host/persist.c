@@ -171,6 +171,10 @@ size_t ork_w_dump(const ork_w *w, void *out, size_t cap) {
         return r;
     }
     if (!w->dB) return 0;
+    /* the stamp names the payload's layout: W4A4 nibble panels load back through ork_i4_mm_load or
+     * ork_i4a8_mm_load_tiled, whichever entry point the weight ran through */
+    const int dt = w->rkind == ORKH_F16 ? DT_F16 : w->rkind == ORKH_I8 ? DT_I8 : w->rkind == ORKH_I4U ? DT_I4 : -1;
+    if (dt < 0) return 0;
     const size_t need = ORK_PACK_HDR_BYTES + w->dbytes;
     if (!out) return need;
     if (cap < need) return 0;
@@ -179,7 +183,7 @@ size_t ork_w_dump(const ork_w *w, void *out, size_t cap) {
         orki_hip_fail("ork_w_dump");
         return 0;
     }
-    pack_stamp(out, w->dtype, w->K, w->N);
+    pack_stamp(out, dt, w->K, w->N);
     return need;
 }
 
@@ -236,4 +240,16 @@ ork_w *ork_i8_mm_load_import(ork_npu *c, int K, int N, const void *blob, size_t 
 ork_w *ork_f16_mm_load_import(ork_npu *c, int K, int N, const void *blob, size_t n) {
     (void)c, (void)K, (void)N, (void)blob, (void)n;
     return NULL; /* no dma-buf import here: callers fall back to ork_f16_mm_load */
+}
+
+/* reference include/ork/weights.h:231-235: a W4A4 pack (the tiled int4 blob ork_w_dump writes) loaded as
+ * an int8-computed weight: its int4 values are the codes ork_i8_mm_run multiplies with, and G (0: none)
+ * is the group size for ork_i8_mm_run_grouped. Scales come from the caller. */
+ork_w *ork_i4a8_mm_load_tiled(ork_npu *c, int K, int N, const void *blob, size_t n, int G) {
+    if (N % 64 || G < 0 || (G > 0 && K % G)) return NULL;
+    ork_w *w = load_common("ork_i4a8_mm_load_tiled", c, K, N, DT_I4, ORKH_I4U, blob, n);
+    if (!w) return NULL;
+    w->dtype = DT_I8; /* runs through the int8 entry points */
+    w->gsize = G;
+    return w;
 }

@@ -98,6 +98,98 @@ int ork_f16_mm_run(ork_npu *c, ork_w *w, int M, const ork_f16 *A, float *C) {
     return run_common("ork_f16_mm_run", c, w, DT_F16, M, A, C, 2);
 }
 
+/* Grouped runs: ork_i8_mm_run_grouped (src/npu/i8/run.c:45-137) and ork_i4_mm_run_grouped
+ * (src/npu/i4/run.c:367-459). C f32[M][N] = the per-K-group int32 partials, each scaled by
+ * aScale[m*(K/G)+g] and bScale[g*N+n] and summed in ascending g (src/npu/core/buf.c:501-520), so the result
+ * is bit-identical to the reference's offline path. -1 on a NULL argument, a weight of the wrong kind or
+ * without a group size, A/C overlap, an offline context or a device failure (the reference's -1 cases);
+ * -3 for a group size the kernels cannot split at (G % 32), as the reference answers -3 for a device group
+ * size it does not support. Operands and scales may be host memory or ork_dev_alloc buffers. */
+static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M, const int8_t *A, const float *aS,
+                       const float *bS, float *C) {
+    if (!c || !w || !A || !aS || !bS || !C || M < 1) { orki_err("%s: NULL argument or M < 1", who); return -1; }
+    if (orki_need_device(c, who)) return -1;
+    if (w->dtype != want_dt || !w->dB || w->rkind == ORKH_F16) {
+        orki_err("%s: weight is %s, this run needs %s", who, w->dB ? dt_name(w->dtype) : "offline", dt_name(want_dt));
+        return -1;
+    }
+    const int K = w->K, N = w->N, G = w->gsize;
+    if (G < 1 || K % G) {
+        orki_err("%s: weight has no group size (ork_i4_mm_pack_grouped / ork_w_set_group)", who);
+        return -1;
+    }
+    if (G % 32) {
+        orki_err("%s: G=%d unsupported on the device: a group must be whole 32-k chunks", who, G);
+        return -3;
+    }
+    if ((w->rkind == ORKH_I4U || w->rkind == ORKH_NF4) && K > 131072) {
+        orki_err("%s: K=%d exceeds the int4 path's exact-accumulation bound (131072)", who, K);
+        return -1;
+    }
+    const int Sk = K / G;
+    const size_t abytes = (size_t)M * K, cbytes = (size_t)M * N * 4, asz = (size_t)M * Sk * 4,
+                 bsz = (size_t)Sk * N * 4, pbytes = (size_t)Sk * M * N * 4;
+    if (abytes >= ORKH_MAX_OPERAND_BYTES || w->dbytes >= ORKH_MAX_OPERAND_BYTES) {
+        orki_err("%s: operand too large for 32-bit buffer offsets", who);
+        return -1;
+    }
+    if (orki_check_overlap(who, (uintptr_t)A, (uintptr_t)A + abytes, (uintptr_t)C, (uintptr_t)C + cbytes)) return -1;
+
+    const int a_dev = orki_dev_find(c, A, abytes) && ((uintptr_t)A % 16 == 0);
+    const int c_dev = orki_dev_find(c, C, cbytes);
+    const int as_dev = orki_dev_find(c, aS, asz), bs_dev = orki_dev_find(c, bS, bsz);
+    const void *dA = A;
+    const float *dAS = aS, *dBS = bS;
+    float *dC = C;
+    if (!a_dev) {
+        void *st = orki_stage(c, &c->sA, abytes);
+        if (!st || orkh_h2d(st, A, abytes, c->stream)) { orki_hip_fail(who); return -1; }
+        dA = st;
+    }
+    if (!as_dev || !bs_dev) {
+        const size_t boff = (asz + 255) & ~(size_t)255;
+        uint8_t *st = orki_stage(c, &c->sS, boff + bsz);
+        if (!st) { orki_hip_fail(who); return -1; }
+        if (!as_dev) {
+            if (orkh_h2d(st, aS, asz, c->stream)) { orki_hip_fail(who); return -1; }
+            dAS = (const float *)st;
+        }
+        if (!bs_dev) {
+            if (orkh_h2d(st + boff, bS, bsz, c->stream)) { orki_hip_fail(who); return -1; }
+            dBS = (const float *)(st + boff);
+        }
+    }
+    if (!c_dev && !(dC = orki_stage(c, &c->sC, cbytes))) { orki_hip_fail(who); return -1; }
+    int32_t *P = orki_stage(c, &c->sW, pbytes);
+    if (!P) { orki_hip_fail(who); return -1; }
+    orkh_mm p;
+    memset(&p, 0, sizeof p);
+    p.kind = w->rkind;
+    p.M = M;
+    p.K = K;
+    p.N = N;
+    p.KB = w->KB;
+    p.A = dA;
+    p.lda = K;
+    p.B = w->dB;
+    p.ldc = N;
+    memcpy(p.lut, w->lut, sizeof p.lut);
+    const int rc = orkh_mm_launch_grouped(&p, G, P, dAS, dBS, dC, N, c->stream);
+    if (rc) { orki_hip_fail(who); return -1; }
+    if (!c_dev && orkh_d2h(C, dC, cbytes, c->stream)) { orki_hip_fail(who); return -1; }
+    if (c->async && a_dev && c_dev && as_dev && bs_dev) return 0;
+    if (orkh_sync(c->stream)) { orki_hip_fail(who); return -1; }
+    return 0;
+}
+
+int ork_i8_mm_run_grouped(ork_npu *c, ork_w *w, int M, const int8_t *A, const float *aScale, const float *bScale, float *C) {
+    return run_grouped("ork_i8_mm_run_grouped", c, w, DT_I8, M, A, aScale, bScale, C);
+}
+
+int ork_i4_mm_run_grouped(ork_npu *c, ork_w *w, int M, const int8_t *A, const float *aScale, const float *bScale, float *C) {
+    return run_grouped("ork_i4_mm_run_grouped", c, w, DT_I4, M, A, aScale, bScale, C);
+}
+
 const char *ork_w_plan_name(ork_npu *c, const ork_w *w, int M) {
     if (!c || !w || w->rkind < 0 || M < 1) return "none";
     orkh_plan q;

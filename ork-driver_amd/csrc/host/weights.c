@@ -312,3 +312,21 @@ ork_w *ork_i4_mm_pack(ork_npu *c, int K, int N, const int8_t *B) {
     if (rc) { free(w); return NULL; }
     return w;
 }
+
+/* ---- grouped scales ---------------------------------------------------------------------------------
+ * ork_i4_mm_pack_grouped (src/npu/i4/pack.c:686-700): the W4A4 pack plus a K-group size (K%32, N%64, G%32,
+ * K%G, G <= 10752). ork_w_set_group (src/npu.c:1191-1200): int4 or int8 weights, K%G. The group size
+ * only selects the scale layout of the grouped runs; the resident panels are the same as ungrouped. */
+ork_w *ork_i4_mm_pack_grouped(ork_npu *c, int K, int N, const int8_t *B, int G) {
+    if (!c || !B || K <= 0 || N <= 0 || K % 32 || N % 64 || G <= 0 || G % 32 || K % G || G > 10752) return NULL;
+    ork_w *w = ork_i4_mm_pack(c, K, N, B);
+    if (w) w->gsize = G;
+    return w;
+}
+
+int ork_w_set_group(ork_w *w, int G) {
+    if (!w || (w->dtype != DT_I4 && w->dtype != DT_I8)) return -1;
+    if (G > 0 && w->K % G) return -1;
+    w->gsize = G > 0 ? G : 0;
+    return 0;
+}

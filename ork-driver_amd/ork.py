@@ -45,6 +45,11 @@ API = {
     "ork_w_codes": (_P, [_P]),
     "ork_i4a8_w_dump": (C.c_size_t, [_P, _P, C.c_size_t]),
     "ork_pack_hdr_bytes": (C.c_size_t, []),
+    "ork_i4_mm_pack_grouped": (_P, [_P, C.c_int, C.c_int, _P, C.c_int]),
+    "ork_w_set_group": (C.c_int, [_P, C.c_int]),
+    "ork_i4a8_mm_load_tiled": (_P, [_P, C.c_int, C.c_int, _P, C.c_size_t, C.c_int]),
+    "ork_i8_mm_run_grouped": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P]),
+    "ork_i4_mm_run_grouped": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P]),
     "ork_w_dump": (C.c_size_t, [_P, _P, C.c_size_t]),
     "ork_i8_w_dump_cpu": (C.c_size_t, [_P, C.c_int, C.c_int, _P, _P, C.c_size_t]),
     "ork_i8_w_dump_bf_cpu": (C.c_size_t, [_P, C.c_int, C.c_int, _P, _P, C.c_size_t]),

@@ -1,0 +1,186 @@
+"""GPU parity of the grouped-scale runs (ork_i4_mm_run_grouped, ork_i8_mm_run_grouped).
+
+The bar is bit-exact fp32 equality with oracle.gemm_grouped, itself pinned bit for bit to the reference's
+own compiled orki_cpu_gemm_grouped (src/npu/core/buf.c:501-520): each K-group's int32 partial is exact,
+and the scaled sums run in the same ascending order without fused multiply-adds on both sides.
+Shapes: examples/i4.c gtest (grouped W4A4, G 128 and 64), examples/test_grouped_i8.c (grouped int8 through
+ork_i4a8_mm_load_tiled, N up to 20480 -- the reference's Sn > 1 cases), G = 32, row tiles (M > 16),
+int8 and NF4 weights with ork_w_set_group, host and device operands.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import ork
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _run(fn, npu, w, A, aS, bS):
+    M, N = A.shape[0], ork.dims(w)[1]
+    C = np.full((M, N), np.nan, np.float32)
+    rc = fn(npu.h, w, M, ork.ptr(A), ork.ptr(aS), ork.ptr(bS), ork.ptr(C))
+    return rc, C
+
+
+def _gtest_inputs(M, K, N, G):
+    """examples/i4.c gtest (:62-72): LCG values in [-1, 1] quantised to int4 per (row, group) and per
+    (group, column) with scale absmax/7, rounding as the reference does (+-0.5f, truncate, clamp [-8, 7])."""
+    Sk = K // G
+    s = (7 + M + K + N + G) & 0xFFFFFFFF
+    raw = np.empty(M * K + K * N, np.int64)
+    for i in range(raw.size):
+        s = (s * 1103515245 + 12345) & 0xFFFFFFFF
+        raw[i] = (s >> 9) % 2001 - 1000
+    vals = raw.astype(np.float32) / np.float32(1000.0)
+    Af = vals[:M * K].reshape(M, K)
+    Bf = vals[M * K:].reshape(K, N)
+
+    def q(x, sc):
+        t = (x / sc).astype(np.float32) + np.where(x >= 0, np.float32(0.5), np.float32(-0.5)).astype(np.float32)
+        return np.clip(np.trunc(t), -8, 7).astype(np.int8)
+
+    aS = np.maximum(np.abs(Af.reshape(M, Sk, G)).max(2), np.float32(1e-9)) / np.float32(7)
+    Ai = q(Af.reshape(M, Sk, G), aS[:, :, None]).reshape(M, K)
+    bS = np.maximum(np.abs(Bf.reshape(Sk, G, N)).max(1), np.float32(1e-9)) / np.float32(7)
+    Bi = q(Bf.reshape(Sk, G, N), bS[:, None, :]).reshape(K, N)
+    return Ai, Bi, aS.astype(np.float32), bS.astype(np.float32)
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 2048, 256, 128), (1, 4096, 512, 128), (4, 2048, 128, 64),
+                                     (8, 1024, 256, 64), (3, 512, 128, 32), (100, 1024, 192, 256)])
+def test_i4_grouped_exact(npu, M, K, N, G):
+    _say("w4a4 grouped", M, K, N, G)
+    L = ork.lib()
+    A, B, aS, bS = _gtest_inputs(M, K, N, G)
+    w = L.ork_i4_mm_pack_grouped(npu.h, K, N, ork.ptr(B), G)
+    assert w
+    rc, C = _run(L.ork_i4_mm_run_grouped, npu, w, A, aS, bS)
+    assert rc == 0
+    assert np.array_equal(C, O.gemm_grouped(A, B, aS, bS, G))
+    L.ork_mm_free(npu.h, w)
+
+
+def _grouped_i8_inputs(M, K, N, G):
+    """examples/test_grouped_i8.c: int4-range weights, int8-range activations (r4 * 7), patterned scales."""
+    rng = np.random.default_rng(M * 31 + K + N + G)
+    B = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
+    A = (rng.integers(-8, 8, size=(M, K)) * 7).astype(np.int8)
+    SG = K // G
+    aS = (0.001 * ((np.arange(M * SG) % 13) + 1)).astype(np.float32).reshape(M, SG)
+    bS = (0.002 * ((np.arange(SG * N) % 7) + 1)).astype(np.float32).reshape(SG, N)
+    return A, B, aS, bS
+
+
+@pytest.mark.parametrize("M,K,N,G", [(8, 2048, 4096, 512), (8, 2048, 16384, 512), (8, 4096, 20480, 1024),
+                                     (4, 3072, 12288, 1024)])
+def test_i8_grouped_tiled_load_exact(npu, M, K, N, G):
+    _say("i8 grouped via load_tiled", M, K, N, G)
+    L = ork.lib()
+    A, B, aS, bS = _grouped_i8_inputs(M, K, N, G)
+    blob = ork.dump_cpu(npu.h, B, w4a4=True)
+    w = L.ork_i4a8_mm_load_tiled(npu.h, K, N, ork.ptr(blob), blob.nbytes, G)
+    assert w
+    rc, C = _run(L.ork_i8_mm_run_grouped, npu, w, A, aS, bS)
+    assert rc == 0
+    assert np.array_equal(C, O.gemm_grouped(A, B, aS, bS, G))
+    # the same weight runs ungrouped through ork_i8_mm_run, exact int32
+    rc, Ci = npu.run_i8(w, A)
+    assert rc == 0 and np.array_equal(Ci, O.gemm_i32(A, B))
+    L.ork_mm_free(npu.h, w)
+
+
+@pytest.mark.parametrize("G,M", [(32, 1), (64, 20), (256, 1), (2048, 5)])
+def test_i8_set_group_exact(npu, G, M):
+    _say("i8 set_group", G, M)
+    L = ork.lib()
+    K, N = 2048, 384
+    rng = np.random.default_rng(G + M)
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    aS = rng.uniform(1e-3, 1e-2, size=(M, K // G)).astype(np.float32)
+    bS = rng.uniform(1e-3, 1e-2, size=(K // G, N)).astype(np.float32)
+    w = npu.pack_i8(B)
+    assert L.ork_w_set_group(w, G) == 0
+    rc, C = _run(L.ork_i8_mm_run_grouped, npu, w, A, aS, bS)
+    assert rc == 0 and np.array_equal(C, O.gemm_grouped(A, B, aS, bS, G))
+    L.ork_mm_free(npu.h, w)
+
+
+@pytest.mark.parametrize("nf4", [0, 1])
+def test_i4a8_grouped_exact(npu, nf4):
+    _say("i4a8 grouped", nf4)
+    L = ork.lib()
+    K, N, M, G = 1024, 256, 3, 128
+    rng = np.random.default_rng(40 + nf4)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    if nf4:
+        os.environ["ORK_NF4"] = "1"
+    try:
+        w, _ = npu.pack_i4a8(W)
+    finally:
+        os.environ.pop("ORK_NF4", None)
+    _, _, codes = O.pack_i4a8(W, nf4=bool(nf4))
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    aS = rng.uniform(1e-3, 1e-2, size=(M, K // G)).astype(np.float32)
+    bS = rng.uniform(1e-3, 1e-2, size=(K // G, N)).astype(np.float32)
+    assert L.ork_w_set_group(w, G) == 0
+    rc, C = _run(L.ork_i8_mm_run_grouped, npu, w, A, aS, bS)
+    assert rc == 0 and np.array_equal(C, O.gemm_grouped(A, codes, aS, bS, G))
+    L.ork_mm_free(npu.h, w)
+
+
+def test_grouped_device_operands_async(npu):
+    _say("grouped device operands")
+    L = ork.lib()
+    M, K, N, G = 16, 1024, 256, 128
+    A, B, aS, bS = _gtest_inputs(M, K, N, G)
+    w = L.ork_i4_mm_pack_grouped(npu.h, K, N, ork.ptr(B), G)
+    bufs = []
+    for arr in (A, aS, bS):
+        d = L.ork_dev_alloc(npu.h, arr.nbytes)
+        assert d and L.ork_dev_upload(npu.h, d, ork.ptr(arr), arr.nbytes) == 0
+        bufs.append(d)
+    dC = L.ork_dev_alloc(npu.h, M * N * 4)
+    L.ork_npu_set_async(npu.h, 1)
+    try:
+        assert L.ork_i4_mm_run_grouped(npu.h, w, M, bufs[0], bufs[1], bufs[2], dC) == 0
+        assert L.ork_npu_sync(npu.h) == 0
+    finally:
+        L.ork_npu_set_async(npu.h, 0)
+    C = np.empty((M, N), np.float32)
+    assert L.ork_dev_download(npu.h, ork.ptr(C), dC, C.nbytes) == 0
+    assert np.array_equal(C, O.gemm_grouped(A, B, aS, bS, G))
+    for d in bufs + [dC]:
+        L.ork_dev_free(npu.h, d)
+    L.ork_mm_free(npu.h, w)
+
+
+def test_grouped_errors(npu):
+    _say("grouped errors")
+    L = ork.lib()
+    K, N = 512, 128
+    B = np.zeros((K, N), np.int8)
+    A = np.zeros((2, K), np.int8)
+    aS = np.ones((2, K // 64), np.float32)
+    bS = np.ones((K // 64, N), np.float32)
+    w = npu.pack_i8(B)
+    assert _run(L.ork_i8_mm_run_grouped, npu, w, A, aS, bS)[0] == -1          # no group size
+    assert L.ork_w_set_group(w, 96) == -1                                      # K % G
+    assert L.ork_w_set_group(w, 16) == 0
+    assert _run(L.ork_i8_mm_run_grouped, npu, w, A, aS, bS)[0] == -3          # G % 32
+    assert L.ork_w_set_group(w, 64) == 0
+    assert _run(L.ork_i4_mm_run_grouped, npu, w, A, aS, bS)[0] == -1          # int8 weight, int4 run
+    assert _run(L.ork_i8_mm_run_grouped, npu, w, A, aS, bS)[0] == 0
+    wf = npu.pack_f16(np.zeros((K, N), np.float16))
+    assert L.ork_w_set_group(wf, 64) == -1                                     # fp16 has no groups
+    assert L.ork_i4_mm_pack_grouped(npu.h, K, N, ork.ptr(B), 48) is None        # G % 32
+    assert L.ork_i4_mm_pack_grouped(npu.h, K, 96, ork.ptr(np.zeros((K, 96), np.int8)), 64) is None  # N % 64
+    L.ork_mm_free(npu.h, w)
+    L.ork_mm_free(npu.h, wf)

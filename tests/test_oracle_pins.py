@@ -227,3 +227,41 @@ def test_o4n1_layout_and_qerr(nf4):
 def test_o4n1_c3_size():
     """examples/test_matmul.c:528: the K=2048, N=6144 blob is 20 + 4N + K*N/2 = 6,316,052 bytes."""
     assert O.lib().oracle_i4a8_blob(2048, 6144, O._ptr(np.zeros(1, np.float32)), None, 0, 0, None, 0, None) == 6316052
+
+
+def _grouped_case(seed, M, K, N, G, w4=True):
+    rng = np.random.default_rng(seed)
+    lo, hi = (-8, 8) if w4 else (-128, 128)
+    A = rng.integers(lo, hi, size=(M, K), dtype=np.int8)
+    B = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
+    aS = rng.uniform(1e-3, 2e-2, size=(M, K // G)).astype(np.float32)
+    bS = rng.uniform(1e-3, 2e-2, size=(K // G, N)).astype(np.float32)
+    return A, B, aS, bS
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 2048, 256, 128), (4, 2048, 128, 64), (3, 512, 96, 32), (2, 256, 64, 256)])
+def test_grouped_oracle_pins(M, K, N, G):
+    """oracle_gemm_grouped against the reference's own compiled orki_cpu_gemm_grouped (bit for bit, where
+    oracle/_ref builds), a numpy float32 restatement of the per-group order, and G = K closed form."""
+    A, B, aS, bS = _grouped_case(M + K + N + G, M, K, N, G)
+    C = O.gemm_grouped(A, B, aS, bS, G)
+    if O.ref_available():
+        assert np.array_equal(C, O.ref_gemm_grouped(A, B, aS, bS, G))
+    Sk = K // G
+    want = np.zeros((M, N), np.float32)
+    for g in range(Sk):
+        P = (A[:, g * G:(g + 1) * G].astype(np.int64) @ B[g * G:(g + 1) * G].astype(np.int64)).astype(np.int32)
+        want = want + (P.astype(np.float32) * aS[:, g:g + 1]) * bS[g][None, :]
+    assert np.array_equal(C, want)
+    # a planted mistake (one group's scales transposed onto the next group) must not agree
+    if Sk > 1:
+        bad = bS.copy()
+        bad[[0, 1]] = bad[[1, 0]]
+        assert not np.array_equal(O.gemm_grouped(A, B, aS, bad, G), C)
+
+
+def test_grouped_oracle_single_group_closed_form():
+    A, B, aS, bS = _grouped_case(5, 3, 512, 64, 512, w4=False)
+    C = O.gemm_grouped(A, B, aS, bS, 512)
+    P = O.gemm_i32(A, B).astype(np.float32)
+    assert np.array_equal(C, np.float32(0) + (P * aS) * bS)
