@@ -86,16 +86,18 @@ class Hip:
         return ms.value
 
 
-def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run"):
-    """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % len(ws)] through `entry`."""
+def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scales=None):
+    """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % len(ws)] through `entry`; the
+    grouped entry points also take the device scale buffers `scales` = (aScale, bScale)."""
     import ork
 
     L = ork.lib()
     stream = L.ork_npu_stream(npu.h)
     fn = getattr(L, entry)
+    mid = tuple(scales) if scales else ()
 
     def run(i):
-        rc = fn(npu.h, ws[i % len(ws)], M, dA, dC)
+        rc = fn(npu.h, ws[i % len(ws)], M, dA, *mid, dC)
         if rc:
             raise RuntimeError(f"{entry} rc={rc}")
 
@@ -211,7 +213,47 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
     L.ork_npu_set_async(npu.h, 1)
     for w in ws4:
         L.ork_mm_free(npu.h, w)
+
+    # ---- grouped scales (not a BASELINE config): W4A4 K=N=4096 with G=128 scales, M in {1, 256}; and the
+    # grouped int8 shape of examples/test_grouped_i8.c (W4A4 pack loaded as int8, K=2048, N=16384, G=512)
+    G4 = 128
+    Sk4 = K4 // G4
+    aS4 = rng.uniform(1e-3, 1e-2, size=(256, Sk4)).astype(np.float32)
+    bS4 = rng.uniform(1e-3, 1e-2, size=(Sk4, N4)).astype(np.float32)
+    dS4 = [L.ork_dev_alloc(npu.h, a.nbytes) for a in (aS4, bS4)]
+    assert all(dS4) and all(L.ork_dev_upload(npu.h, d, ork.ptr(a), a.nbytes) == 0 for d, a in zip(dS4, (aS4, bS4)))
+    wg4 = [L.ork_i4_mm_pack_grouped(npu.h, K4, N4, ork.ptr(B4), G4) for _ in range(64)]
+    assert all(wg4)
+    for M in (1, 256):
+        g, _ = measure(npu, hip, wg4, M, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run_grouped", dS4)
+        nbytes = K4 * N4 // 2 + M * K4 + 4 * (M * Sk4 + Sk4 * N4) + 4 * M * N4
+        rec("grouped W4A4 K=N=4096 G=128", "grouped_i4u", M, g, nbytes, 2 * M * N4 * K4,
+            "hbm" if M <= 16 else "mfma_int8")
+    L.ork_npu_set_async(npu.h, 0)
+    Cg = np.empty((4, N4), np.float32)
+    assert L.ork_i4_mm_run_grouped(npu.h, wg4[0], 4, dA4, dS4[0], dS4[1], dC) == 0
+    assert L.ork_dev_download(npu.h, ork.ptr(Cg), dC, Cg.nbytes) == 0
+    assert np.array_equal(Cg, O.gemm_grouped(A4[:4], B4, aS4[:4], bS4, G4)), "grouped W4A4 spot check"
+    L.ork_npu_set_async(npu.h, 1)
+    for w in wg4:
+        L.ork_mm_free(npu.h, w)
     L.ork_dev_free(npu.h, dA4)
+    K8, N8, G8, M8 = 2048, 16384, 512, 8
+    B8 = rng.integers(-8, 8, size=(K8, N8), dtype=np.int8)
+    blob8 = ork.dump_cpu(npu.h, B8, w4a4=True)
+    wg8 = [L.ork_i4a8_mm_load_tiled(npu.h, K8, N8, ork.ptr(blob8), blob8.nbytes, G8) for _ in range(40)]
+    aS8 = rng.uniform(1e-3, 1e-2, size=(M8, K8 // G8)).astype(np.float32)
+    bS8 = rng.uniform(1e-3, 1e-2, size=(K8 // G8, N8)).astype(np.float32)
+    dS8 = [L.ork_dev_alloc(npu.h, a.nbytes) for a in (aS8, bS8)]
+    assert all(wg8) and all(dS8)
+    assert all(L.ork_dev_upload(npu.h, d, ork.ptr(a), a.nbytes) == 0 for d, a in zip(dS8, (aS8, bS8)))
+    g, _ = measure(npu, hip, wg8, M8, dA, dC, steps_for(0.01), 16, "ork_i8_mm_run_grouped", dS8)
+    rec("grouped int8 (W4A4 pack) K=2048 N=16384 G=512", "grouped_i4u", M8, g,
+        K8 * N8 // 2 + M8 * K8 + 4 * (M8 * 4 + 4 * N8) + 4 * M8 * N8, 2 * M8 * N8 * K8, "hbm")
+    for w in wg8:
+        L.ork_mm_free(npu.h, w)
+    for d in dS4 + dS8:
+        L.ork_dev_free(npu.h, d)
     return out
 
 

@@ -114,11 +114,10 @@ typedef struct orkh_group {
     int n;
     orkh_gtask t[ORKH_GROUP_MAX];
 } orkh_group;
-/* Grouped run: per-K-group int32 partials into P [K/G][M][N] (device scratch), then
- * C[m][n] = sum_g ((float)P[g][m][n] * aS[m*(K/G)+g]) * bS[g*N+n] in ascending g. Integer kinds only;
- * G % 32 == 0, K % G == 0. 0 / -2 bad arguments / -1 HIP error. */
-int orkh_mm_launch_grouped(const orkh_mm *p, int G, int32_t *P, const float *aS, const float *bS, float *C, int ldc,
-                           void *stream);
+/* Grouped run: C[m][n] = sum over K-groups g ascending of ((float)P_g[m][n] * aS[m*(K/G)+g]) * bS[g*N+n],
+ * P_g the exact int32 partial of group g. Integer kinds only; G % 32 == 0, K % G == 0.
+ * 0 / -2 bad arguments / -1 HIP error. */
+int orkh_mm_launch_grouped(const orkh_mm *p, int G, const float *aS, const float *bS, float *C, int ldc, void *stream);
 int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream);
 /* Names of the compiled kernel variants, for diagnostics ("stream_i8_mt1_w4", ...). */
 const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *plan);

@@ -346,72 +346,86 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const c_t *ws, c_t *C, in
 
 // ------------------------------------------------------------------------------------------------
 // Grouped runs (per-(row, K-group) activation scales and per-(K-group, column) weight scales): the scales
-// cannot be factored out of the K sum, so each K-group's int32 partial is produced exactly and combined
-// in fp32 afterwards, in ascending group order.
-// k_grouped: grid (N/16, K/G, row tiles of 16*MT), 4 waves. Workgroup (nb, grp, mtile) owns panel nb and
-// the blocks holding k in [grp*G, grp*G + G); the waves take those blocks round-robin and reduce through
-// LDS. Every A chunk is 16 k wide and 16-k aligned and G % 32 == 0, so a chunk lies wholly inside or
-// outside the group: chunks outside are zero, and a block shared by two groups is read by both.
+// cannot be factored out of the K sum, so each K-group's int32 partial is produced exactly, scaled, and the
+// scaled terms are summed in ascending group order -- the float sequence of the reference's grouped
+// accumulate (src/npu/core/buf.c:501-520): c = 0; c = c + ((float)P_g * aS[m][g]) * bS[g][n], no fused
+// multiply-adds.
+// k_grouped: grid (N/16, row tiles of 16*MT), 4 waves. Workgroup (nb, mtile) owns panel nb and walks its
+// K-groups QG at a time: wave w computes groups w, w+4, ... of the chunk over the blocks holding
+// k in [g*G, g*G + G) (every A chunk is 16 k wide and 16-k aligned and G % 32 == 0, so a chunk lies wholly
+// inside or outside a group: chunks outside are zero; a block shared by two groups is read by both),
+// writes the scaled terms to LDS, and after a barrier each thread adds the chunk's terms of its own output
+// elements in group order.
+constexpr int QG = 8; // groups per LDS chunk
+
 template <int KIND, int MT>
-__global__ __launch_bounds__(256) void k_grouped(orkh_mm p, int G, int32_t *P) {
+__global__ __launch_bounds__(256) void k_grouped(orkh_mm p, int G, const float *aS, const float *bS, float *C, int ldc) {
+#pragma clang fp contract(off)
     using T = KT<KIND>;
-    __shared__ int32_t red[4][MT * 256];
+    __shared__ float xs[QG][MT * 256];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nb = blockIdx.x, grp = blockIdx.y, m0 = blockIdx.z * 16 * MT;
-    const int k_lo = grp * G, k_hi = min(k_lo + G, p.K);
-    const int kb_lo = k_lo / T::KPB, kb_hi = (k_hi + T::KPB - 1) / T::KPB;
-    const int r16 = lane & 15, g = lane >> 4;
+    const int nb = blockIdx.x, m0 = blockIdx.y * 16 * MT;
+    const int Sk = p.K / G;
+    const int r16 = lane & 15, gq = lane >> 4;
     const char *A = (const char *)p.A;
     const Lut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
     const v4i *bp = (const v4i *)p.B + (size_t)nb * p.KB * 64 + lane;
+    const int ncol = nb * 16 + (lane & 15);
 
-    v4i acc[MT];
+    float c[MT]; // this thread's output elements e = threadIdx.x + 256 * i, summed in group order
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) acc[mt] = v4i{0, 0, 0, 0};
-    for (int kb = kb_lo + w; kb < kb_hi; kb += 4) {
-        v4i av[T::STEPS][MT];
+    for (int i = 0; i < MT; i++) c[i] = 0.0f;
+
+    for (int g0 = 0; g0 < Sk; g0 += QG) {
+        const int nq = min(QG, Sk - g0);
+        for (int q = w; q < nq; q += 4) {
+            const int grp = g0 + q, k_lo = grp * G, k_hi = k_lo + G;
+            const int kb_lo = k_lo / T::KPB, kb_hi = (k_hi + T::KPB - 1) / T::KPB;
+            v4i acc[MT];
 #pragma unroll
-        for (int s = 0; s < T::STEPS; s++)
+            for (int mt = 0; mt < MT; mt++) acc[mt] = v4i{0, 0, 0, 0};
+            for (int kb = kb_lo; kb < kb_hi; kb++) {
+                v4i av[T::STEPS][MT];
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const int row = m0 + mt * 16 + r16, k = kb * T::KPB + a_koff<KIND>(s, g);
-                const bool ok = row < p.M && k >= k_lo && k < k_hi;
-                av[s][mt] = *(const v4i *)(A + (size_t)(ok ? row : 0) * p.lda + (ok ? k : 0));
-                if (!ok) av[s][mt] = v4i{0, 0, 0, 0};
+                for (int s = 0; s < T::STEPS; s++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        const int row = m0 + mt * 16 + r16, k = kb * T::KPB + a_koff<KIND>(s, gq);
+                        const bool ok = row < p.M && k >= k_lo && k < k_hi;
+                        av[s][mt] = *(const v4i *)(A + (size_t)(ok ? row : 0) * p.lda + (ok ? k : 0));
+                        if (!ok) av[s][mt] = v4i{0, 0, 0, 0};
+                    }
+                v4i op[T::STEPS];
+                decode<KIND>(__builtin_nontemporal_load(bp + (size_t)kb * 64), op, L);
+#pragma unroll
+                for (int s = 0; s < T::STEPS; s++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) acc[mt] = mma(av[s][mt], op[s], acc[mt]);
             }
-        v4i op[T::STEPS];
-        decode<KIND>(__builtin_nontemporal_load(bp + (size_t)kb * 64), op, L);
+            // scaled term of each output element of the tile: acc[mt][r] is row (lane/16)*4 + r, column lane%16
+            const float bsn = bS[(size_t)grp * p.N + ncol];
 #pragma unroll
-        for (int s = 0; s < T::STEPS; s++)
+            for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) acc[mt] = mma(av[s][mt], op[s], acc[mt]);
+                for (int r = 0; r < 4; r++) {
+                    const int m = min(m0 + mt * 16 + (lane >> 4) * 4 + r, p.M - 1);
+                    xs[q][mt * 256 + r * 64 + lane] = ((float)finish<KIND>(acc[mt][r]) * aS[(size_t)m * Sk + grp]) * bsn;
+                }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+            for (int q = 0; q < nq; q++) c[i] = c[i] + xs[q][threadIdx.x + 256 * i];
+        __syncthreads();
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) red[w][mt * 256 + r * 64 + lane] = acc[mt][r];
-    __syncthreads();
-    for (int e = threadIdx.x; e < MT * 256; e += 256) {
-        const int32_t sum = red[0][e] + red[1][e] + red[2][e] + red[3][e];
+    for (int i = 0; i < MT; i++) {
+        const int e = threadIdx.x + 256 * i;
         const int mt = e >> 8, r = (e >> 6) & 3, ln = e & 63;
         const int m = m0 + mt * 16 + (ln >> 4) * 4 + r;
         const int n = nb * 16 + (ln & 15);
-        if (m < p.M) P[((size_t)grp * p.M + m) * p.N + n] = finish<KIND>(sum);
+        if (m < p.M) C[(size_t)m * ldc + n] = c[i];
     }
-}
-
-// C[m][n] = sum over g ascending of ((float)P[g][m][n] * aS[m][g]) * bS[g][n], from 0.0f, without fused
-// multiply-adds: the float sequence of the reference's grouped accumulate (src/npu/core/buf.c:501-520).
-__global__ __launch_bounds__(256) void k_group_combine(const int32_t *P, const float *aS, const float *bS, float *C,
-                                                       int M, int N, int Sk, int ldc) {
-#pragma clang fp contract(off)
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t MN = (size_t)M * N;
-    if (i >= MN) return;
-    const int m = (int)(i / N), n = (int)(i % N);
-    float c = 0.0f;
-    for (int g = 0; g < Sk; g++) c = c + ((float)P[(size_t)g * MN + i] * aS[(size_t)m * Sk + g]) * bS[(size_t)g * N + n];
-    C[(size_t)m * ldc + n] = c;
 }
 
 // Dynamic LDS of k_tiled: KG groups x 2 stage buffers of A fragments, or (KG > 1) the 4-wave partial
@@ -780,8 +794,8 @@ extern "C" int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream) 
     return 0;
 }
 
-extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, int G, int32_t *P, const float *aS, const float *bS, float *C,
-                                      int ldc, void *stream) {
+extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, int G, const float *aS, const float *bS, float *C, int ldc,
+                                      void *stream) {
     hipStream_t s = (hipStream_t)stream;
     if (G < 32 || G % 32 || p->K % G || p->N % 16 || p->M < 1 || ldc < p->N ||
         (p->kind != ORKH_I8 && p->kind != ORKH_I4U && p->kind != ORKH_NF4)) {
@@ -789,20 +803,17 @@ extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, int G, int32_t *P, const
                  ldc);
         return -2;
     }
-    const int Sk = p->K / G, MT = p->M > 16 ? 4 : 1;
-    const dim3 grid((unsigned)(p->N / 16), (unsigned)Sk, (unsigned)((p->M + 16 * MT - 1) / (16 * MT))), block(256);
-#define ORKH_GROUPED_CASE(KIND)                                                                      \
-    if (MT == 1) hipLaunchKernelGGL((k_grouped<KIND, 1>), grid, block, 0, s, *p, G, P);               \
-    else hipLaunchKernelGGL((k_grouped<KIND, 4>), grid, block, 0, s, *p, G, P);
+    const int MT = p->M > 16 ? 4 : 1;
+    const dim3 grid((unsigned)(p->N / 16), (unsigned)((p->M + 16 * MT - 1) / (16 * MT))), block(256);
+#define ORKH_GROUPED_CASE(KIND)                                                                              \
+    if (MT == 1) hipLaunchKernelGGL((k_grouped<KIND, 1>), grid, block, 0, s, *p, G, aS, bS, C, ldc);          \
+    else hipLaunchKernelGGL((k_grouped<KIND, 4>), grid, block, 0, s, *p, G, aS, bS, C, ldc);
     switch (p->kind) {
     case ORKH_I8: ORKH_GROUPED_CASE(ORKH_I8) break;
     case ORKH_I4U: ORKH_GROUPED_CASE(ORKH_I4U) break;
     default: ORKH_GROUPED_CASE(ORKH_NF4) break;
     }
 #undef ORKH_GROUPED_CASE
-    const size_t MN = (size_t)p->M * p->N;
-    hipLaunchKernelGGL(k_group_combine, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, s, (const int32_t *)P, aS,
-                       bS, C, p->M, p->N, Sk, ldc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_lerr, sizeof g_lerr, "launch: %s", hipGetErrorString(e));

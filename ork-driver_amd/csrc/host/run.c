@@ -128,7 +128,7 @@ static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M
     }
     const int Sk = K / G;
     const size_t abytes = (size_t)M * K, cbytes = (size_t)M * N * 4, asz = (size_t)M * Sk * 4,
-                 bsz = (size_t)Sk * N * 4, pbytes = (size_t)Sk * M * N * 4;
+                 bsz = (size_t)Sk * N * 4;
     if (abytes >= ORKH_MAX_OPERAND_BYTES || w->dbytes >= ORKH_MAX_OPERAND_BYTES) {
         orki_err("%s: operand too large for 32-bit buffer offsets", who);
         return -1;
@@ -160,8 +160,6 @@ static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M
         }
     }
     if (!c_dev && !(dC = orki_stage(c, &c->sC, cbytes))) { orki_hip_fail(who); return -1; }
-    int32_t *P = orki_stage(c, &c->sW, pbytes);
-    if (!P) { orki_hip_fail(who); return -1; }
     orkh_mm p;
     memset(&p, 0, sizeof p);
     p.kind = w->rkind;
@@ -174,7 +172,7 @@ static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M
     p.B = w->dB;
     p.ldc = N;
     memcpy(p.lut, w->lut, sizeof p.lut);
-    const int rc = orkh_mm_launch_grouped(&p, G, P, dAS, dBS, dC, N, c->stream);
+    const int rc = orkh_mm_launch_grouped(&p, G, dAS, dBS, dC, N, c->stream);
     if (rc) { orki_hip_fail(who); return -1; }
     if (!c_dev && orkh_d2h(C, dC, cbytes, c->stream)) { orki_hip_fail(who); return -1; }
     if (c->async && a_dev && c_dev && as_dev && bs_dev) return 0;
