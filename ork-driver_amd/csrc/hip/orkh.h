@@ -66,7 +66,7 @@ int         orkh_device_sync(void);
 int         orkh_ptr_is_device(const void *p);
 
 /* ---- matmul launch ---- */
-enum { ORKH_ALGO_STREAM = 0, ORKH_ALGO_TILED = 1, ORKH_ALGO_GEMV = 2 };
+enum { ORKH_ALGO_STREAM = 0, ORKH_ALGO_TILED = 1, ORKH_ALGO_GEMV = 2, ORKH_ALGO_TILED2 = 3 };
 
 /* One C[M][N] = A[M][K] x B[K][N] launch on resident panels. A is row-major with row stride lda
  * elements (int8 for the integer kinds, fp16 for ORKH_F16); C is row-major int32 (integer kinds) or
@@ -88,7 +88,7 @@ typedef struct orkh_mm {
 
 /* Launch plan chosen by the host planner (ork-driver_amd/csrc/host/plan.c). */
 typedef struct orkh_plan {
-    int algo;             /* ORKH_ALGO_STREAM | ORKH_ALGO_TILED */
+    int algo;             /* ORKH_ALGO_STREAM | ORKH_ALGO_TILED | ORKH_ALGO_GEMV | ORKH_ALGO_TILED2 */
     /* GEMV (M = 1 only): the STREAM grid and fields below, VALU dot products instead of MFMA.
      * STREAM: grid (N/16, ksplit), wpg waves per workgroup, each wave kbw K-blocks of one panel,
      * mt = ceil(M/16) row tiles (1..4). ksplit > 1 writes partials to ws and adds a reduce pass. */

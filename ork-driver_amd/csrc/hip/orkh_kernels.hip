@@ -428,6 +428,159 @@ __global__ __launch_bounds__(256) void k_grouped(orkh_mm p, int G, const float *
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// k_tiled2: one 16-wave workgroup per BM x BN output tile (waves 4 x 4 over the tile). Both operands
+// go HBM/L2 -> LDS with direct-to-LDS buffer loads (no VGPR round trip), issued in MFMA fragment order so
+// the LDS image of a stage is already the operand layout: A fragment (mb, kbl, step) = 16 rows x 16 bytes
+// per lane row/k-group exactly as mma() takes it, B = the 1 KiB panel blocks verbatim. A ring of R stage
+// slots keeps R - 1 stages in flight; each stage costs one barrier. Loads are hidden from the compiler
+// (inline asm), so their completion is tracked by hand: every wave issues IPW loads per stage (padding
+// loads land in a junk block) and waits until at most (R - 2) * IPW are outstanding before the barrier
+// that publishes the stage. Raw buffer loads return 0 past a resource's end, which zero-fills M / N / K
+// edges and the stages past the end of K.
+// M0 carries the LDS destination; nothing else in these kernels uses M0 (checked in the ISA), so the
+// clobber of that reserved register is safe and its warning is silenced here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_byte), "v"(voff),
+                 "s"(r)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int VM> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(VM >= 0 && VM < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int KIND, int BM, int BN, int KS> struct T2 {
+    using T = KT<KIND>;
+    static constexpr int WM = 4, WN = 4, NW = 16;
+    static constexpr int MB = BM / 16, NB = BN / 16, MTW = MB / WM, NTW = NB / WN;
+    static constexpr int NIA = MB * KS * T::STEPS, NIB = NB * KS, NI = NIA + NIB;  // loads per stage
+    static constexpr int IPW = (NI + NW - 1) / NW;                               // per wave
+    static constexpr int JUNK = IPW * NW > NI ? 1 : 0;
+    static constexpr int SLOT = (NI + JUNK) * 1024;
+    static constexpr int R = (163840 / SLOT) < 4 ? (163840 / SLOT) : 4;          // ring depth within 160 KiB
+    static constexpr size_t LDS = (size_t)R * SLOT;
+    static_assert(MB % WM == 0 && NB % WN == 0 && R >= 2 && (R - 2) * IPW < 64, "tile");
+};
+
+template <int KIND, int BM, int BN, int KS>
+__global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntiles_all, int kbs, void *ws) {
+    using T = KT<KIND>;
+    using P = T2<KIND, BM, BN, KS>;
+    constexpr int R = P::R;
+    typedef typename T::acc_t acc_t;
+    typedef typename T::c_t c_t;
+    extern __shared__ v4i sm[];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wv % P::WM, wn = wv / P::WM;
+    // XCD-aware order: WG b runs on XCD b%8; each XCD gets a contiguous run of tiles, M fastest, so every
+    // M-tile that reads a given B column panel shares one L2.
+    const int nT = gridDim.x, bid = blockIdx.x;
+    const int per = nT / 8, rem = nT % 8, x = bid % 8, j = bid / 8;
+    const int tl = (x < rem) ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    const int ks = tl / ntiles_all, tile = tl % ntiles_all;
+    const int m0 = (tile % mtiles) * BM, nb0 = (tile / mtiles) * P::NB;
+    const int NBtot = p.N / 16;
+    const int kb_lo = ks * kbs, kb_hi = min(kb_lo + kbs, p.KB);
+    const int k_hi = min(kb_hi * T::KPB, p.K);
+    const uint32_t lda_b = (uint32_t)p.lda * T::ESZ;
+    const __amdgpu_buffer_rsrc_t Ar = make_rsrc(p.A, (uint32_t)p.M * lda_b);
+    const __amdgpu_buffer_rsrc_t Br = make_rsrc(p.B, (uint32_t)NBtot * p.KB * 1024u);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)sm;
+    const Lut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
+
+    // this wave's loads: i = wv + q * NW; A fragment (mb, kbl, step) or B block (nbl, kbl)
+    uint32_t voff[P::IPW];
+    int kof[P::IPW];
+#pragma unroll
+    for (int q = 0; q < P::IPW; q++) {
+        const int i = wv + q * P::NW;
+        voff[q] = OOB;
+        kof[q] = 0;
+        if (i < P::NIA) {
+            const int mb = i / (KS * T::STEPS), rest = i % (KS * T::STEPS);
+            const int kbl = rest / T::STEPS, st = rest % T::STEPS;
+            const int row = m0 + mb * 16 + (lane & 15);
+            kof[q] = kbl * T::KPB + a_koff<KIND>(st, lane >> 4);
+            if (row < p.M) voff[q] = (uint32_t)row * lda_b + (uint32_t)kof[q] * T::ESZ;
+        } else if (i < P::NI) {
+            const int ii = i - P::NIA, nbl = ii / KS;
+            kof[q] = ii % KS;
+            if (nb0 + nbl < NBtot) voff[q] = ((uint32_t)(nb0 + nbl) * p.KB * 64 + lane) * 16;
+        }
+    }
+    const int nst = (kb_hi - kb_lo + KS - 1) / KS;
+    auto issue = [&](int st) {
+        const uint32_t slot = lds0 + (uint32_t)(st % R) * P::SLOT;
+        const int kb0 = kb_lo + st * KS;
+#pragma unroll
+        for (int q = 0; q < P::IPW; q++) {
+            const int i = wv + q * P::NW;
+            if (i < P::NIA) {
+                const int k = kb0 * T::KPB + kof[q];
+                lds_dma16(Ar, (voff[q] != OOB && k < k_hi) ? voff[q] + (uint32_t)kb0 * T::KPB * T::ESZ : OOB,
+                          slot + i * 1024);
+            } else {
+                const int kb = kb0 + kof[q];
+                lds_dma16(Br, (i < P::NI && voff[q] != OOB && kb < kb_hi) ? voff[q] + (uint32_t)kb * 1024u : OOB,
+                          slot + (i < P::NI ? i : P::NI) * 1024);
+            }
+        }
+    };
+
+    acc_t acc[P::MTW][P::NTW];
+#pragma unroll
+    for (int a = 0; a < P::MTW; a++)
+#pragma unroll
+        for (int b = 0; b < P::NTW; b++) acc[a][b] = acc_t{0, 0, 0, 0};
+
+#pragma unroll
+    for (int st = 0; st < R - 1; st++) issue(st);
+    for (int s = 0; s < nst; s++) {
+        wait_vmcnt<(R - 2) * P::IPW>();
+        __syncthreads();
+        issue(s + R - 1); // into the slot of stage s - 1, which every wave finished before the barrier
+        const v4i *As = sm + (s % R) * (P::SLOT / 16);
+        const v4i *Bs = As + P::NIA * 64;
+#pragma unroll
+        for (int kbl = 0; kbl < KS; kbl++) {
+            v4i op[P::NTW][T::STEPS];
+#pragma unroll
+            for (int jn = 0; jn < P::NTW; jn++) decode<KIND>(Bs[((wn * P::NTW + jn) * KS + kbl) * 64 + lane], op[jn], L);
+#pragma unroll
+            for (int st = 0; st < T::STEPS; st++)
+#pragma unroll
+                for (int i = 0; i < P::MTW; i++) {
+                    const v4i a = As[(((wm * P::MTW + i) * KS + kbl) * T::STEPS + st) * 64 + lane];
+#pragma unroll
+                    for (int jn = 0; jn < P::NTW; jn++) acc[i][jn] = mma(a, op[jn][st], acc[i][jn]);
+                }
+        }
+    }
+    wait_vmcnt<0>();
+
+    const bool split = gridDim.x > ntiles_all;
+    c_t *C = split ? (c_t *)ws + (size_t)ks * p.M * p.N : (c_t *)p.C;
+    const size_t ldc = split ? (size_t)p.N : (size_t)p.ldc;
+#pragma unroll
+    for (int i = 0; i < P::MTW; i++)
+#pragma unroll
+        for (int jn = 0; jn < P::NTW; jn++) {
+            const int nbk = nb0 + wn * P::NTW + jn;
+            if (nbk >= NBtot) continue;
+            const int n = nbk * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + (wm * P::MTW + i) * 16 + (lane >> 4) * 4 + r;
+                if (m < p.M) C[(size_t)m * ldc + n] = finish<KIND>(acc[i][jn][r]);
+            }
+        }
+}
+
 // Dynamic LDS of k_tiled: KG groups x 2 stage buffers of A fragments, or (KG > 1) the 4-wave partial
 // tile parked for the final cross-group sum, whichever is larger.
 template <int KIND, int BM, int BN, int KS, int KG>
@@ -675,11 +828,46 @@ int launch_tiled_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     return 0;
 }
 
+// K-blocks per stage of k_tiled2: ~128 bytes of each activation row per stage for small tiles, ~64 for the
+// 256 x 256 tile (whose ring would not fit otherwise).
+template <int KIND, int BM, int BN> constexpr int t2_ks() {
+    if (KIND == ORKH_I4U || KIND == ORKH_NF4) return 1;
+    return BM * BN >= 65536 ? 1 : 2;
+}
+
+template <int KIND, int BM, int BN>
+int launch_tiled2_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
+    constexpr int KS = t2_ks<KIND, BM, BN>();
+    using P = T2<KIND, BM, BN, KS>;
+    auto kern = k_tiled2<KIND, BM, BN, KS>;
+    static bool attr = false; // per instantiation: allow more than the default 64 KiB of dynamic LDS
+    if (!attr) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)P::LDS) != hipSuccess)
+            return -1;
+        attr = true;
+    }
+    const int mtiles = (p->M + BM - 1) / BM;
+    const int ntiles = (p->N / 16 + P::NB - 1) / P::NB;
+    const int ksplit = q->ksplit > 1 ? q->ksplit : 1;
+    const int kbs = ksplit > 1 ? q->kbs : p->KB;
+    hipLaunchKernelGGL(kern, dim3(mtiles * ntiles * ksplit), dim3(1024), P::LDS, s, *p, mtiles, mtiles * ntiles, kbs,
+                       q->ws);
+    return 0;
+}
+
 template <int KIND>
 int launch_tiled(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     if (q->ksplit > 1 && (!q->ws || (long)q->ksplit * q->kbs < p->KB)) {
         snprintf(g_lerr, sizeof g_lerr, "tiled plan: ksplit=%d kbs=%d does not cover KB=%d or has no ws", q->ksplit,
                  q->kbs, p->KB);
+        return -2;
+    }
+    if (q->algo == ORKH_ALGO_TILED2) {
+        if (q->bm == 256 && q->bn == 256) return launch_tiled2_v<KIND, 256, 256>(p, q, s);
+        if (q->bm == 128 && q->bn == 128) return launch_tiled2_v<KIND, 128, 128>(p, q, s);
+        if (q->bm == 64 && q->bn == 192) return launch_tiled2_v<KIND, 64, 192>(p, q, s);
+        if (q->bm == 64 && q->bn == 64) return launch_tiled2_v<KIND, 64, 64>(p, q, s);
+        snprintf(g_lerr, sizeof g_lerr, "tiled2 plan: %dx%d unsupported", q->bm, q->bn);
         return -2;
     }
     if (q->bm == 128 && q->bn == 96) return launch_tiled_v<KIND, 128, 96>(p, q, s);
@@ -831,8 +1019,9 @@ extern "C" const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *q) {
     else if (q->algo == ORKH_ALGO_STREAM)
         snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d", k, q->mt, q->wpg, q->kbw, q->ksplit);
     else if (q->ksplit > 1)
-        snprintf(b, sizeof b, "tiled_%s_%dx%d_ks%d", k, q->bm, q->bn, q->ksplit);
+        snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
+                 q->ksplit);
     else
-        snprintf(b, sizeof b, "tiled_%s_%dx%d", k, q->bm, q->bn);
+        snprintf(b, sizeof b, "%s_%s_%dx%d", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn);
     return b;
 }

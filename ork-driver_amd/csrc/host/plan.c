@@ -11,6 +11,7 @@
  *            shapes that leave the machine underfilled. ORK_KSPLIT=n forces a split (tests).
  *   M >  64  tiled: the BM x BN tile (128x96, 128x128 or 64x64) and K split with the least modelled
  *            time (operand bytes per workgroup-round, plus partials and a reduce launch when split). */
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -62,18 +63,70 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
         return 0;
     }
 
-    /* Tiled: each CU pulls its tiles' A and B rows through L2 at a roughly fixed rate, so the time of a
-     * round of workgroups is about the operand bytes one workgroup loads. K is split across
-     * workgroups when that cuts the per-workgroup bytes by more than the partial sums and the extra
+    const char *tf = getenv("ORK_TILE"); /* testing / A-B: "BMxBN" forces that tile of the LDS-ring kernel */
+    int fbm, fbn;
+    if (tf && sscanf(tf, "%dx%d", &fbm, &fbn) == 2) {
+        const char *fks2 = getenv("ORK_KSPLIT");
+        int ks = fks2 ? atoi(fks2) : 1;
+        if (ks < 1) ks = 1;
+        if (ks > KB) ks = KB;
+        q->algo = ORKH_ALGO_TILED2;
+        q->bm = fbm;
+        q->bn = fbn;
+        q->kbs = cdiv(KB, ks);
+        q->ksplit = cdiv(KB, q->kbs);
+        if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
+        return 0;
+    }
+    const char *fks = getenv("ORK_KSPLIT");
+    int ks_force = fks ? atoi(fks) : 0;
+    if (ks_force > 0) ks_force = cdiv(KB, cdiv(KB, ks_force < KB ? ks_force : KB)); /* as a split can realise it */
+    double best = -1;
+
+    /* The LDS-ring kernel (k_tiled2) for int8, fp16 and uniform int4. Each workgroup is bound by how fast its
+     * operand tiles reach the CU (measured ~15 B/clk per CU, i.e. ~0.027 us per KiB) plus ~1.5 us of
+     * set-up, so a round of workgroups costs about 1.5 + 0.027 * (A + B + C KiB of one workgroup) us.
+     * Measured on K=2048..6144, M=128..4096 int8 / fp16 / W4A4 shapes to within ~15%. A K split adds
+     * the partials' round trip and the reduce launch (~3 us + 2 * ks * M * N * 4 B at 4 TB/s).
+     * NF4 keeps k_tiled: four waves share each decoded B block here, and the codebook decode is not
+     * cheap enough to repeat. */
+    if (rkind != ORKH_NF4 && !(force && !strcmp(force, "tiled"))) {
+        static const int cfg2[][2] = {{256, 256}, {128, 128}, {64, 192}, {64, 64}};
+        const int kpb = rkind == ORKH_I8 ? 64 : rkind == ORKH_F16 ? 32 : 128;
+        const int abpk = rkind == ORKH_F16 ? 2 * kpb : kpb; /* A bytes per row per K-block */
+        for (int i = 0; i < 4; i++) {
+            const int bm = cfg2[i][0], bn = cfg2[i][1];
+            const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);
+            for (int ks = ks_force > 0 ? ks_force : 1; ks <= (ks_force > 0 ? ks_force : 8); ks *= (ks_force > 0 ? 8 : 2)) {
+                const int kbs = cdiv(KB, ks);
+                if (ks_force <= 0 && (cdiv(KB, kbs) != ks || (ks > 1 && kbs < 4))) continue;
+                const long wgs = tiles * ks;
+                const long rounds = (wgs + cu - 1) / cu;
+                const double kib = ((double)bm * abpk * kbs + (double)bn / 16 * 1024 * kbs + (double)bm * bn * 4) / 1024;
+                double t = rounds * (1.5 + 0.027 * kib);
+                if (ks > 1) t += 3.0 + 2.0 * ks * (double)M * N * 4 / 4e6;
+                if (best < 0 || t < best - 1e-9) {
+                    best = t;
+                    q->algo = ORKH_ALGO_TILED2;
+                    q->bm = bm;
+                    q->bn = bn;
+                    q->ksplit = ks;
+                    q->kbs = kbs;
+                }
+            }
+        }
+        if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
+        return 0;
+    }
+
+    /* k_tiled (NF4, or ORK_PLAN=tiled): each CU pulls its tiles' A and B rows through L2 at a roughly fixed
+     * rate, so the time of a round of workgroups is about the operand bytes one workgroup loads. K is split
+     * across workgroups when that cuts the per-workgroup bytes by more than the partial sums and the extra
      * reduce launch (~2 us) cost. Model units: us at ~48 KB/us per CU (measured order of magnitude),
      * 5 TB/s for the partials' HBM round trip. */
     static const int cfg[][2] = {{128, 96}, {128, 128}, {64, 64}};
     const int bpk = 64;                                                  /* B bytes per column per K-block, every kind */
     const int apk = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 128 : 64; /* A bytes per row per K-block */
-    const char *fks = getenv("ORK_KSPLIT");
-    int ks_force = fks ? atoi(fks) : 0;
-    if (ks_force > 0) ks_force = cdiv(KB, cdiv(KB, ks_force < KB ? ks_force : KB)); /* as a split can realise it */
-    double best = -1;
     for (int i = 0; i < 3; i++) {
         const int bm = cfg[i][0], bn = cfg[i][1];
         const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);

@@ -436,3 +436,48 @@ def test_run_errors(npu):
     ork.free(wi8)
     ork.free(wi4)
     assert L.ork_io_failures() == 0
+
+
+@pytest.mark.parametrize("tile", ["256x256", "128x128", "64x192", "64x64"])
+@pytest.mark.parametrize("ks", [1, 3])
+def test_lds_ring_tiles_all_kinds(npu, tile, ks):
+    """The LDS-ring tiled kernel at every tile shape the planner can choose, unsplit and K-split: exact for
+    int8, uniform-int4 i4a8 and W4A4, within the fp16 bar (and run-to-run identical) for fp16. M, N and K
+    tails: M = 300 and 70 are no tile multiple, N = 224 (14 panels) leaves a partial tile for every tile
+    width, K = 2080 ends mid K-block for int8 (K % 64 = 32) and the nibble kinds (K % 128 = 32)."""
+    _say("lds-ring tile", tile, "ks", ks)
+    rng = np.random.default_rng(hash((tile, ks)) % 2**32)
+    K, N = 2080, 224
+    for M in (300, 70):
+        B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+        A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+        w = npu.pack_i8(B)
+        assert w
+        with _env(ORK_TILE=tile, ORK_KSPLIT=ks):
+            rc, C = npu.run_i8(w, A)
+            name = npu.plan_name(w, M)
+        assert name.startswith("tiled2_i8_" + tile), name
+        assert rc == 0 and np.array_equal(C, O.gemm_i32(A, B)), ("i8", name)
+        ork.free(w)
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        w, _ = npu.pack_i4a8(W)
+        _, _, codes = O.pack_i4a8(W)
+        with _env(ORK_TILE=tile, ORK_KSPLIT=ks):
+            rc, C = npu.run_i8(w, A)
+        assert rc == 0 and np.array_equal(C, O.gemm_i32(A, codes)), ("i4a8 uniform", M)
+        ork.free(w)
+    A4, B4 = O.gen_i4_test(150, 1056, 256)   # W4A4 needs N % 64
+    w = npu.pack_i4(B4)
+    with _env(ORK_TILE=tile, ORK_KSPLIT=ks):
+        rc, C = npu.run_i4(w, A4)
+    assert rc == 0 and np.array_equal(C, O.gemm_i32(A4, B4)), "w4a4"
+    ork.free(w)
+    Ah = rng.standard_normal((130, 1056)).astype(np.float16)
+    Bh = (rng.standard_normal((1056, 224)) * 0.02).astype(np.float16)
+    w = npu.pack_f16(Bh)
+    with _env(ORK_TILE=tile, ORK_KSPLIT=ks):
+        rc, C1 = npu.run_f16(w, Ah)
+        rc2, C2 = npu.run_f16(w, Ah)
+    assert rc == 0 and rc2 == 0 and np.array_equal(C1, C2)
+    assert O.fp16_err(C1, O.gemm_f16_f64acc(Ah, Bh)) <= FP16_TOL
+    ork.free(w)
