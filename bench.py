@@ -282,7 +282,7 @@ def measure_chain(npu, hip, L, ws, dA, dC, S, steps):
     return ms
 
 
-def measure_decoder(npu, nf4, prompt_len=128, decode_len=256):
+def measure_decoder(npu, nf4, prompt_len=128, decode_len=256, graph=True):
     """the Qwen3-1.7B-shaped decoder (28 layers, hidden 2048, 16 Q / 8 KV heads,
     head_dim 128, SwiGLU 6144, vocab 151936), seeded N(0, 0.02) weights packed w8a8 per channel (NF4 w4a8
     FFNs when nf4), prefill of 128 seeded tokens, then 256 greedy decode steps (context <= 512). Every
@@ -298,12 +298,12 @@ def measure_decoder(npu, nf4, prompt_len=128, decode_len=256):
         assert m.init_random(0x6F726B00 + (5 << 8)) == 0
         init_s = time.perf_counter() - t0
         prompt = np.random.default_rng(0x6F726B05).integers(0, cfg.vocab, prompt_len).astype(np.int32)
-        assert m.prefill(prompt) == 0 and m.decode(4, graph=True) == 0   # warm-up and graph capture
+        assert m.prefill(prompt) == 0 and m.decode(4, graph=graph) == 0   # warm-up and graph capture
         t0 = time.perf_counter()
         assert m.prefill(prompt) == 0
         pre_s = time.perf_counter() - t0
         t0 = time.perf_counter()
-        assert m.decode(decode_len, graph=True) == 0
+        assert m.decode(decode_len, graph=graph) == 0
         dec_s = time.perf_counter() - t0
         toks = m.tokens()
         logits = m.last_logits()
@@ -391,6 +391,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the sweep over BASELINE configs 1-4")
     ap.add_argument("--no-decoder", action="store_true", help="skip BASELINE config 5 (the Qwen3-shaped decoder)")
+    ap.add_argument("--eager-decoder", action="store_true",
+                    help="profiling: launch the decode steps eagerly instead of replaying the captured graph (same kernels)")
     ap.add_argument("--only", choices=["gemv", "m512", "chain", "decoder"],
                     help="profiling: time only one kernel (decoder: only BASELINE config 5, w8a8)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -412,7 +414,7 @@ def main():
         return
     if args.only == "decoder":
         with ork.Npu() as npu:
-            print(json.dumps(measure_decoder(npu, 0)), flush=True)
+            print(json.dumps(measure_decoder(npu, 0, graph=not args.eager_decoder)), flush=True)
         return
     rng = np.random.default_rng(0x6F726B00 + (1 << 8))
     W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)   # f32[N][K]
