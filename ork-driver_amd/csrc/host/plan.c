@@ -6,11 +6,15 @@
  * 8192-wide outputs and M into CBUF-sized row groups, each a separate submit with a host int32
  * accumulate. On MI355X every shape is one launch (plus a reduce pass when K is split across
  * workgroups); the planner only decides how to fill 256 CUs:
- *   M <= 64  stream: one 16-column panel per workgroup, waves split K in runs of 1 KiB blocks (8 per
- *            run for the int8/fp16 GEMV); K is split across workgroups only for long-K, few-panel
- *            shapes that leave the machine underfilled. ORK_KSPLIT=n forces a split (tests).
- *   M >  64  tiled: the BM x BN tile (128x96, 128x128 or 64x64) and K split with the least modelled
- *            time (operand bytes per workgroup-round, plus partials and a reduce launch when split). */
+ *   M = 1    GEMV: one 16-column panel per workgroup, waves split K in runs of 8 KiB; K is split across
+ *            workgroups only for long-K, few-panel shapes that leave the machine underfilled.
+ *   M <= 64  the streaming kernel (same grid, runs of 1-4 KiB) or the LDS-ring tiled kernel, whichever a
+ *            delivery model of both prices lower, each with its best K split (NF4: streaming, by the
+ *            occupancy rule of the GEMV).
+ *   M >  64  the LDS-ring tiled kernel (k_tiled for NF4): the tile and K split with the least modelled time.
+ * Both time models charge a workgroup for a fixed set-up, the operand bytes that must reach its CU and
+ * its multiply-accumulates; a K split adds its partials' round trip and the reduce launch.
+ * ORK_PLAN=stream|tiled, ORK_TILE=BMxBN and ORK_KSPLIT=n force a kernel, tile or split (tests, A/B). */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -19,57 +23,126 @@
 
 static int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+/* A bytes per activation row per 1 KiB weight block (K-block of the panel layout) */
+static int a_bytes_per_kb(int rkind) { return rkind == ORKH_F16 ? 64 : (rkind == ORKH_I8 ? 64 : 128); }
+static int kpb_of(int rkind) { return rkind == ORKH_I8 ? 64 : rkind == ORKH_F16 ? 32 : 128; }
+
+/* Streaming-kernel geometry for a K split of ks (1 = unsplit). Run length per wave: 8 KiB in flight per
+ * wave for the int8/fp16 GEMV (M = 1); more waves with shorter runs where each block costs more issue
+ * (more rows, int4 decode). Measured on the K=2048, N=6144 panels; the run lengths on either side were
+ * within 2-4%. */
+static void stream_geom(int rkind, int M, int KB, int ks, orkh_plan *q) {
+    const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
+    const int need = cdiv(KB, kbw_target); /* waves per panel at the target run length */
+    const int wpg = need <= 4 ? 4 : 8;
+    if (ks > KB) ks = KB;
+    if (ks < 1) ks = 1;
+    const int kbs = cdiv(KB, ks);
+    q->mt = cdiv(M, 16);
+    q->wpg = wpg;
+    q->kbs = kbs;
+    q->kbw = cdiv(kbs, wpg);
+    q->ksplit = cdiv(KB, kbs);
+}
+
+/* The GEMV's split rule: split only when the panels leave the machine underfilled (< 4 waves per CU) AND
+ * each wave would otherwise stream more than two runs back to back; the split costs a second launch
+ * (the fixed-order reduce), which a one-run wave never repays. */
+static int stream_rule_ks(int rkind, int M, int KB, int NB, int cu) {
+    orkh_plan g;
+    stream_geom(rkind, M, KB, 1, &g);
+    const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
+    const int runs = cdiv(cdiv(KB, g.wpg), kbw_target);
+    int ks = 1;
+    if ((long)NB * g.wpg < 4L * cu && runs > 2) {
+        ks = cdiv(4 * cu, NB * g.wpg);
+        if (ks > runs) ks = runs; /* every wave keeps a full run */
+    }
+    return ks;
+}
+
+/* Time models (us) of the two MFMA kernels, for int8, fp16 and uniform int4 weights. A workgroup's time is
+ * the sum of
+ *   a fixed launch / drain cost and a cost per workgroup placed on the busiest CU ("per"),
+ *   the operand bytes that must reach its CU (A rows, B blocks, C tile), per KiB: the ~15 B/clk per CU
+ *   that L2 delivers, and (LDS-ring kernel) a further share that grows with the number of CUs pulling
+ *   at once, and
+ *   its multiply-accumulates at the kind's rate (per million MACs: int8 ~0.1 us, fp16 ~0.19 us, int4
+ *   with decode ~0.2 us in the LDS-ring kernel -- the MFMA peaks; ~10x that in the streaming kernel,
+ *   whose few waves per panel keep dependent MFMA chains);
+ * with nothing overlapped between the three. A K split adds the reduce launch and the int32/fp32
+ * partials written and read back. Least-squares fits to 588 timed launches (int8, fp16, W4A8, W4A4;
+ * M = 16..4096, K = 2048..6144, N = 2048..22016; every tile and split on offer): 4% rms error for the
+ * streaming kernel, 7% for the tiled one, and the pick within 1% of the fastest timed candidate. */
+static double mac_rate(int rkind, int tiled) {
+    if (rkind == ORKH_I8) return tiled ? 0.100 : 0.94;
+    if (rkind == ORKH_F16) return tiled ? 0.187 : 1.90;
+    return tiled ? 0.199 : 0.91;
+}
+
+static double stream_us(int rkind, int M, int N, int KB, int cu, int ks) {
+    orkh_plan g;
+    stream_geom(rkind, M, KB, ks, &g);
+    const long wgs = (long)(N / 16) * g.ksplit;
+    const double per = (double)((wgs + cu - 1) / cu);
+    const double kib = ((double)M * a_bytes_per_kb(rkind) * g.kbs + 1024.0 * g.kbs + 64.0 * M) / 1024;
+    const double mmac = (double)g.mt * 16 * 16 * g.kbs * kpb_of(rkind) / 1e6;
+    double t = 1.74 + per * (0.103 + 0.017 * kib + mac_rate(rkind, 0) * mmac);
+    if (g.ksplit > 1) t += 2.81 + 0.327 * g.ksplit * (double)M * N * 4 / 1e6;
+    return t;
+}
+
+/* The LDS-ring kernel (k_tiled2): every tile and split on offer priced by the model above; A counts the
+ * whole tile height, since rows past M still issue (zero-filled) loads. Returns the modelled time of
+ * the best and fills q with it. */
+static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force, orkh_plan *q) {
+    static const int cfg2[][2] = {{256, 256}, {128, 128}, {64, 192}, {64, 64}};
+    const int NB = N / 16;
+    const int abpk = a_bytes_per_kb(rkind), kpb = kpb_of(rkind);
+    double best = -1;
+    for (int i = 0; i < 4; i++) {
+        const int bm = cfg2[i][0], bn = cfg2[i][1];
+        const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);
+        for (int ks = ks_force > 0 ? ks_force : 1; ks <= (ks_force > 0 ? ks_force : 8); ks *= (ks_force > 0 ? 8 : 2)) {
+            const int kbs = cdiv(KB, ks);
+            if (ks_force <= 0 && (cdiv(KB, kbs) != ks || (ks > 1 && kbs < 4))) continue;
+            const long wgs = tiles * ks;
+            const double per = (double)((wgs + cu - 1) / cu);
+            const double busy = (double)(wgs < cu ? wgs : cu) / cu;
+            const double kib = ((double)bm * abpk * kbs + (double)bn / 16 * 1024 * kbs + (double)bm * bn * 4) / 1024;
+            const double mmac = (double)bm * bn * kbs * kpb / 1e6;
+            double t = 4.09 + per * (0.35 + (0.0104 + 0.0058 * busy) * kib + mac_rate(rkind, 1) * mmac);
+            if (ks > 1) t += 2.11 + 0.456 * ks * (double)M * N * 4 / 1e6;
+            if (best < 0 || t < best - 1e-9) {
+                best = t;
+                q->algo = ORKH_ALGO_TILED2;
+                q->bm = bm;
+                q->bn = bn;
+                q->ksplit = ks;
+                q->kbs = kbs;
+            }
+        }
+    }
+    return best;
+}
+
 int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes) {
     (void)K;
     memset(q, 0, sizeof *q);
     *ws_bytes = 0;
     const int cu = (c && c->cores > 0) ? c->cores : 256;
     const int NB = N / 16;
-    int stream = M <= 64;
     const char *force = getenv("ORK_PLAN");
-    if (force && !strcmp(force, "tiled")) stream = 0;
-    if (force && !strcmp(force, "stream") && M <= 64) stream = 1;
+    const int f_stream = force && !strcmp(force, "stream"), f_tiled = force && !strcmp(force, "tiled");
+    const char *fks = getenv("ORK_KSPLIT");
+    int ks_force = fks ? atoi(fks) : 0;
+    if (ks_force > KB) ks_force = KB;
+    if (ks_force > 0) ks_force = cdiv(KB, cdiv(KB, ks_force)); /* as a split can realise it */
 
-    if (stream) {
-        /* M = 1 takes the VALU-dot GEMV (same grid and fields); ORK_PLAN=stream keeps the MFMA kernel. */
-        q->algo = (M == 1 && !(force && !strcmp(force, "stream"))) ? ORKH_ALGO_GEMV : ORKH_ALGO_STREAM;
-        q->mt = cdiv(M, 16);
-        /* Run length per wave: 8 KiB in flight per wave for the int8/fp16 GEMV (M = 1); more waves with
-         * shorter runs where each block costs more issue (more rows, int4 decode). Measured on the
-         * K=2048, N=6144 panels; the run lengths on either side were within 2-4%. */
-        const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
-        const int need = cdiv(KB, kbw_target); /* waves per panel at the target run length */
-        const int wpg = need <= 4 ? 4 : 8;
-        /* K is split across workgroups only when the panels leave the machine underfilled (< 4 waves
-         * per CU) AND each wave would otherwise stream more than two runs back to back: the split
-         * costs a second launch (the fixed-order reduce, ~2 us), which a one-run wave never repays. */
-        int ksplit = 1;
-        const int runs = cdiv(cdiv(KB, wpg), kbw_target);
-        if ((long)NB * wpg < 4L * cu && runs > 2) {
-            ksplit = cdiv(4 * cu, NB * wpg);
-            if (ksplit > runs) ksplit = runs; /* every wave keeps a full run */
-        }
-        const char *fks = getenv("ORK_KSPLIT");
-        if (fks && atoi(fks) > 0) ksplit = atoi(fks);
-        if (ksplit > KB) ksplit = KB;
-        if (ksplit < 1) ksplit = 1;
-        const int kbs = cdiv(KB, ksplit);
-        ksplit = cdiv(KB, kbs);
-        q->wpg = wpg;
-        q->kbs = kbs;
-        q->kbw = cdiv(kbs, wpg);
-        q->ksplit = ksplit;
-        if (ksplit > 1) *ws_bytes = (size_t)ksplit * M * N * 4;
-        return 0;
-    }
-
-    const char *tf = getenv("ORK_TILE"); /* testing / A-B: "BMxBN" forces that tile of the LDS-ring kernel */
+    const char *tf = getenv("ORK_TILE"); /* "BMxBN": that tile of the LDS-ring kernel, at any M */
     int fbm, fbn;
     if (tf && sscanf(tf, "%dx%d", &fbm, &fbn) == 2) {
-        const char *fks2 = getenv("ORK_KSPLIT");
-        int ks = fks2 ? atoi(fks2) : 1;
-        if (ks < 1) ks = 1;
-        if (ks > KB) ks = KB;
+        const int ks = ks_force > 0 ? ks_force : 1;
         q->algo = ORKH_ALGO_TILED2;
         q->bm = fbm;
         q->bn = fbn;
@@ -78,43 +151,37 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }
-    const char *fks = getenv("ORK_KSPLIT");
-    int ks_force = fks ? atoi(fks) : 0;
-    if (ks_force > 0) ks_force = cdiv(KB, cdiv(KB, ks_force < KB ? ks_force : KB)); /* as a split can realise it */
-    double best = -1;
 
-    /* The LDS-ring kernel (k_tiled2) for int8, fp16 and uniform int4. Each workgroup is bound by how fast its
-     * operand tiles reach the CU (measured ~15 B/clk per CU, i.e. ~0.027 us per KiB) plus ~1.5 us of
-     * set-up, so a round of workgroups costs about 1.5 + 0.027 * (A + B + C KiB of one workgroup) us.
-     * Measured on K=2048..6144, M=128..4096 int8 / fp16 / W4A4 shapes to within ~15%. A K split adds
-     * the partials' round trip and the reduce launch (~3 us + 2 * ks * M * N * 4 B at 4 TB/s).
-     * NF4 keeps k_tiled: four waves share each decoded B block here, and the codebook decode is not
-     * cheap enough to repeat. */
-    if (rkind != ORKH_NF4 && !(force && !strcmp(force, "tiled"))) {
-        static const int cfg2[][2] = {{256, 256}, {128, 128}, {64, 192}, {64, 64}};
-        const int kpb = rkind == ORKH_I8 ? 64 : rkind == ORKH_F16 ? 32 : 128;
-        const int abpk = rkind == ORKH_F16 ? 2 * kpb : kpb; /* A bytes per row per K-block */
-        for (int i = 0; i < 4; i++) {
-            const int bm = cfg2[i][0], bn = cfg2[i][1];
-            const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);
-            for (int ks = ks_force > 0 ? ks_force : 1; ks <= (ks_force > 0 ? ks_force : 8); ks *= (ks_force > 0 ? 8 : 2)) {
-                const int kbs = cdiv(KB, ks);
-                if (ks_force <= 0 && (cdiv(KB, kbs) != ks || (ks > 1 && kbs < 4))) continue;
-                const long wgs = tiles * ks;
-                const long rounds = (wgs + cu - 1) / cu;
-                const double kib = ((double)bm * abpk * kbs + (double)bn / 16 * 1024 * kbs + (double)bm * bn * 4) / 1024;
-                double t = rounds * (1.5 + 0.027 * kib);
-                if (ks > 1) t += 3.0 + 2.0 * ks * (double)M * N * 4 / 4e6;
-                if (best < 0 || t < best - 1e-9) {
-                    best = t;
-                    q->algo = ORKH_ALGO_TILED2;
-                    q->bm = bm;
-                    q->bn = bn;
-                    q->ksplit = ks;
-                    q->kbs = kbs;
-                }
+    if (M <= 64 && !f_tiled) {
+        int ks;
+        if (M == 1 || f_stream || ks_force > 0 || rkind == ORKH_NF4) {
+            ks = ks_force > 0 ? ks_force : stream_rule_ks(rkind, M, KB, NB, cu);
+        } else {
+            /* both kernels priced, each at its best split; the streaming kernel wins ties */
+            ks = 1;
+            double ts = stream_us(rkind, M, N, KB, cu, 1);
+            for (int k = 2; k <= 8; k *= 2) {
+                if (cdiv(KB, cdiv(KB, k)) != k || cdiv(KB, k) < 4) continue;
+                const double t = stream_us(rkind, M, N, KB, cu, k);
+                if (t < ts - 1e-9) { ts = t; ks = k; }
+            }
+            orkh_plan t2;
+            memset(&t2, 0, sizeof t2);
+            if (tiled2_best(rkind, M, N, KB, cu, 0, &t2) < ts - 1e-9) {
+                *q = t2;
+                if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
+                return 0;
             }
         }
+        /* M = 1 takes the VALU-dot GEMV (same grid and fields); ORK_PLAN=stream keeps the MFMA kernel. */
+        q->algo = (M == 1 && !f_stream) ? ORKH_ALGO_GEMV : ORKH_ALGO_STREAM;
+        stream_geom(rkind, M, KB, ks, q);
+        if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
+        return 0;
+    }
+
+    if (rkind != ORKH_NF4 && !f_tiled) {
+        tiled2_best(rkind, M, N, KB, cu, ks_force, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }
@@ -123,10 +190,12 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
      * rate, so the time of a round of workgroups is about the operand bytes one workgroup loads. K is split
      * across workgroups when that cuts the per-workgroup bytes by more than the partial sums and the extra
      * reduce launch (~2 us) cost. Model units: us at ~48 KB/us per CU (measured order of magnitude),
-     * 5 TB/s for the partials' HBM round trip. */
+     * 5 TB/s for the partials' HBM round trip. NF4 stays here: four waves share each decoded B block, and
+     * the codebook decode is not cheap enough to repeat in every wave as k_tiled2 would. */
     static const int cfg[][2] = {{128, 96}, {128, 128}, {64, 64}};
     const int bpk = 64;                                                  /* B bytes per column per K-block, every kind */
     const int apk = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 128 : 64; /* A bytes per row per K-block */
+    double best = -1;
     for (int i = 0; i < 3; i++) {
         const int bm = cfg[i][0], bn = cfg[i][1];
         const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);

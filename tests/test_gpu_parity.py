@@ -481,3 +481,61 @@ def test_lds_ring_tiles_all_kinds(npu, tile, ks):
     assert rc == 0 and rc2 == 0 and np.array_equal(C1, C2)
     assert O.fp16_err(C1, O.gemm_f16_f64acc(Ah, Bh)) <= FP16_TOL
     ork.free(w)
+
+
+@pytest.mark.parametrize("tile", ["64x192", "64x64"])
+@pytest.mark.parametrize("M", [1, 5, 17, 48, 64])
+def test_lds_ring_small_m(npu, tile, M):
+    """The LDS-ring kernel below one tile height (the planner takes it from M = 24 on wide or long-K
+    shapes): rows past M are zero-filled loads and unwritten C rows. int8 exact, unsplit and split; fp16
+    within the bar."""
+    _say("lds-ring small M", tile, M)
+    rng = np.random.default_rng(M * 7 + len(tile))
+    K, N = 2080, 224
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    w = npu.pack_i8(B)
+    for ks in (1, 2):
+        with _env(ORK_TILE=tile, ORK_KSPLIT=ks):
+            rc, C = npu.run_i8(w, A)
+            name = npu.plan_name(w, M)
+        assert name.startswith("tiled2_i8_" + tile), name
+        assert rc == 0 and np.array_equal(C, O.gemm_i32(A, B)), name
+    ork.free(w)
+    Ah = rng.standard_normal((M, 1056)).astype(np.float16)
+    Bh = (rng.standard_normal((1056, 224)) * 0.02).astype(np.float16)
+    w = npu.pack_f16(Bh)
+    with _env(ORK_TILE=tile):
+        rc, C = npu.run_f16(w, Ah)
+    assert rc == 0 and O.fp16_err(C, O.gemm_f16_f64acc(Ah, Bh)) <= FP16_TOL
+    ork.free(w)
+
+
+@pytest.mark.parametrize("kind,K,N,M", [("i8", 2048, 6144, 48), ("i8", 6144, 2048, 64), ("i4a8", 2048, 6144, 64),
+                                        ("f16", 2048, 6144, 32), ("i8", 2048, 22016, 24)])
+def test_planner_mid_m_default(npu, kind, K, N, M):
+    """Default plans at 17 <= M <= 64 where the time model prefers the LDS-ring kernel (possibly K-split):
+    results as exact as every other route."""
+    _say("planner mid-M", kind, K, N, M)
+    rng = np.random.default_rng(K + N + M)
+    if kind == "f16":
+        Ah = rng.standard_normal((M, K)).astype(np.float16)
+        Bh = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+        w = npu.pack_f16(Bh)
+        rc, C = npu.run_f16(w, Ah)
+        assert npu.plan_name(w, M).startswith("tiled2_"), npu.plan_name(w, M)
+        assert rc == 0 and O.fp16_err(C, O.gemm_f16_f64acc(Ah, Bh)) <= FP16_TOL
+        ork.free(w)
+        return
+    A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    if kind == "i8":
+        B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+        w = npu.pack_i8(B)
+    else:
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        w, _ = npu.pack_i4a8(W)
+        _, _, B = O.pack_i4a8(W)
+    rc, C = npu.run_i8(w, A)
+    assert npu.plan_name(w, M).startswith("tiled2_"), npu.plan_name(w, M)
+    assert rc == 0 and np.array_equal(C, O.gemm_i32(A, B)), npu.plan_name(w, M)
+    ork.free(w)
