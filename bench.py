@@ -351,23 +351,66 @@ def copy_calibration(hip, L, reps=96):
         print(f"[bench] copy calibration: {reps} device copies of {nbytes} bytes", file=sys.stderr, flush=True)
 
 
+def cpu_model():
+    """The host CPU's model name and logical CPU count (reported beside every CPU number)."""
+    name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return f"{name}, {os.cpu_count()} logical CPUs"
+
+
+def _time_calls(fn, budget_s):
+    fn()
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
+
+
 def cpu_baseline(W_codes, A_row, budget_s):
     """The reference's own CPU GEMM (orki_cpu_gemm_i32 from oracle/_ref) single-threaded on M=1 calls of
-    the same workload, for ~budget_s seconds. Falls back to the oracle restatement if _ref is absent."""
+    the same workload, for ~budget_s seconds. Falls back to the oracle restatement if _ref is absent.
+    M = 1 is single-threaded in the reference whatever the build (its pragma is `if(M>1)`)."""
     import oracle as O
 
     kind = "reference" if O.ref_available() else "port"
     fn = O.ref_gemm_i32 if kind == "reference" else O.gemm_i32
-    fn(A_row, W_codes)
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        fn(A_row, W_codes)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
+    dt, n = _time_calls(lambda: fn(A_row, W_codes), budget_s)
     return {"value": round(algo_bytes(1) / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
             "sample": f"{n} M=1 calls of the K=2048,N=6144 int8 GEMM (orki_cpu_gemm_i32 as built, -O2, 1 thread), "
-                      f"{dt * 1e3:.2f} ms/call"}
+                      f"{dt * 1e3:.2f} ms/call; host {cpu_model()}"}
+
+
+def cpu_baseline_m512(W_codes, A512, budget_s):
+    """The M=512 GEMM on the host with the reference's own orki_cpu_gemm_i32: one thread (the library as the
+    reference builds it) on a 16-row sample of the same A -- its rows are independent k-outer AXPY passes, so
+    the time scales by 512/16 -- and, from the -fopenmp build of the same sources, full M=512 calls with the
+    row-parallel pragma (src/npu/core/buf.c:438) on every host thread. ~budget_s seconds each."""
+    import oracle as O
+
+    if not O.ref_available():
+        dt, n = _time_calls(lambda: O.gemm_i32(A512[:16], W_codes), budget_s)
+        return {"value": round(algo_ops(512) / (dt * 32) / 1e12, 5), "unit": "TOP/s", "cores": 1, "kind": "port",
+                "sample": f"{n} calls of 16 rows of the M=512 GEMM (oracle restatement, 1 thread), x32 rows"}
+    dt1, n1 = _time_calls(lambda: O.ref_gemm_i32(A512[:16], W_codes), budget_s)
+    out = {"value": round(algo_ops(512) / (dt1 * 32) / 1e12, 5), "unit": "TOP/s", "cores": 1, "kind": "reference",
+           "sample": f"{n1} calls of 16 rows of the M=512 K=2048 N=6144 GEMM (orki_cpu_gemm_i32 as built, -O2, "
+                     f"1 thread), {dt1 * 1e3:.1f} ms per 16 rows, scaled to 512 rows; host {cpu_model()}"}
+    if O.ref_omp_available():
+        threads = O.ref_omp().ref_threads()
+        dtm, nm = _time_calls(lambda: O.ref_gemm_i32(A512, W_codes, omp=True), budget_s)
+        out["all_cores"] = {"value": round(algo_ops(512) / dtm / 1e12, 5), "unit": "TOP/s", "cores": threads,
+                            "kind": "reference",
+                            "sample": f"{nm} full M=512 calls, orki_cpu_gemm_i32 built with -fopenmp (its row-parallel "
+                                      f"pragma live), {threads} threads, {dtm * 1e3:.1f} ms/call"}
+    return out
 
 
 def traffic_from_profiles(kernel_tag):
@@ -547,6 +590,7 @@ def main():
         out["configs"] = configs
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(codes, A512[:1], args.cpu_seconds)
+        out["m512"]["cpu_baseline"] = cpu_baseline_m512(codes, A512, args.cpu_seconds / 2)
     print(json.dumps(out), flush=True)
 
 

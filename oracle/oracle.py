@@ -11,10 +11,12 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "_build", "libork_oracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libork_ref.so")
+REF_OMP_SO = os.path.join(HERE, "_ref", "libork_ref_omp.so")
 
 _P = C.c_void_p
 _lib = None
 _ref = None
+_ref_omp = None
 
 
 def _ptr(a):
@@ -72,20 +74,41 @@ def ref_available():
     return os.path.exists(REF_SO)
 
 
+def _load_ref(path):
+    R = C.CDLL(path)
+    R.ref_gemm_i32.argtypes = [C.c_int, C.c_int, C.c_int, _P, _P, _P]
+    R.ref_i4_quant_chan.argtypes = [_P, C.c_int, C.c_float, C.c_int, _P, _P, _P]
+    R.ref_i4_expand_chan_to_i8.argtypes = [_P, C.c_int, _P]
+    R.ref_gemm_grouped.argtypes = [C.c_int] * 4 + [_P] * 5
+    R.ref_gemm_grouped.restype = C.c_int
+    R.ref_threads.restype = C.c_int
+    return R
+
+
 def ref():
-    """The reference's own CPU functions, compiled from its sources (oracle/ref.mk)."""
+    """The reference's own CPU functions, compiled from its sources (oracle/ref.mk), single-threaded as the
+    reference library is built."""
     global _ref
     if _ref is None:
         if not ref_available():
             raise RuntimeError(f"reference library not built: {REF_SO}")
-        R = C.CDLL(REF_SO)
-        R.ref_gemm_i32.argtypes = [C.c_int, C.c_int, C.c_int, _P, _P, _P]
-        R.ref_i4_quant_chan.argtypes = [_P, C.c_int, C.c_float, C.c_int, _P, _P, _P]
-        R.ref_i4_expand_chan_to_i8.argtypes = [_P, C.c_int, _P]
-        R.ref_gemm_grouped.argtypes = [C.c_int] * 4 + [_P] * 5
-        R.ref_gemm_grouped.restype = C.c_int
-        _ref = R
+        _ref = _load_ref(REF_SO)
     return _ref
+
+
+def ref_omp_available():
+    return os.path.exists(REF_OMP_SO)
+
+
+def ref_omp():
+    """The same functions built with -fopenmp: orki_cpu_gemm_i32's row-parallel pragma
+    (src/npu/core/buf.c:438) runs on ref_omp().ref_threads() host threads."""
+    global _ref_omp
+    if _ref_omp is None:
+        if not ref_omp_available():
+            raise RuntimeError(f"reference OpenMP library not built: {REF_OMP_SO}")
+        _ref_omp = _load_ref(REF_OMP_SO)
+    return _ref_omp
 
 
 FNV_OFFSET = 1469598103934665603
@@ -109,13 +132,14 @@ def gemm_i32(A, B, naive=False):
     return Cm
 
 
-def ref_gemm_i32(A, B):
+def ref_gemm_i32(A, B, omp=False):
+    """orki_cpu_gemm_i32 as the reference builds it (omp=False: one thread) or with its OpenMP pragma live."""
     A = np.ascontiguousarray(A, dtype=np.int8)
     B = np.ascontiguousarray(B, dtype=np.int8)
     M, K = A.shape
     N = B.shape[1]
     Cm = np.empty((M, N), dtype=np.int32)
-    ref().ref_gemm_i32(M, K, N, _ptr(A), _ptr(B), _ptr(Cm))
+    (ref_omp() if omp else ref()).ref_gemm_i32(M, K, N, _ptr(A), _ptr(B), _ptr(Cm))
     return Cm
 
 

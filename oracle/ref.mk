@@ -29,6 +29,25 @@ $(OUT)/ref_driver.o: $(HERE)ref_driver.c
 	mkdir -p $(OUT)
 	$(CLANG) $(CFLAGS) -c $< -o $@
 
+# The same translation units with -fopenmp: the reference's `#pragma omp parallel for ... if(M>1)` over rows
+# (src/npu/core/buf.c:438) becomes live, as in the reference Makefile's OpenMP tool targets (:192). This is the
+# all-cores CPU baseline; libomp comes from the ROCm LLVM tree (rpath below).
+OMPLIB  := /opt/rocm/llvm/lib
+OMPOBJS := $(OUT)/omp/buf.o $(OUT)/omp/quant.o $(OUT)/omp/ref_driver.o
+$(OUT)/libork_ref_omp.so: $(OMPOBJS)
+	echo '{ global: ref_*; local: *; };' > $(OUT)/ref.map
+	$(CLANG) -shared -fuse-ld=lld -fopenmp -Wl,--gc-sections -Wl,--version-script=$(OUT)/ref.map -Wl,-z,defs \
+	    -L$(OMPLIB) -Wl,-rpath,$(OMPLIB) -o $@ $(OMPOBJS) -lm -pthread
+$(OUT)/omp/buf.o: $(REF)/src/npu/core/buf.c
+	mkdir -p $(OUT)/omp
+	$(CLANG) $(CFLAGS) -fopenmp -c $< -o $@
+$(OUT)/omp/quant.o: $(REF)/src/npu/i4/quant.c
+	mkdir -p $(OUT)/omp
+	$(CLANG) $(CFLAGS) -fopenmp -c $< -o $@
+$(OUT)/omp/ref_driver.o: $(HERE)ref_driver.c
+	mkdir -p $(OUT)/omp
+	$(CLANG) $(CFLAGS) -fopenmp -c $< -o $@
+
 # The reference's own example/test program examples/quant.c, compiled UNMODIFIED from the reference tree
 # against this repository's drop-in header (include/ork_npu.h) and linked to libork_npu.so: a C consumer
 # of the reference API running on the MI355X engine, checked by its own embedded FNV-64 goldens.

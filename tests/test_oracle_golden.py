@@ -64,6 +64,8 @@ def test_gemm_vs_naive_and_reference():
         assert np.array_equal(C, A.astype(np.int64) @ B.astype(np.int64))
         if O.ref_available():
             assert np.array_equal(C, O.ref_gemm_i32(A, B)), (M, K, N)
+        if O.ref_omp_available():  # the -fopenmp build (the CPU baseline's all-cores leg): same integers
+            assert np.array_equal(C, O.ref_gemm_i32(A, B, omp=True)), (M, K, N)
 
 
 def test_gemm_int8_extremes_closed_form():
