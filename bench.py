@@ -227,9 +227,13 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
     for M in (1, 256):
         g, _ = measure(npu, hip, wg4, M, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run_grouped", dS4)
         nbytes = K4 * N4 // 2 + M * K4 + 4 * (M * Sk4 + Sk4 * N4) + 4 * M * N4
-        rec("grouped W4A4 K=N=4096 G=128", "grouped_i4u", M, g, nbytes, 2 * M * N4 * K4,
+        rec("grouped W4A4 K=N=4096 G=128", npu.grouped_plan_name(wg4[0], M), M, g, nbytes, 2 * M * N4 * K4,
             "hbm" if M <= 16 else "mfma_int8")
     L.ork_npu_set_async(npu.h, 0)
+    Cg = np.empty((256, N4), np.float32)  # what the timed M=256 launches wrote (every copy holds B4)
+    assert L.ork_dev_download(npu.h, ork.ptr(Cg), dC, Cg.nbytes) == 0
+    rows = np.r_[0:2, 254:256]
+    assert np.array_equal(Cg[rows], O.gemm_grouped(A4[rows], B4, aS4[rows], bS4, G4)), "grouped W4A4 M=256 spot check"
     Cg = np.empty((4, N4), np.float32)
     assert L.ork_i4_mm_run_grouped(npu.h, wg4[0], 4, dA4, dS4[0], dS4[1], dC) == 0
     assert L.ork_dev_download(npu.h, ork.ptr(Cg), dC, Cg.nbytes) == 0
@@ -248,7 +252,7 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
     assert all(wg8) and all(dS8)
     assert all(L.ork_dev_upload(npu.h, d, ork.ptr(a), a.nbytes) == 0 for d, a in zip(dS8, (aS8, bS8)))
     g, _ = measure(npu, hip, wg8, M8, dA, dC, steps_for(0.01), 16, "ork_i8_mm_run_grouped", dS8)
-    rec("grouped int8 (W4A4 pack) K=2048 N=16384 G=512", "grouped_i4u", M8, g,
+    rec("grouped int8 (W4A4 pack) K=2048 N=16384 G=512", npu.grouped_plan_name(wg8[0], M8), M8, g,
         K8 * N8 // 2 + M8 * K8 + 4 * (M8 * 4 + 4 * N8) + 4 * M8 * N8, 2 * M8 * N8 * K8, "hbm")
     for w in wg8:
         L.ork_mm_free(npu.h, w)

@@ -21,4 +21,7 @@ int          ork_npu_sync(ork_npu *ctx);
 void        *ork_npu_stream(ork_npu *ctx);
 /* Name of the kernel variant the planner picks for (kind of w, M); for diagnostics and profiling. */
 const char  *ork_w_plan_name(ork_npu *ctx, const ork_w *w, int M);
+/* The same for a grouped-scale run (ork_i8_mm_run_grouped / ork_i4_mm_run_grouped) of w at M rows:
+ * "grouped_<kind>_mt<n>" (panel streaming) or "tiled2g_<kind>_<BM>x<BN>"; "none" without a group size. */
+const char  *ork_w_grouped_plan_name(ork_npu *ctx, const ork_w *w, int M);
 #endif

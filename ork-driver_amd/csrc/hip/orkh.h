@@ -115,10 +115,14 @@ typedef struct orkh_group {
     orkh_gtask t[ORKH_GROUP_MAX];
 } orkh_group;
 /* Grouped run: C[m][n] = sum over K-groups g ascending of ((float)P_g[m][n] * aS[m*(K/G)+g]) * bS[g*N+n],
- * P_g the exact int32 partial of group g. Integer kinds only; G % 32 == 0, K % G == 0.
- * 0 / -2 bad arguments / -1 HIP error. */
-int orkh_mm_launch_grouped(const orkh_mm *p, int G, const float *aS, const float *bS, float *C, int ldc, void *stream);
+ * P_g the exact int32 partial of group g. Integer kinds only; G % 32 == 0, K % G == 0. plan->algo selects
+ * the panel-streaming k_grouped (ORKH_ALGO_STREAM) or the LDS-ring tile k_tiled2g (ORKH_ALGO_TILED2, bm x bn;
+ * int8 and uniform int4). 0 / -2 bad arguments / -1 HIP error. */
+int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *plan, int G, const float *aS, const float *bS, float *C,
+                           int ldc, void *stream);
 int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream);
+/* Bytes of LDS the stage ring of k_tiled2 takes for (kind, bm x bn); -1 for a tile that is not built. */
+int orkh_tiled2_ring_lds(int kind, int bm, int bn);
 /* Names of the compiled kernel variants, for diagnostics ("stream_i8_mt1_w4", ...). */
 const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *plan);
 

@@ -466,8 +466,18 @@ template <int KIND, int BM, int BN, int KS> struct T2 {
     static_assert(MB % WM == 0 && NB % WN == 0 && R >= 2 && (R - 2) * IPW < 64, "tile");
 };
 
-template <int KIND, int BM, int BN, int KS>
-__global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntiles_all, int kbs, void *ws) {
+// Grouped mode of k_tiled2 (ork_*_mm_run_grouped): C is fp32 and every output is the sum, in ascending g, of
+// ((float)P_g * aS[m][g]) * bS[g][n] with P_g the exact int32 partial over K-group g (src/npu/core/buf.c:501-520).
+struct T2Group {
+    int G;            // group size in k; G % 32 == 0 and K % G == 0
+    const float *aS;  // [M][K/G]
+    const float *bS;  // [K/G][N]
+};
+
+template <int KIND, int BM, int BN, int KS, int GR>
+__device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int ntiles_all, int kbs, void *ws,
+                                            const T2Group &gp) {
+#pragma clang fp contract(off)
     using T = KT<KIND>;
     using P = T2<KIND, BM, BN, KS>;
     constexpr int R = P::R;
@@ -538,6 +548,64 @@ __global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntil
 #pragma unroll
         for (int b = 0; b < P::NTW; b++) acc[a][b] = acc_t{0, 0, 0, 0};
 
+    // grouped mode: fp32 running sums, and this tile's scales in LDS after the ring -- aS rows m0.. (BM x Sk,
+    // one contiguous run of aS) and bS columns n0.. of every group (Sk x BN) -- brought in by direct-to-LDS
+    // loads issued before the ring's, so the first stage's wait covers them and no later wait drains the
+    // ring. Rows past M read zeros and columns past N read a neighbouring row; neither is stored.
+    const int Sk = GR ? p.K / gp.G : 1;
+    const int sca_kib = GR ? (BM * Sk * 4 + 1023) / 1024 : 0;
+    const int scb_kib = GR ? (Sk * BN * 4 + 1023) / 1024 : 0;
+    const float *sAl = (const float *)(sm + P::LDS / 16);
+    const float *sBl = sAl + sca_kib * 256;
+    float cacc[P::MTW][P::NTW][4];
+    float sa[P::MTW][4], sb[P::NTW]; // scales of the next group to close
+    int gcur = 0, gend = GR ? gp.G : 0; // that group and the k where it ends
+    const int gps = GR == 2 ? gp.G / (KS * T::KPB) : 1; // stages per group (groups of whole stages)
+    int sgs = 0;                                          // stages of the current group done
+    auto load_sc = [&](int g) {
+#pragma unroll
+        for (int i = 0; i < P::MTW; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sa[i][r] = sAl[((wm * P::MTW + i) * 16 + (lane >> 4) * 4 + r) * Sk + g];
+#pragma unroll
+        for (int jn = 0; jn < P::NTW; jn++) sb[jn] = sBl[g * BN + (wn * P::NTW + jn) * 16 + (lane & 15)];
+    };
+    // close group gcur: its exact partial, scaled, joins the fp32 sums in group order; read the next scales
+    auto close_group = [&]() {
+#pragma unroll
+        for (int i = 0; i < P::MTW; i++)
+#pragma unroll
+            for (int jn = 0; jn < P::NTW; jn++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float t = ((float)finish<KIND>(acc[i][jn][r]) * sa[i][r]) * sb[jn];
+                    cacc[i][jn][r] = cacc[i][jn][r] + t;
+                    acc[i][jn][r] = 0;
+                }
+        gcur++;
+        if (gcur < Sk) load_sc(gcur); // read ahead: waited for at the next close
+    };
+    if constexpr (GR) {
+#pragma unroll
+        for (int i = 0; i < P::MTW; i++)
+#pragma unroll
+            for (int jn = 0; jn < P::NTW; jn++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) cacc[i][jn][r] = 0.0f;
+        const uint32_t scl = lds0 + (uint32_t)P::LDS;
+        const __amdgpu_buffer_rsrc_t Sa = make_rsrc(gp.aS, (uint32_t)p.M * Sk * 4u);
+        const __amdgpu_buffer_rsrc_t Sb = make_rsrc(gp.bS, (uint32_t)Sk * p.N * 4u);
+        for (int i = wv; i < sca_kib + scb_kib; i += P::NW) {
+            if (i < sca_kib) {
+                lds_dma16(Sa, (uint32_t)m0 * Sk * 4u + (uint32_t)i * 1024u + lane * 16u, scl + i * 1024);
+            } else {
+                const int f = (i - sca_kib) * 256 + lane * 4; // first float of this lane within the Sk x BN tile
+                const int g = f / BN, c = f - g * BN;
+                lds_dma16(Sb, g < Sk ? ((uint32_t)g * p.N + nb0 * 16 + c) * 4u : OOB, scl + i * 1024);
+            }
+        }
+    }
+
 #pragma unroll
     for (int st = 0; st < R - 1; st++) issue(st);
     for (int s = 0; s < nst; s++) {
@@ -546,26 +614,78 @@ __global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntil
         issue(s + R - 1); // into the slot of stage s - 1, which every wave finished before the barrier
         const v4i *As = sm + (s % R) * (P::SLOT / 16);
         const v4i *Bs = As + P::NIA * 64;
+        if constexpr (GR) {
+            if (s == 0) load_sc(0); // the scales landed with stage 0 (older loads, same wait)
+        }
+        if constexpr (GR != 1) {
 #pragma unroll
-        for (int kbl = 0; kbl < KS; kbl++) {
-            v4i op[P::NTW][T::STEPS];
+            for (int kbl = 0; kbl < KS; kbl++) {
+                v4i op[P::NTW][T::STEPS];
 #pragma unroll
-            for (int jn = 0; jn < P::NTW; jn++) decode<KIND>(Bs[((wn * P::NTW + jn) * KS + kbl) * 64 + lane], op[jn], L);
+                for (int jn = 0; jn < P::NTW; jn++) decode<KIND>(Bs[((wn * P::NTW + jn) * KS + kbl) * 64 + lane], op[jn], L);
 #pragma unroll
-            for (int st = 0; st < T::STEPS; st++)
+                for (int st = 0; st < T::STEPS; st++)
 #pragma unroll
-                for (int i = 0; i < P::MTW; i++) {
-                    const v4i a = As[(((wm * P::MTW + i) * KS + kbl) * T::STEPS + st) * 64 + lane];
+                    for (int i = 0; i < P::MTW; i++) {
+                        const v4i a = As[(((wm * P::MTW + i) * KS + kbl) * T::STEPS + st) * 64 + lane];
 #pragma unroll
-                    for (int jn = 0; jn < P::NTW; jn++) acc[i][jn] = mma(a, op[jn][st], acc[i][jn]);
+                        for (int jn = 0; jn < P::NTW; jn++) acc[i][jn] = mma(a, op[jn][st], acc[i][jn]);
+                    }
+            }
+        }
+        if constexpr (GR == 2) {
+            // groups of whole stages: the stage ran as in the plain kernel; close the group it ends
+            if (++sgs == gps) {
+                sgs = 0;
+                close_group();
+            }
+        }
+        if constexpr (GR == 1) {
+            // every fragment of the stage is read first, as above, so the LDS latencies overlap; then the
+            // K-blocks run group by group. A 16-k A chunk lies wholly inside one group (G % 32 == 0).
+            v4i afr[KS][T::STEPS][P::MTW], bop[KS][P::NTW][T::STEPS];
+#pragma unroll
+            for (int kbl = 0; kbl < KS; kbl++) {
+#pragma unroll
+                for (int jn = 0; jn < P::NTW; jn++)
+                    decode<KIND>(Bs[((wn * P::NTW + jn) * KS + kbl) * 64 + lane], bop[kbl][jn], L);
+#pragma unroll
+                for (int st = 0; st < T::STEPS; st++)
+#pragma unroll
+                    for (int i = 0; i < P::MTW; i++)
+                        afr[kbl][st][i] = As[(((wm * P::MTW + i) * KS + kbl) * T::STEPS + st) * 64 + lane];
+            }
+#pragma unroll
+            for (int kbl = 0; kbl < KS; kbl++) {
+                const int kb = kb_lo + s * KS + kbl;
+                if (kb >= kb_hi) break;
+                const int kb_k0 = kb * T::KPB, kb_k1 = min(kb_k0 + T::KPB, p.K);
+                // the groups meeting [kb_k0, kb_k1) in order, from the running group gcur (no division: a
+                // division per block on every wave saturates the CU's scalar unit)
+                for (;;) {
+                    const int ghi = gend, glo = gend - gp.G;
+                    const bool whole = glo <= kb_k0 && ghi >= kb_k1;
+#pragma unroll
+                    for (int st = 0; st < T::STEPS; st++) {
+                        const int kk = kb_k0 + a_koff<KIND>(st, lane >> 4);
+                        const bool in = whole || (kk >= glo && kk < ghi);
+#pragma unroll
+                        for (int i = 0; i < P::MTW; i++) {
+                            const v4i a = in ? afr[kbl][st][i] : v4i{0, 0, 0, 0};
+#pragma unroll
+                            for (int jn = 0; jn < P::NTW; jn++) acc[i][jn] = mma(a, bop[kbl][jn][st], acc[i][jn]);
+                        }
+                    }
+                    if (ghi > kb_k1) break; // the group runs on into the next block
+                    close_group(); // group gcur closes in this block
+                    gend += gp.G;
+                    if (ghi == kb_k1) break;
                 }
+            }
         }
     }
     wait_vmcnt<0>();
 
-    const bool split = gridDim.x > ntiles_all;
-    c_t *C = split ? (c_t *)ws + (size_t)ks * p.M * p.N : (c_t *)p.C;
-    const size_t ldc = split ? (size_t)p.N : (size_t)p.ldc;
 #pragma unroll
     for (int i = 0; i < P::MTW; i++)
 #pragma unroll
@@ -576,9 +696,30 @@ __global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntil
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + (wm * P::MTW + i) * 16 + (lane >> 4) * 4 + r;
-                if (m < p.M) C[(size_t)m * ldc + n] = finish<KIND>(acc[i][jn][r]);
+                if (m >= p.M) continue;
+                if constexpr (GR) {
+                    ((float *)p.C)[(size_t)m * p.ldc + n] = cacc[i][jn][r];
+                } else {
+                    const bool split = gridDim.x > ntiles_all;
+                    c_t *C = split ? (c_t *)ws + (size_t)ks * p.M * p.N : (c_t *)p.C;
+                    const size_t ldc = split ? (size_t)p.N : (size_t)p.ldc;
+                    C[(size_t)m * ldc + n] = finish<KIND>(acc[i][jn][r]);
+                }
             }
         }
+}
+
+template <int KIND, int BM, int BN, int KS>
+__global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntiles_all, int kbs, void *ws) {
+    tiled2_body<KIND, BM, BN, KS, 0>(p, mtiles, ntiles_all, kbs, ws, T2Group{0, nullptr, nullptr});
+}
+
+// Grouped runs (never K-split: the groups close in order inside one workgroup). GR 2: every group is whole
+// stages (G % (KS * KPB) == 0), so the stage runs as in the plain kernel and a group closes between stages;
+// GR 1: any G % 32 == 0, walked K-block by K-block.
+template <int KIND, int BM, int BN, int KS, int GR>
+__global__ __launch_bounds__(1024) void k_tiled2g(orkh_mm p, int mtiles, int ntiles_all, T2Group gp) {
+    tiled2_body<KIND, BM, BN, KS, GR>(p, mtiles, ntiles_all, p.KB, nullptr, gp);
 }
 
 // Dynamic LDS of k_tiled: KG groups x 2 stage buffers of A fragments, or (KG > 1) the 4-wave partial
@@ -982,26 +1123,87 @@ extern "C" int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream) 
     return 0;
 }
 
-extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, int G, const float *aS, const float *bS, float *C, int ldc,
-                                      void *stream) {
-    hipStream_t s = (hipStream_t)stream;
-    if (G < 32 || G % 32 || p->K % G || p->N % 16 || p->M < 1 || ldc < p->N ||
-        (p->kind != ORKH_I8 && p->kind != ORKH_I4U && p->kind != ORKH_NF4)) {
-        snprintf(g_lerr, sizeof g_lerr, "grouped: kind %d M %d K %d N %d G %d ldc %d", p->kind, p->M, p->K, p->N, G,
-                 ldc);
+namespace {
+template <int KIND, int BM, int BN>
+int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s) {
+    constexpr int KS = t2_ks<KIND, BM, BN>();
+    using P = T2<KIND, BM, BN, KS>;
+    const bool whole = gp.G % (KS * KT<KIND>::KPB) == 0;
+    auto kern = whole ? k_tiled2g<KIND, BM, BN, KS, 2> : k_tiled2g<KIND, BM, BN, KS, 1>;
+    const int Sk = p->K / gp.G;
+    const size_t lds = P::LDS + (size_t)((BM * Sk * 4 + 1023) / 1024 + (Sk * BN * 4 + 1023) / 1024) * 1024;
+    if (lds > 163840) {
+        snprintf(g_lerr, sizeof g_lerr, "grouped tiled2 %dx%d: %d groups need %zu B of LDS", BM, BN, Sk, lds);
         return -2;
     }
-    const int MT = p->M > 16 ? 4 : 1;
-    const dim3 grid((unsigned)(p->N / 16), (unsigned)((p->M + 16 * MT - 1) / (16 * MT))), block(256);
+    static bool attr[2] = {false, false}; // per instantiation: allow up to 160 KiB of dynamic LDS
+    if (!attr[whole]) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840) != hipSuccess)
+            return -1;
+        attr[whole] = true;
+    }
+    const int mtiles = (p->M + BM - 1) / BM;
+    const int ntiles = (p->N / 16 + P::NB - 1) / P::NB;
+    hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(1024), lds, s, *p, mtiles, mtiles * ntiles, gp);
+    return 0;
+}
+
+template <int KIND>
+int launch_tiled2g(const orkh_mm *p, const orkh_plan *q, const T2Group &gp, hipStream_t s) {
+    if (q->bm == 64 && q->bn == 192) return launch_tiled2g_v<KIND, 64, 192>(p, gp, s);
+    if (q->bm == 64 && q->bn == 64) return launch_tiled2g_v<KIND, 64, 64>(p, gp, s);
+    snprintf(g_lerr, sizeof g_lerr, "grouped tiled2 plan: %dx%d unsupported", q->bm, q->bn);
+    return -2;
+}
+} // namespace
+
+extern "C" int orkh_tiled2_ring_lds(int kind, int bm, int bn) {
+#define ORKH_RING(KIND)                                                                                      \
+    if (bm == 64 && bn == 64) return (int)T2<KIND, 64, 64, t2_ks<KIND, 64, 64>()>::LDS;                       \
+    if (bm == 64 && bn == 192) return (int)T2<KIND, 64, 192, t2_ks<KIND, 64, 192>()>::LDS;                    \
+    if (bm == 128 && bn == 128) return (int)T2<KIND, 128, 128, t2_ks<KIND, 128, 128>()>::LDS;                 \
+    if (bm == 256 && bn == 256) return (int)T2<KIND, 256, 256, t2_ks<KIND, 256, 256>()>::LDS;                 \
+    return -1;
+    switch (kind) {
+    case ORKH_I8: ORKH_RING(ORKH_I8)
+    case ORKH_I4U: ORKH_RING(ORKH_I4U)
+    case ORKH_NF4: ORKH_RING(ORKH_NF4)
+    case ORKH_F16: ORKH_RING(ORKH_F16)
+    default: return -1;
+    }
+#undef ORKH_RING
+}
+
+extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *q, int G, const float *aS, const float *bS,
+                                      float *C, int ldc, void *stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (G < 32 || G % 32 || p->K % G || p->N % 16 || p->M < 1 || ldc < p->N ||
+        (p->kind != ORKH_I8 && p->kind != ORKH_I4U && p->kind != ORKH_NF4) ||
+        (q->algo == ORKH_ALGO_TILED2 && p->kind == ORKH_NF4)) {
+        snprintf(g_lerr, sizeof g_lerr, "grouped: kind %d M %d K %d N %d G %d ldc %d algo %d", p->kind, p->M, p->K,
+                 p->N, G, ldc, q->algo);
+        return -2;
+    }
+    if (q->algo == ORKH_ALGO_TILED2) {
+        orkh_mm pc = *p;
+        pc.C = C;
+        pc.ldc = ldc;
+        const T2Group gp = {G, aS, bS};
+        const int rc = p->kind == ORKH_I8 ? launch_tiled2g<ORKH_I8>(&pc, q, gp, s) : launch_tiled2g<ORKH_I4U>(&pc, q, gp, s);
+        if (rc) return rc;
+    } else {
+        const int MT = p->M > 16 ? 4 : 1;
+        const dim3 grid((unsigned)(p->N / 16), (unsigned)((p->M + 16 * MT - 1) / (16 * MT))), block(256);
 #define ORKH_GROUPED_CASE(KIND)                                                                              \
     if (MT == 1) hipLaunchKernelGGL((k_grouped<KIND, 1>), grid, block, 0, s, *p, G, aS, bS, C, ldc);          \
     else hipLaunchKernelGGL((k_grouped<KIND, 4>), grid, block, 0, s, *p, G, aS, bS, C, ldc);
-    switch (p->kind) {
-    case ORKH_I8: ORKH_GROUPED_CASE(ORKH_I8) break;
-    case ORKH_I4U: ORKH_GROUPED_CASE(ORKH_I4U) break;
-    default: ORKH_GROUPED_CASE(ORKH_NF4) break;
-    }
+        switch (p->kind) {
+        case ORKH_I8: ORKH_GROUPED_CASE(ORKH_I8) break;
+        case ORKH_I4U: ORKH_GROUPED_CASE(ORKH_I4U) break;
+        default: ORKH_GROUPED_CASE(ORKH_NF4) break;
+        }
 #undef ORKH_GROUPED_CASE
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_lerr, sizeof g_lerr, "launch: %s", hipGetErrorString(e));

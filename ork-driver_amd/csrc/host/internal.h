@@ -86,6 +86,8 @@ void   orki_tile_nib_kn(const int8_t *B_kn, int K, int N, int KB, uint8_t *out);
 
 /* ---- planner (plan.c) ---- */
 int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes);
+/* Kernel for a grouped-scale run (never K-split). */
+void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB, int G, orkh_plan *q);
 
 /* ---- context helpers (context.c) ---- */
 int   orki_need_device(const ork_npu *c, const char *who);

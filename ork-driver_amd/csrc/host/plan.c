@@ -95,12 +95,12 @@ static double stream_us(int rkind, int M, int N, int KB, int cu, int ks) {
 /* The LDS-ring kernel (k_tiled2): every tile and split on offer priced by the model above; A counts the
  * whole tile height, since rows past M still issue (zero-filled) loads. Returns the modelled time of
  * the best and fills q with it. */
-static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force, orkh_plan *q) {
+static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force, int cfg_from, orkh_plan *q) {
     static const int cfg2[][2] = {{256, 256}, {128, 128}, {64, 192}, {64, 64}};
     const int NB = N / 16;
     const int abpk = a_bytes_per_kb(rkind), kpb = kpb_of(rkind);
     double best = -1;
-    for (int i = 0; i < 4; i++) {
+    for (int i = cfg_from; i < 4; i++) {
         const int bm = cfg2[i][0], bn = cfg2[i][1];
         const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);
         for (int ks = ks_force > 0 ? ks_force : 1; ks <= (ks_force > 0 ? ks_force : 8); ks *= (ks_force > 0 ? 8 : 2)) {
@@ -167,7 +167,7 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
             }
             orkh_plan t2;
             memset(&t2, 0, sizeof t2);
-            if (tiled2_best(rkind, M, N, KB, cu, 0, &t2) < ts - 1e-9) {
+            if (tiled2_best(rkind, M, N, KB, cu, 0, 0, &t2) < ts - 1e-9) {
                 *q = t2;
                 if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
                 return 0;
@@ -181,7 +181,7 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
     }
 
     if (rkind != ORKH_NF4 && !f_tiled) {
-        tiled2_best(rkind, M, N, KB, cu, ks_force, q);
+        tiled2_best(rkind, M, N, KB, cu, ks_force, 0, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }
@@ -218,4 +218,54 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
     q->algo = ORKH_ALGO_TILED;
     if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
     return 0;
+}
+
+/* Grouped-scale runs (ork_*_mm_run_grouped). The groups must close in ascending order inside one workgroup, so
+ * K is never split. Few rows: k_grouped streams each 16-column panel (and re-reads A per panel). With more
+ * rows, int8 and uniform int4 take the LDS-ring kernel at the unsplit 64-row tile (64x192 or 64x64) the time
+ * model prices lowest, when the tile's scales fit in LDS beside its ring (else 64x64, else k_grouped):
+ *   from 32 rows when every group is whole 128-k stages (G % 128 == 0: the stage runs as in the plain kernel
+ *   and a group closes between stages; e.g. W4A4 K=N=4096 G=128: 42.9 -> 21.6 us at M=256);
+ *   from 128 rows otherwise (groups end inside stages and the kernel walks them K-block by K-block).
+ * NF4 stays on k_grouped (its codebook decode would repeat in every wave row).
+ * ORK_PLAN=stream|tiled forces either (tests, A/B). */
+#define ORKI_GROUPED_TILED_M 32
+#define ORKI_GROUPED_TILED_M_PARTIAL 128
+void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB, int G, orkh_plan *q) {
+    memset(q, 0, sizeof *q);
+    const int cu = (c && c->cores > 0) ? c->cores : 256;
+    const char *force = getenv("ORK_PLAN");
+    int tiled = M >= (G % 128 == 0 ? ORKI_GROUPED_TILED_M : ORKI_GROUPED_TILED_M_PARTIAL);
+    if (force && !strcmp(force, "stream")) tiled = 0;
+    if (force && !strcmp(force, "tiled")) tiled = 1;
+    if (tiled && rkind != ORKH_NF4) {
+        const char *tf = getenv("ORK_TILE");
+        int fbm, fbn;
+        if (tf && sscanf(tf, "%dx%d", &fbm, &fbn) == 2) {
+            q->algo = ORKH_ALGO_TILED2;
+            q->bm = fbm;
+            q->bn = fbn;
+        } else {
+            tiled2_best(rkind, M, N, KB, cu, 1, 2, q); /* the 64-row tiles: the larger ones spill with the fp32 sums */
+        }
+        /* the tile's scales (BM x K/G and K/G x BN floats) sit in LDS beside the stage ring */
+        const int Sk = K / G;
+        for (int pass = 0; pass < 2 && q->algo == ORKH_ALGO_TILED2; pass++) {
+            const long sc = ((long)q->bm * Sk * 4 + 1023) / 1024 * 1024 + ((long)Sk * q->bn * 4 + 1023) / 1024 * 1024;
+            const int ring = orkh_tiled2_ring_lds(rkind, q->bm, q->bn);
+            if (ring > 0 && ring + sc <= 163840) {
+                q->ksplit = 1;
+                q->kbs = KB;
+                return;
+            }
+            if (q->bm == 64 && q->bn == 64) break;
+            q->bm = 64; /* the smallest ring */
+            q->bn = 64;
+        }
+        memset(q, 0, sizeof *q);
+    }
+    q->algo = ORKH_ALGO_STREAM;
+    q->mt = M > 16 ? 4 : 1;
+    q->ksplit = 1;
+    q->kbs = KB;
 }

@@ -172,7 +172,9 @@ static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M
     p.B = w->dB;
     p.ldc = N;
     memcpy(p.lut, w->lut, sizeof p.lut);
-    const int rc = orkh_mm_launch_grouped(&p, G, dAS, dBS, dC, N, c->stream);
+    orkh_plan q;
+    orki_plan_grouped(c, w->rkind, M, K, N, w->KB, G, &q);
+    const int rc = orkh_mm_launch_grouped(&p, &q, G, dAS, dBS, dC, N, c->stream);
     if (rc) { orki_hip_fail(who); return -1; }
     if (!c_dev && orkh_d2h(C, dC, cbytes, c->stream)) { orki_hip_fail(who); return -1; }
     if (c->async && a_dev && c_dev && as_dev && bs_dev) return 0;
@@ -197,4 +199,15 @@ const char *ork_w_plan_name(ork_npu *c, const ork_w *w, int M) {
     memset(&p, 0, sizeof p);
     p.kind = w->rkind;
     return orkh_mm_variant(&p, &q);
+}
+
+const char *ork_w_grouped_plan_name(ork_npu *c, const ork_w *w, int M) {
+    static _Thread_local char b[64];
+    if (!c || !w || w->rkind < 0 || w->rkind == ORKH_F16 || M < 1 || w->gsize < 1) return "none";
+    orkh_plan q;
+    orki_plan_grouped(c, w->rkind, M, w->K, w->N, w->KB, w->gsize, &q);
+    const char *k = w->rkind == ORKH_I8 ? "i8" : w->rkind == ORKH_I4U ? "i4u" : "nf4";
+    if (q.algo == ORKH_ALGO_TILED2) snprintf(b, sizeof b, "tiled2g_%s_%dx%d", k, q.bm, q.bn);
+    else snprintf(b, sizeof b, "grouped_%s_mt%d", k, q.mt);
+    return b;
 }

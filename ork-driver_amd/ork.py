@@ -79,6 +79,7 @@ API = {
     "ork_npu_sync": (C.c_int, [_P]),
     "ork_npu_stream": (_P, [_P]),
     "ork_w_plan_name": (C.c_char_p, [_P, _P, C.c_int]),
+    "ork_w_grouped_plan_name": (C.c_char_p, [_P, _P, C.c_int]),
 }
 
 
@@ -213,6 +214,9 @@ class Npu:
 
     def plan_name(self, w, M):
         return lib().ork_w_plan_name(self.h, w, M).decode()
+
+    def grouped_plan_name(self, w, M):
+        return lib().ork_w_grouped_plan_name(self.h, w, M).decode()
 
 
 def dims(w):

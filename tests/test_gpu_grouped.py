@@ -184,3 +184,101 @@ def test_grouped_errors(npu):
     assert L.ork_i4_mm_pack_grouped(npu.h, K, 96, ork.ptr(np.zeros((K, 96), np.int8)), 64) is None  # N % 64
     L.ork_mm_free(npu.h, w)
     L.ork_mm_free(npu.h, wf)
+
+
+def _env_run(env, fn, npu, w, A, aS, bS):
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return _run(fn, npu, w, A, aS, bS)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("tile", [None, "64x64", "64x192"])
+@pytest.mark.parametrize("kind,M,K,N,G", [
+    ("i8", 64, 2048, 256, 128),     # groups of one 128-k stage
+    ("i8", 100, 2080, 224, 160),    # groups end inside stages and K-blocks; K tail mid-block; partial tiles
+    ("i8", 33, 1024, 192, 32),      # two groups per K-block
+    ("i8", 256, 2048, 384, 2048),   # one group
+    ("i8", 70, 2048, 224, 512),     # groups of four stages; partial tiles
+    ("w4a4", 256, 2048, 512, 128),  # one group per K-block (examples/i4.c gtest shape family)
+    ("w4a4", 70, 1056, 320, 96),    # groups straddle the 128-k blocks; K tail; partial tiles
+    ("w4a4", 48, 1024, 128, 32),    # four groups per K-block
+])
+def test_grouped_tiled_exact(npu, tile, kind, M, K, N, G):
+    """The LDS-ring grouped kernel (k_tiled2g; ORK_PLAN=tiled, and ORK_TILE when given) against the oracle bit
+    for bit, and against the panel-streaming k_grouped forced on the same inputs. G % 128 == 0 runs the
+    whole-stage variant, the other group sizes the K-block walk."""
+    _say("grouped tiled", kind, M, K, N, G, tile)
+    L = ork.lib()
+    if kind == "i8":
+        rng = np.random.default_rng(M + K + N + G)
+        B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+        A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+        aS = rng.uniform(1e-3, 1e-2, size=(M, K // G)).astype(np.float32)
+        bS = rng.uniform(1e-3, 1e-2, size=(K // G, N)).astype(np.float32)
+        w = npu.pack_i8(B)
+        assert L.ork_w_set_group(w, G) == 0
+        fn = L.ork_i8_mm_run_grouped
+    else:
+        A, B, aS, bS = _gtest_inputs(M, K, N, G)
+        w = L.ork_i4_mm_pack_grouped(npu.h, K, N, ork.ptr(B), G)
+        assert w
+        fn = L.ork_i4_mm_run_grouped
+    env = {"ORK_PLAN": "tiled", **({"ORK_TILE": tile} if tile else {})}
+    rc, C = _env_run(env, fn, npu, w, A, aS, bS)
+    os.environ.update(env)
+    try:
+        name = npu.grouped_plan_name(w, M)
+    finally:
+        for k in env:
+            os.environ.pop(k, None)
+    assert name.startswith("tiled2g_") and (tile is None or name.endswith(tile)), name
+    assert rc == 0 and np.array_equal(C, O.gemm_grouped(A, B, aS, bS, G)), name
+    rc2, C2 = _env_run({"ORK_PLAN": "stream"}, fn, npu, w, A, aS, bS)
+    assert rc2 == 0 and np.array_equal(C, C2)
+    L.ork_mm_free(npu.h, w)
+
+
+def test_grouped_plan_names(npu):
+    """Default plans: few rows stream panels (k_grouped); int8 / uniform int4 take the LDS-ring kernel from 32
+    rows when G % 128 == 0 and from 128 rows otherwise; NF4 always streams."""
+    L = ork.lib()
+    B = np.zeros((1024, 256), np.int8)
+    w = npu.pack_i8(B)
+    assert npu.grouped_plan_name(w, 8) == "none"  # no group size yet
+    assert L.ork_w_set_group(w, 128) == 0
+    assert npu.grouped_plan_name(w, 8).startswith("grouped_i8_")
+    assert npu.grouped_plan_name(w, 31).startswith("grouped_i8_")
+    assert npu.grouped_plan_name(w, 32).startswith("tiled2g_i8_")
+    assert L.ork_w_set_group(w, 64) == 0
+    assert npu.grouped_plan_name(w, 127).startswith("grouped_i8_")
+    assert npu.grouped_plan_name(w, 128).startswith("tiled2g_i8_")
+    L.ork_mm_free(npu.h, w)
+    W = (np.random.default_rng(1).standard_normal((256, 1024)) * 0.02).astype(np.float32)
+    os.environ["ORK_NF4"] = "1"
+    try:
+        w, _ = npu.pack_i4a8(W)
+    finally:
+        os.environ.pop("ORK_NF4", None)
+    assert L.ork_w_set_group(w, 128) == 0
+    assert npu.grouped_plan_name(w, 256).startswith("grouped_nf4_")
+    L.ork_mm_free(npu.h, w)
+
+
+def test_grouped_default_plan_exact(npu):
+    """The default plan at M = 256 (the LDS-ring kernel) on a grouped W4A4 shape, bit for bit."""
+    _say("grouped default plan W4A4 M=256")
+    L = ork.lib()
+    M, K, N, G = 256, 1024, 512, 128
+    A, B, aS, bS = _gtest_inputs(M, K, N, G)
+    w = L.ork_i4_mm_pack_grouped(npu.h, K, N, ork.ptr(B), G)
+    assert npu.grouped_plan_name(w, M).startswith("tiled2g_i4u_")
+    rc, C = _run(L.ork_i4_mm_run_grouped, npu, w, A, aS, bS)
+    assert rc == 0 and np.array_equal(C, O.gemm_grouped(A, B, aS, bS, G))
+    L.ork_mm_free(npu.h, w)
