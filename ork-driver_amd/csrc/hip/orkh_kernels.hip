@@ -686,25 +686,23 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     }
     wait_vmcnt<0>();
 
+    // epilogue: one 64-bit base per lane (its first row and column), 32-bit offsets from it
+    const int mr0 = m0 + wm * P::MTW * 16 + (lane >> 4) * 4, nc0 = (nb0 + wn * P::NTW) * 16 + (lane & 15);
+    const bool split = !GR && gridDim.x > ntiles_all;
+    const size_t ldc = split ? (size_t)p.N : (size_t)p.ldc;
+    using o_t = typename std::conditional<GR != 0, float, c_t>::type;
+    o_t *Cl = (split ? (o_t *)ws + (size_t)ks * p.M * p.N : (o_t *)p.C) + (size_t)mr0 * ldc + nc0;
 #pragma unroll
     for (int i = 0; i < P::MTW; i++)
 #pragma unroll
         for (int jn = 0; jn < P::NTW; jn++) {
-            const int nbk = nb0 + wn * P::NTW + jn;
-            if (nbk >= NBtot) continue;
-            const int n = nbk * 16 + (lane & 15);
+            if (nb0 + wn * P::NTW + jn >= NBtot) continue;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + (wm * P::MTW + i) * 16 + (lane >> 4) * 4 + r;
-                if (m >= p.M) continue;
-                if constexpr (GR) {
-                    ((float *)p.C)[(size_t)m * p.ldc + n] = cacc[i][jn][r];
-                } else {
-                    const bool split = gridDim.x > ntiles_all;
-                    c_t *C = split ? (c_t *)ws + (size_t)ks * p.M * p.N : (c_t *)p.C;
-                    const size_t ldc = split ? (size_t)p.N : (size_t)p.ldc;
-                    C[(size_t)m * ldc + n] = finish<KIND>(acc[i][jn][r]);
-                }
+                if (mr0 + i * 16 + r >= p.M) continue;
+                const uint32_t off = (uint32_t)(i * 16 + r) * (uint32_t)ldc + (uint32_t)(jn * 16);
+                if constexpr (GR) Cl[off] = cacc[i][jn][r];
+                else Cl[off] = finish<KIND>(acc[i][jn][r]);
             }
         }
 }
