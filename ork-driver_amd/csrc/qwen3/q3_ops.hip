@@ -4,7 +4,7 @@
 // silu, :83-90 the int8 activation round trip, :115-127 flash-style GQA attention; examples/layer.c:21-30,
 // examples/decode.c:21-26; the per-row activation quantisation of examples/quant.c:34-37). Here they are
 // small fused kernels on the library's stream, so activations never leave HBM between the matmuls:
-//   k_norm_quant      [embedding lookup | residual add of a matmul result] + RMSNorm + per-row int8 quant
+//   k_norm_quant_*    [embedding lookup | residual add of a matmul result] + RMSNorm + per-row int8 quant
 //   k_qkv_post        q/k/v dequant + per-head RMSNorm (Qwen3 q_norm / k_norm) + RoPE + KV-cache append
 //   k_attn_part       causal GQA attention over one 64-key chunk: running max, sum and P.V per query head
 //   k_attn_quant      combine the chunks (log-sum-exp) + per-row int8 quant of the attention output
@@ -22,45 +22,90 @@
 
 namespace {
 
+// Wave-wide sum / max in every lane, on the cross-lane paths of the VALU: DPP quad_perm swaps (lanes
+// l ^ 1, l ^ 2), DPP row_half_mirror and row_mirror (the other quad of an 8-lane half, the other half of a
+// 16-lane row), then v_permlane16_swap / v_permlane32_swap (l ^ 16, l ^ 32). Every step combines the same two
+// partials in every lane (a + b == b + a), so all lanes hold the identical result. Six LDS-crossbar shuffles
+// (ds_bpermute) did the same in ~5x the latency.
+template <int CTRL> __device__ inline float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ inline float xor16(float v) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return __builtin_bit_cast(float, (int)((threadIdx.x & 16) == 0 ? s[1] : s[0]));
+}
+__device__ inline float xor32(float v) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return __builtin_bit_cast(float, (int)((threadIdx.x & 32) == 0 ? s[1] : s[0]));
+}
 __device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v = v + dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+    v = v + dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+    v = v + dpp<0x141>(v); // row_half_mirror
+    v = v + dpp<0x140>(v); // row_mirror
+    v = v + xor16(v);
+    return v + xor32(v);
 }
 __device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    v = fmaxf(v, xor16(v));
+    return fmaxf(v, xor32(v));
 }
-// Block-wide sum / max (blockDim a multiple of 64, at most 1024). red[] holds 16 floats. The result
-// reaches every thread; the waves' partials are added in wave order.
+// Block-wide sum / max (blockDim a multiple of 64, at most 1024). red[] holds 16 floats, 16-byte aligned, and
+// must not be in use by another reduction of the same workgroup (each call site has its own): one barrier,
+// after which every thread folds the waves' partials in wave order (float4 LDS reads where they fill).
 __device__ inline float block_sum(float v, float *red) {
     v = wave_sum(v);
-    __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
+    const int nw = (int)(blockDim.x >> 6);
     float s = 0.f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += red[i];
+    if ((nw & 3) == 0) {
+        const float4 *r4 = (const float4 *)red;
+        for (int i = 0; i < nw >> 2; i++) {
+            const float4 q = r4[i];
+            s = s + q.x;
+            s = s + q.y;
+            s = s + q.z;
+            s = s + q.w;
+        }
+    } else {
+        for (int i = 0; i < nw; i++) s = s + red[i];
+    }
     return s;
 }
 __device__ inline float block_max(float v, float *red) {
     v = wave_max(v);
-    __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    float m = red[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); i++) m = fmaxf(m, red[i]);
+    const int nw = (int)(blockDim.x >> 6);
+    float m = -INFINITY;
+    if ((nw & 3) == 0) {
+        const float4 *r4 = (const float4 *)red;
+        for (int i = 0; i < nw >> 2; i++) {
+            const float4 q = r4[i];
+            m = fmaxf(fmaxf(m, q.x), fmaxf(q.y, fmaxf(q.z, q.w)));
+        }
+    } else {
+        for (int i = 0; i < nw; i++) m = fmaxf(m, red[i]);
+    }
     return m;
 }
 
 // Rows live in registers: thread i holds elements i, i + blockDim, ... (E of them, E a compile-time
-// bound), so every global load of a row is issued before the first arithmetic that needs it.
+// bound), so every global load of a row is issued before the first arithmetic that needs it. Loads are
+// unconditional (from a clamped index, zeroed after): a load under a per-lane condition becomes a branch
+// whose join waits for that load, which would serialise the row's loads into one round trip each.
 template <int E, typename T>
 __device__ inline void load_row(T (&v)[E], const T *__restrict__ src, int n) {
 #pragma unroll
     for (int k = 0; k < E; k++) {
         const int i = threadIdx.x + k * blockDim.x;
-        v[k] = i < n ? src[i] : T(0);
+        const T x = src[min(i, n - 1)];
+        v[k] = i < n ? x : T(0);
     }
 }
 
@@ -69,12 +114,13 @@ __device__ inline void load_row(T (&v)[E], const T *__restrict__ src, int n) {
 // rounds to the same integer unless it lies within 1e-4 of a half-way point (|x / s| <= 127.5, where
 // 2 ulp < 1.6e-5); there the exact quotient decides.
 template <int E>
-__device__ inline void quant_regs(const float (&y)[E], int n, int8_t *__restrict__ q, float *s_out, float *red) {
+__device__ inline void quant_regs(const float (&y)[E], int n, int8_t *__restrict__ q, float *s_out) {
+    __shared__ __align__(16) float redq[16];
     float mx = 0.f;
 #pragma unroll
     for (int k = 0; k < E; k++)
         if (threadIdx.x + k * blockDim.x < (unsigned)n) mx = fmaxf(mx, fabsf(y[k]));
-    mx = block_max(mx, red);
+    mx = block_max(mx, redq);
     const float s = mx > 0.f ? mx / 127.0f : 1.0f;
     const float inv = 1.0f / s;
 #pragma unroll
@@ -93,35 +139,42 @@ __device__ inline void quant_regs(const float (&y)[E], int n, int8_t *__restrict
 // Token of a greedy-sampling key (see k_argmax): low 32 bits hold ~index.
 __device__ inline int key_token(unsigned long long k) { return (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)); }
 
-template <int E>
-__global__ __launch_bounds__(512) void k_norm_quant(q3_nq p) {
-    __shared__ float red[16];
+// The row source of k_norm_quant, fixed per launch so that every load of the row is issued up front.
+enum { NQ_ACC = 0, NQ_EMB = 1, NQ_X = 2 };
+
+template <int E, int MODE>
+__device__ inline void norm_quant_body(const q3_nq &p) {
+    __shared__ __align__(16) float red[16];
     const int t = blockIdx.x, H = p.H;
     float *__restrict__ xr = p.x + (size_t)t * H;
     float v[E], nw[E];
     int tok = 0;
-    if (p.emb) {
+    if constexpr (MODE == NQ_EMB) {
         tok = p.tok ? p.tok[t] : key_token(*p.best);
         if (tok < 0 || tok >= p.V) tok = 0; // an unset key; the host validates tokens it uploads
         const __half *__restrict__ e = p.emb + (size_t)tok * H;
+        load_row(nw, p.nw, H);
 #pragma unroll
         for (int k = 0; k < E; k++) {
             const int i = threadIdx.x + k * blockDim.x;
-            v[k] = i < H ? __half2float(e[i]) : 0.f;
+            const float x = __half2float(e[min(i, H - 1)]);
+            v[k] = i < H ? x : 0.f;
         }
     } else {
         load_row(v, (const float *)xr, H);
-    }
-    if (p.acc) { // residual add of the previous projection: x += (c * a_scale) * w_scale
-        int32_t c[E];
-        float w[E];
-        load_row(c, p.acc + (size_t)t * H, H);
-        load_row(w, p.acc_ws, H);
-        const float as = p.acc_as[t];
+        if constexpr (MODE == NQ_ACC) { // residual add of the previous projection: x += (c * a_scale) * w_scale
+            int32_t c[E];
+            float w[E];
+            load_row(c, p.acc + (size_t)t * H, H);
+            load_row(w, p.acc_ws, H);
+            const float as = p.acc_as[t];
+            load_row(nw, p.nw, H);
 #pragma unroll
-        for (int k = 0; k < E; k++) v[k] = v[k] + ((float)c[k] * as) * w[k];
+            for (int k = 0; k < E; k++) v[k] = v[k] + ((float)c[k] * as) * w[k];
+        } else {
+            load_row(nw, p.nw, H);
+        }
     }
-    load_row(nw, p.nw, H);
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < E; k++) {
@@ -129,8 +182,8 @@ __global__ __launch_bounds__(512) void k_norm_quant(q3_nq p) {
         if (i < H) xr[i] = v[k];
         ss += v[k] * v[k];
     }
-    ss = block_sum(ss, red); // its barriers also order every read of *best before the clear below
-    if (p.emb && threadIdx.x == 0) {
+    ss = block_sum(ss, red); // its barrier also orders every read of *best before the clear below
+    if (MODE == NQ_EMB && threadIdx.x == 0) {
         if (p.tok) {
             p.toks[p.st[0] + t] = tok;
             if (t == 0 && p.best) *p.best = 0ull;
@@ -145,12 +198,15 @@ __global__ __launch_bounds__(512) void k_norm_quant(q3_nq p) {
     const float r = 1.0f / sqrtf(ss / (float)H + p.eps);
 #pragma unroll
     for (int k = 0; k < E; k++) v[k] = (v[k] * r) * nw[k];
-    quant_regs(v, H, p.a8 + (size_t)t * H, p.as + t, red);
+    quant_regs(v, H, p.a8 + (size_t)t * H, p.as + t);
 }
+template <int E> __global__ __launch_bounds__(512) void k_norm_quant_acc(q3_nq p) { norm_quant_body<E, NQ_ACC>(p); }
+template <int E> __global__ __launch_bounds__(512) void k_norm_quant_emb(q3_nq p) { norm_quant_body<E, NQ_EMB>(p); }
+template <int E> __global__ __launch_bounds__(512) void k_norm_quant_x(q3_nq p) { norm_quant_body<E, NQ_X>(p); }
 
 __global__ __launch_bounds__(256) void k_qkv_post(q3_qkv p) {
     __shared__ float v[Q3_MAX_HD];
-    __shared__ float red[16];
+    __shared__ __align__(16) float red[16];
     const int HD = p.HD, half = HD >> 1, d = threadIdx.x;
     const int h = blockIdx.x, t = blockIdx.y;
     const int QD = p.NH * HD, KVD = p.NKV * HD;
@@ -166,12 +222,9 @@ __global__ __launch_bounds__(256) void k_qkv_post(q3_qkv p) {
     const int32_t cd = c[d];
     const float wd = ws[d], nwd = nw[d], as = p.as[t];
     const float cs = p.rcos[(size_t)pos * half + i], sn = p.rsin[(size_t)pos * half + i];
-    int32_t cvd = 0;
-    float wvd = 0.f;
-    if (kv) {
-        cvd = p.cv[(size_t)t * KVD + g * HD + d];
-        wvd = p.wsv[g * HD + d];
-    }
+    const int gv = kv ? g : 0; // unconditional loads (q heads read kv head 0's and drop it)
+    const int32_t cvd = p.cv[(size_t)t * KVD + gv * HD + d];
+    const float wvd = p.wsv[gv * HD + d];
     const float x = ((float)cd * as) * wd;
     const float ss = block_sum(x * x, red);
     const float r = 1.0f / sqrtf(ss / (float)HD + p.eps);
@@ -251,13 +304,12 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
         as = p.as[0];
         cs = p.rcos[(size_t)pos * half + ri];
         sn = p.rsin[(size_t)pos * half + ri];
-        if (own) {
-            ckd = p.ck[kvh * HD + d];
-            cvd = p.cv[kvh * HD + d];
-            wk = p.wsk[kvh * HD + d];
-            wv = p.wsv[kvh * HD + d];
-            kn = p.kn[d];
-        }
+        // the new row's k / v inputs: loaded by every workgroup (unconditional loads), used by the owner
+        ckd = p.ck[kvh * HD + d];
+        cvd = p.cv[kvh * HD + d];
+        wk = p.wsk[kvh * HD + d];
+        wv = p.wsv[kvh * HD + d];
+        kn = p.kn[d];
     } else {
         qs[tid] = p.q[(size_t)t * QD + h0 * HD + tid];
     }
@@ -346,7 +398,6 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
 template <int E>
 __global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
     extern __shared__ float sm[];
-    __shared__ float red[16];
     const int HD = p.HD, NH = p.NH, S = p.S, QD = NH * HD, t = blockIdx.x;
     const float *__restrict__ part = p.part + (size_t)t * NH * S * (HD + 2);
     float *w = sm, *ls = sm + NH * S, *inv = ls + NH * S;
@@ -357,7 +408,10 @@ __global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
         const int h = i / HD, d = i - h * HD;
         const float *ph = part + (size_t)h * S * (HD + 2) + d;
 #pragma unroll
-        for (int s = 0; s < Q3_MAX_S; s++) acc[k][s] = s < S ? ph[(size_t)s * (HD + 2)] : 0.f;
+        for (int s = 0; s < Q3_MAX_S; s++) {
+            const float x = ph[(size_t)min(s, S - 1) * (HD + 2)];
+            acc[k][s] = s < S ? x : 0.f;
+        }
     }
     for (int i = threadIdx.x; i < NH * S; i += blockDim.x) {
         w[i] = part[(size_t)i * (HD + 2) + HD];
@@ -388,12 +442,11 @@ __global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
             if (s < S) num += acc[k][s] * w[h * S + s];
         y[k] = i < QD ? num * inv[h] : 0.f;
     }
-    quant_regs(y, QD, p.a8 + (size_t)t * QD, p.as + t, red);
+    quant_regs(y, QD, p.a8 + (size_t)t * QD, p.as + t);
 }
 
 template <int E>
 __global__ __launch_bounds__(1024) void k_swiglu_quant(q3_glu p) {
-    __shared__ float red[16];
     const int F = p.F, t = blockIdx.x;
     int32_t cg[E], cu[E];
     float wg[E], wu[E], y[E];
@@ -408,7 +461,7 @@ __global__ __launch_bounds__(1024) void k_swiglu_quant(q3_glu p) {
         const float uv = ((float)cu[k] * as) * wu[k];
         y[k] = (gv / (1.0f + expf(-gv))) * uv;
     }
-    quant_regs(y, F, p.a8 + (size_t)t * F, p.as_out + t, red);
+    quant_regs(y, F, p.a8 + (size_t)t * F, p.as_out + t);
 }
 
 // Order-preserving map of a float to 32 bits (larger float -> larger unsigned).
@@ -462,8 +515,10 @@ extern "C" {
     } while (0)
 
 int q3k_norm_quant(const q3_nq *p, void *stream) {
-    if (p->M < 1 || p->H < 64 || p->H > 512 * 16 || (p->emb && !p->tok && p->M != 1)) return -2;
-    Q3_ROW_DISPATCH(k_norm_quant, 512, p->H, dim3(p->M), 0, (hipStream_t)stream, *p);
+    if (p->M < 1 || p->H < 64 || p->H > 512 * 16 || (p->emb && !p->tok && p->M != 1) || (p->emb && p->acc)) return -2;
+    if (p->emb) Q3_ROW_DISPATCH(k_norm_quant_emb, 512, p->H, dim3(p->M), 0, (hipStream_t)stream, *p);
+    else if (p->acc) Q3_ROW_DISPATCH(k_norm_quant_acc, 512, p->H, dim3(p->M), 0, (hipStream_t)stream, *p);
+    else Q3_ROW_DISPATCH(k_norm_quant_x, 512, p->H, dim3(p->M), 0, (hipStream_t)stream, *p);
     return launch_ok();
 }
 
