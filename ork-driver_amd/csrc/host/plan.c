@@ -241,7 +241,7 @@ void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB,
     if (tiled && rkind != ORKH_NF4) {
         const char *tf = getenv("ORK_TILE");
         int fbm, fbn;
-        if (tf && sscanf(tf, "%dx%d", &fbm, &fbn) == 2) {
+        if (tf && sscanf(tf, "%dx%d", &fbm, &fbn) == 2 && fbm == 64 && (fbn == 64 || fbn == 192)) {
             q->algo = ORKH_ALGO_TILED2;
             q->bm = fbm;
             q->bn = fbn;
