@@ -361,6 +361,8 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
         const int gg = tid >> 6, j = tid & 63;
         const float4 *qr = (const float4 *)(qs + gg * HD), *kr = (const float4 *)(Ks + j * KS);
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        // unrolled so that eight iterations' LDS reads are in flight together (HD is a runtime value)
+#pragma unroll 8
         for (int e = 0; e < HD4; e++) {
             const float4 qv = qr[e], kv = kr[e];
             a0 += qv.x * kv.x;
@@ -418,17 +420,17 @@ __global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
         ls[i] = part[(size_t)i * (HD + 2) + HD + 1];
     }
     __syncthreads();
-    for (int h = threadIdx.x; h < NH; h += blockDim.x) {
-        float mx = -INFINITY;
-        for (int s = 0; s < S; s++) mx = fmaxf(mx, w[h * S + s]);
-        float den = 0.f;
-        for (int s = 0; s < S; s++) {
-            const float m = w[h * S + s];
-            const float e = m == -INFINITY ? 0.f : expf(m - mx);
-            w[h * S + s] = e;
-            den += ls[h * S + s] * e;
-        }
-        inv[h] = den > 0.f ? 1.0f / den : 0.f;
+    // chunk weights, one wave per head, lane s = chunk s (S <= Q3_MAX_S <= 64): e_s = exp(m_s - max m) and
+    // 1 / sum_s l_s e_s
+    for (int h = (int)(threadIdx.x >> 6); h < NH; h += (int)(blockDim.x >> 6)) {
+        const int ln = threadIdx.x & 63, sc = min(ln, S - 1);
+        const float m0 = w[h * S + sc], l0 = ls[h * S + sc];
+        const float m = ln < S ? m0 : -INFINITY;
+        const float mx = wave_max(m);
+        const float e = m == -INFINITY ? 0.f : expf(m - mx);
+        const float den = wave_sum(ln < S ? l0 * e : 0.f);
+        if (ln < S) w[h * S + ln] = e;
+        if (ln == 0) inv[h] = den > 0.f ? 1.0f / den : 0.f;
     }
     __syncthreads();
     float y[E];
