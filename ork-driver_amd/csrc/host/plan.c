@@ -31,10 +31,15 @@ static int kpb_of(int rkind) { return rkind == ORKH_I8 ? 64 : rkind == ORKH_F16 
  * wave for the int8/fp16 GEMV (M = 1); more waves with shorter runs where each block costs more issue
  * (more rows, int4 decode). Measured on the K=2048, N=6144 panels; the run lengths on either side were
  * within 2-4%. */
-static void stream_geom(int rkind, int M, int KB, int ks, orkh_plan *q) {
+static void stream_geom(int rkind, int M, int KB, int NB, int cu, int ks, orkh_plan *q) {
     const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
     const int need = cdiv(KB, kbw_target); /* waves per panel at the target run length */
-    const int wpg = need <= 4 ? 4 : 8;
+    int wpg = need <= 4 ? 4 : 8;
+    /* an int8 GEMV with fewer panels than CUs runs 8 shorter waves per panel: 2.94 -> 2.84 us at K=N=2048,
+     * 2.80 -> 2.67 us at N=1024; with more panels than CUs 4 stay ahead (3.94 vs 4.04 us at N=6144) */
+    if (M == 1 && rkind == ORKH_I8 && NB < cu) wpg = 8;
+    const char *fw = getenv("ORK_WPG"); /* testing / A-B: waves per panel of the GEMV (4 or 8) */
+    if (M == 1 && fw && (atoi(fw) == 4 || atoi(fw) == 8)) wpg = atoi(fw);
     if (ks > KB) ks = KB;
     if (ks < 1) ks = 1;
     const int kbs = cdiv(KB, ks);
@@ -50,7 +55,7 @@ static void stream_geom(int rkind, int M, int KB, int ks, orkh_plan *q) {
  * (the fixed-order reduce), which a one-run wave never repays. */
 static int stream_rule_ks(int rkind, int M, int KB, int NB, int cu) {
     orkh_plan g;
-    stream_geom(rkind, M, KB, 1, &g);
+    stream_geom(rkind, M, KB, NB, cu, 1, &g);
     const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
     const int runs = cdiv(cdiv(KB, g.wpg), kbw_target);
     int ks = 1;
@@ -82,7 +87,7 @@ static double mac_rate(int rkind, int tiled) {
 
 static double stream_us(int rkind, int M, int N, int KB, int cu, int ks) {
     orkh_plan g;
-    stream_geom(rkind, M, KB, ks, &g);
+    stream_geom(rkind, M, KB, N / 16, cu, ks, &g);
     const long wgs = (long)(N / 16) * g.ksplit;
     const double per = (double)((wgs + cu - 1) / cu);
     const double kib = ((double)M * a_bytes_per_kb(rkind) * g.kbs + 1024.0 * g.kbs + 64.0 * M) / 1024;
@@ -175,7 +180,7 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
         }
         /* M = 1 takes the VALU-dot GEMV (same grid and fields); ORK_PLAN=stream keeps the MFMA kernel. */
         q->algo = (M == 1 && !f_stream) ? ORKH_ALGO_GEMV : ORKH_ALGO_STREAM;
-        stream_geom(rkind, M, KB, ks, q);
+        stream_geom(rkind, M, KB, NB, cu, ks, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }
