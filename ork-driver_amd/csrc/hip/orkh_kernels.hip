@@ -25,6 +25,7 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "orkh.h"
@@ -945,6 +946,26 @@ int launch_stream(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     return -2;
 }
 
+// Raise a kernel's dynamic-LDS limit once per (kernel, device): hipFuncSetAttribute holds per device, so the
+// flags are per device, and atomic, since contexts may launch from several threads.
+constexpr int ORKH_MAX_DEV = 64;
+typedef std::atomic<bool> lds_flags[ORKH_MAX_DEV];
+inline int lds_limit(const void *kern, int bytes, lds_flags &done) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= ORKH_MAX_DEV) {
+        snprintf(g_lerr, sizeof g_lerr, "LDS limit: no current device below %d", ORKH_MAX_DEV);
+        return -1;
+    }
+    if (done[dev].load(std::memory_order_acquire)) return 0;
+    const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) {
+        snprintf(g_lerr, sizeof g_lerr, "hipFuncSetAttribute(%d B of LDS): %s", bytes, hipGetErrorString(e));
+        return -1;
+    }
+    done[dev].store(true, std::memory_order_release);
+    return 0;
+}
+
 template <int KIND, int BM, int BN>
 int launch_tiled_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int KS = 1;
@@ -952,12 +973,8 @@ int launch_tiled_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int KG = 2;
     constexpr size_t lds = tiled_lds_bytes<KIND, BM, BN, KS, KG>();
     auto kern = k_tiled<KIND, BM, BN, KS, D, KG>;
-    static bool attr = false;  // per instantiation: allow more than the default 64 KiB of dynamic LDS
-    if (!attr) {
-        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return -1;
-        attr = true;
-    }
+    static lds_flags attr; // per instantiation: allow more than the default 64 KiB of dynamic LDS
+    if (lds_limit((const void *)kern, (int)lds, attr)) return -1;
     const int mtiles = (p->M + BM - 1) / BM;
     const int ntiles = (p->N / 16 + BN / 16 - 1) / (BN / 16);
     const int ksplit = q->ksplit > 1 ? q->ksplit : 1;
@@ -979,12 +996,8 @@ int launch_tiled2_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int KS = t2_ks<KIND, BM, BN>();
     using P = T2<KIND, BM, BN, KS>;
     auto kern = k_tiled2<KIND, BM, BN, KS>;
-    static bool attr = false; // per instantiation: allow more than the default 64 KiB of dynamic LDS
-    if (!attr) {
-        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)P::LDS) != hipSuccess)
-            return -1;
-        attr = true;
-    }
+    static lds_flags attr; // per instantiation: allow more than the default 64 KiB of dynamic LDS
+    if (lds_limit((const void *)kern, (int)P::LDS, attr)) return -1;
     const int mtiles = (p->M + BM - 1) / BM;
     const int ntiles = (p->N / 16 + P::NB - 1) / P::NB;
     const int ksplit = q->ksplit > 1 ? q->ksplit : 1;
@@ -1134,12 +1147,8 @@ int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s) {
         snprintf(g_lerr, sizeof g_lerr, "grouped tiled2 %dx%d: %d groups need %zu B of LDS", BM, BN, Sk, lds);
         return -2;
     }
-    static bool attr[2] = {false, false}; // per instantiation: allow up to 160 KiB of dynamic LDS
-    if (!attr[whole]) {
-        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840) != hipSuccess)
-            return -1;
-        attr[whole] = true;
-    }
+    static lds_flags attr[2]; // per instantiation: allow up to 160 KiB of dynamic LDS
+    if (lds_limit((const void *)kern, 163840, attr[whole])) return -1;
     const int mtiles = (p->M + BM - 1) / BM;
     const int ntiles = (p->N / 16 + P::NB - 1) / P::NB;
     hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(1024), lds, s, *p, mtiles, mtiles * ntiles, gp);
