@@ -16,9 +16,9 @@ extern "C" {
 typedef uint16_t q3_half;
 #endif
 
-#define Q3_CHUNK 64   /* keys per attention workgroup */
+#define Q3_CHUNK 32   /* keys per attention workgroup (32 or 64) */
 #define Q3_MAX_HD 256 /* head_dim bound of k_qkv_post / k_attn_part */
-#define Q3_MAX_S 16   /* key chunks per row: max_ctx <= 1024 */
+#define Q3_MAX_S 32   /* key chunks per row: max_ctx <= 1024 */
 
 /* st[] decode state: st[0] position of row 0 of the current pass, st[1] next free position.
  * best: greedy-sampling key, (order-preserving bits of the logit << 32) | (0xFFFFFFFF - token). */
@@ -53,7 +53,7 @@ typedef struct q3_qkv { /* q/k/v dequant -> per-head RMSNorm -> RoPE -> q rows, 
     float *kc, *vc; /* [max_ctx][NKV*HD] this layer's cache */
 } q3_qkv;
 
-typedef struct q3_att { /* grid (NKV * query-head sub-groups, S, M): 64-key chunk partials */
+typedef struct q3_att { /* grid (NKV * query-head sub-groups, S, M): Q3_CHUNK-key chunk partials */
     int M, NH, NKV, HD, S, max_ctx;
     const float *q; /* [M][NH*HD] rotated queries (unfused) */
     float *kc, *vc; /* this layer's cache; the fused form appends the new row */

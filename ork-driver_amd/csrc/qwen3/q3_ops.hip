@@ -6,7 +6,7 @@
 // small fused kernels on the library's stream, so activations never leave HBM between the matmuls:
 //   k_norm_quant_*    [embedding lookup | residual add of a matmul result] + RMSNorm + per-row int8 quant
 //   k_qkv_post        q/k/v dequant + per-head RMSNorm (Qwen3 q_norm / k_norm) + RoPE + KV-cache append
-//   k_attn_part       causal GQA attention over one 64-key chunk: running max, sum and P.V per query head
+//   k_attn_part       causal GQA attention over one Q3_CHUNK-key chunk: running max, sum and P.V per query head
 //   k_attn_quant      combine the chunks (log-sum-exp) + per-row int8 quant of the attention output
 //   k_swiglu_quant    gate/up dequant + silu(g) * u + per-row int8 quant
 //   k_argmax          greedy sampling: dequantised logits -> one 64-bit atomic max per workgroup
@@ -54,6 +54,28 @@ __device__ inline float wave_max(float v) {
     v = fmaxf(v, xor16(v));
     return fmaxf(v, xor32(v));
 }
+// The same over aligned groups of W lanes (W = 32 or 64): a group's result in each of its lanes.
+template <int W> __device__ inline float group_sum(float v) {
+    static_assert(W == 32 || W == 64, "group width");
+    v = v + dpp<0xB1>(v);
+    v = v + dpp<0x4E>(v);
+    v = v + dpp<0x141>(v);
+    v = v + dpp<0x140>(v);
+    v = v + xor16(v);
+    if constexpr (W == 64) v = v + xor32(v);
+    return v;
+}
+template <int W> __device__ inline float group_max(float v) {
+    static_assert(W == 32 || W == 64, "group width");
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    v = fmaxf(v, xor16(v));
+    if constexpr (W == 64) v = fmaxf(v, xor32(v));
+    return v;
+}
+
 // Block-wide sum / max (blockDim a multiple of 64, at most 1024). red[] holds 16 floats, 16-byte aligned, and
 // must not be in use by another reduction of the same workgroup (each call site has its own): one barrier,
 // after which every thread folds the waves' partials in wave order (float4 LDS reads where they fill).
@@ -241,11 +263,12 @@ __global__ __launch_bounds__(256) void k_qkv_post(q3_qkv p) {
     }
 }
 
-// One workgroup per (kv head, sub-group of GW query heads, 64-key chunk, query row), GW * HD <= 256
+// One workgroup per (kv head, sub-group of GW query heads, Q3_CHUNK-key chunk, query row), GW * HD <= 256
 // threads: thread (g, d) = query head g of the sub-group, dimension d. Every global load is issued up
 // front and unconditionally (rows past the chunk's last key repeat that key; their probabilities are
-// zero): the chunk's K rows go to LDS as float4, each thread's V column stays in registers. Wave g scores
-// head g's keys one per lane, so the chunk's softmax statistics are two wave reductions.
+// zero): the chunk's K rows go to LDS as float4, each thread's V column stays in registers. Query head g's
+// keys are scored one per lane on Q3_CHUNK consecutive lanes, so the chunk's softmax statistics are two
+// lane-group reductions. 32-key chunks (rather than 64) halve each workgroup's K/V bytes, which bound it.
 // FUSED (one query row, decode): the workgroup also does k_qkv_post's work for itself -- dequantises,
 // normalises and rotates its query heads from the q/k/v matmul results, and the workgroup whose chunk
 // holds the current position builds that position's K/V row (appending it to the cache) -- which saves
@@ -357,8 +380,8 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
         }
     }
     __syncthreads();
-    if (tid < GW * Q3_CHUNK) {
-        const int gg = tid >> 6, j = tid & 63;
+    if (tid < GW * Q3_CHUNK) { // head gg's keys on Q3_CHUNK consecutive lanes
+        const int gg = tid / Q3_CHUNK, j = tid % Q3_CHUNK;
         const float4 *qr = (const float4 *)(qs + gg * HD), *kr = (const float4 *)(Ks + j * KS);
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
         // unrolled so that eight iterations' LDS reads are in flight together (HD is a runtime value)
@@ -371,9 +394,9 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
             a3 += qv.w * kv.w;
         }
         const float sc = j < n ? ((a0 + a1) + (a2 + a3)) * p.scale : -INFINITY;
-        const float m = wave_max(sc);
+        const float m = group_max<Q3_CHUNK>(sc);
         const float pj = j < n ? expf(sc - m) : 0.f;
-        const float l = wave_sum(pj);
+        const float l = group_sum<Q3_CHUNK>(pj);
         P[gg * Q3_CHUNK + j] = pj;
         if (j == 0) {
             ml[2 * gg] = m;
@@ -397,20 +420,20 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
 
 // Combine the chunks of every head (log-sum-exp weights), then quantise the row. Each thread's partial
 // sums are loaded before the chunk weights are known, so the kernel pays one round trip to memory.
-template <int E>
-__global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
+template <int E, int MS>
+__device__ inline void attn_quant_body(const q3_aq &p) {
     extern __shared__ float sm[];
     const int HD = p.HD, NH = p.NH, S = p.S, QD = NH * HD, t = blockIdx.x;
     const float *__restrict__ part = p.part + (size_t)t * NH * S * (HD + 2);
     float *w = sm, *ls = sm + NH * S, *inv = ls + NH * S;
-    float acc[E][Q3_MAX_S];
+    float acc[E][MS];
 #pragma unroll
     for (int k = 0; k < E; k++) {
         const int i = min((int)(threadIdx.x + k * blockDim.x), QD - 1);
         const int h = i / HD, d = i - h * HD;
         const float *ph = part + (size_t)h * S * (HD + 2) + d;
 #pragma unroll
-        for (int s = 0; s < Q3_MAX_S; s++) {
+        for (int s = 0; s < MS; s++) {
             const float x = ph[(size_t)min(s, S - 1) * (HD + 2)];
             acc[k][s] = s < S ? x : 0.f;
         }
@@ -440,12 +463,15 @@ __global__ __launch_bounds__(1024) void k_attn_quant(q3_aq p) {
         const int h = min(i, QD - 1) / HD;
         float num = 0.f;
 #pragma unroll
-        for (int s = 0; s < Q3_MAX_S; s++)
+        for (int s = 0; s < MS; s++)
             if (s < S) num += acc[k][s] * w[h * S + s];
         y[k] = i < QD ? num * inv[h] : 0.f;
     }
     quant_regs(y, QD, p.a8 + (size_t)t * QD, p.as + t);
 }
+template <int E> __global__ __launch_bounds__(1024) void k_attn_quant8(q3_aq p) { attn_quant_body<E, 8>(p); }
+template <int E> __global__ __launch_bounds__(1024) void k_attn_quant16(q3_aq p) { attn_quant_body<E, 16>(p); }
+template <int E> __global__ __launch_bounds__(1024) void k_attn_quant32(q3_aq p) { attn_quant_body<E, 32>(p); }
 
 template <int E>
 __global__ __launch_bounds__(1024) void k_swiglu_quant(q3_glu p) {
@@ -561,7 +587,10 @@ int q3k_attn_part(const q3_att *p, void *stream) {
 int q3k_attn_quant(const q3_aq *p, void *stream) {
     const size_t lds = (size_t)(2 * p->NH * p->S + p->NH) * sizeof(float);
     if (p->M < 1 || p->NH * p->HD > 1024 * 16 || p->S > Q3_MAX_S || lds > 32 * 1024) return -2;
-    Q3_ROW_DISPATCH(k_attn_quant, 1024, p->NH * p->HD, dim3(p->M), lds, (hipStream_t)stream, *p);
+    // chunk loop bound: the smallest instantiated one covering S (each chunk is one load per element)
+    if (p->S <= 8) Q3_ROW_DISPATCH(k_attn_quant8, 1024, p->NH * p->HD, dim3(p->M), lds, (hipStream_t)stream, *p);
+    else if (p->S <= 16) Q3_ROW_DISPATCH(k_attn_quant16, 1024, p->NH * p->HD, dim3(p->M), lds, (hipStream_t)stream, *p);
+    else Q3_ROW_DISPATCH(k_attn_quant32, 1024, p->NH * p->HD, dim3(p->M), lds, (hipStream_t)stream, *p);
     return launch_ok();
 }
 
