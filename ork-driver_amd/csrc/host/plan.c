@@ -172,7 +172,7 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
             }
             orkh_plan t2;
             memset(&t2, 0, sizeof t2);
-            if (tiled2_best(rkind, M, N, KB, cu, 0, 0, &t2) < ts - 1e-9) {
+            if (tiled2_best(rkind, M, N, KB, cu, 0, rkind == ORKH_I4U, &t2) < ts - 1e-9) {
                 *q = t2;
                 if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
                 return 0;
@@ -186,7 +186,8 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
     }
 
     if (rkind != ORKH_NF4 && !f_tiled) {
-        tiled2_best(rkind, M, N, KB, cu, ks_force, 0, q);
+        /* uniform int4 skips the 256 x 256 tile: with the nibble decode its registers spill (20 B per lane) */
+        tiled2_best(rkind, M, N, KB, cu, ks_force, rkind == ORKH_I4U, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }
