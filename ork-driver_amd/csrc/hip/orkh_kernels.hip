@@ -467,6 +467,19 @@ template <int KIND, int BM, int BN, int KS> struct T2 {
     static_assert(MB % WM == 0 && NB % WN == 0 && R >= 2 && (R - 2) * IPW < 64, "tile");
 };
 
+// Quotient and remainder of a wave-uniform x / d (0 <= x, 1 <= d, both < 2^24) on the VALU: the correctly
+// rounded float quotient is within one of the integer one, and one correction fixes it. A scalar integer
+// division is ~35 instructions on the scalar unit, which a workgroup's 16 waves share; two of them per wave
+// in a tiled kernel's prologue queue ~1,000 cycles there.
+__device__ __forceinline__ void udivmod(int x, int d, int &q, int &r) {
+    int qq = (int)((float)x / (float)d);
+    int rr = x - qq * d;
+    if (rr < 0) { qq--; rr += d; }
+    else if (rr >= d) { qq++; rr -= d; }
+    q = __builtin_amdgcn_readfirstlane(qq);
+    r = __builtin_amdgcn_readfirstlane(rr);
+}
+
 // Grouped mode of k_tiled2 (ork_*_mm_run_grouped): C is fp32 and every output is the sum, in ascending g, of
 // ((float)P_g * aS[m][g]) * bS[g][n] with P_g the exact int32 partial over K-group g (src/npu/core/buf.c:501-520).
 struct T2Group {
@@ -493,8 +506,10 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     const int nT = gridDim.x, bid = blockIdx.x;
     const int per = nT / 8, rem = nT % 8, x = bid % 8, j = bid / 8;
     const int tl = (x < rem) ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
-    const int ks = tl / ntiles_all, tile = tl % ntiles_all;
-    const int m0 = (tile % mtiles) * BM, nb0 = (tile / mtiles) * P::NB;
+    int ks, tile, tn, tm;
+    udivmod(tl, ntiles_all, ks, tile);
+    udivmod(tile, mtiles, tn, tm);
+    const int m0 = tm * BM, nb0 = tn * P::NB;
     const int NBtot = p.N / 16;
     const int kb_lo = ks * kbs, kb_hi = min(kb_lo + kbs, p.KB);
     const int k_hi = min(kb_hi * T::KPB, p.K);
@@ -1002,6 +1017,10 @@ int launch_tiled2_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     const int ntiles = (p->N / 16 + P::NB - 1) / P::NB;
     const int ksplit = q->ksplit > 1 ? q->ksplit : 1;
     const int kbs = ksplit > 1 ? q->kbs : p->KB;
+    if ((long)mtiles * ntiles * ksplit >= (1L << 24)) { // the kernel's tile-index division is exact below 2^24
+        snprintf(g_lerr, sizeof g_lerr, "tiled2: %ld workgroups", (long)mtiles * ntiles * ksplit);
+        return -2;
+    }
     hipLaunchKernelGGL(kern, dim3(mtiles * ntiles * ksplit), dim3(1024), P::LDS, s, *p, mtiles, mtiles * ntiles, kbs,
                        q->ws);
     return 0;
@@ -1151,6 +1170,10 @@ int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s) {
     if (lds_limit((const void *)kern, 163840, attr[whole])) return -1;
     const int mtiles = (p->M + BM - 1) / BM;
     const int ntiles = (p->N / 16 + P::NB - 1) / P::NB;
+    if ((long)mtiles * ntiles >= (1L << 24)) { // the kernel's tile-index division is exact below 2^24
+        snprintf(g_lerr, sizeof g_lerr, "grouped tiled2: %ld workgroups", (long)mtiles * ntiles);
+        return -2;
+    }
     hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(1024), lds, s, *p, mtiles, mtiles * ntiles, gp);
     return 0;
 }
