@@ -462,8 +462,11 @@ template <int KIND, int BM, int BN, int KS> struct T2 {
     static constexpr int IPW = (NI + NW - 1) / NW;                               // per wave
     static constexpr int JUNK = IPW * NW > NI ? 1 : 0;
     static constexpr int SLOT = (NI + JUNK) * 1024;
-    static constexpr int R = (163840 / SLOT) < 4 ? (163840 / SLOT) : 4;          // ring depth within 160 KiB
-    static constexpr size_t LDS = (size_t)R * SLOT;
+    // NF4: a stage's B blocks are decoded once, into int8 MFMA operands in LDS, instead of by each of the
+    // WM waves that read a block (the codebook decode is ~8x the VALU work of the uniform-int4 one)
+    static constexpr int DEC = KIND == ORKH_NF4 ? NIB * T::STEPS * 1024 : 0;
+    static constexpr int R = ((163840 - DEC) / SLOT) < 4 ? ((163840 - DEC) / SLOT) : 4; // ring within 160 KiB
+    static constexpr size_t LDS = (size_t)R * SLOT + DEC;
     static_assert(MB % WM == 0 && NB % WN == 0 && R >= 2 && (R - 2) * IPW < 64, "tile");
 };
 
@@ -633,12 +636,32 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         if constexpr (GR) {
             if (s == 0) load_sc(0); // the scales landed with stage 0 (older loads, same wait)
         }
+        const v4i *Dec = sm + P::R * (P::SLOT / 16); // NF4: the stage's decoded B blocks, [block][step]
+        if constexpr (KIND == ORKH_NF4) {
+            // block b of the stage by wave b % NW, each lane its 16 bytes; one barrier publishes them. The
+            // previous stage's readers all passed the barrier above, so the buffer is free.
+            for (int b = wv; b < P::NIB; b += P::NW) {
+                v4i op[T::STEPS];
+                decode<KIND>(Bs[b * 64 + lane], op, L);
+#pragma unroll
+                for (int st = 0; st < T::STEPS; st++) ((v4i *)Dec)[(b * T::STEPS + st) * 64 + lane] = op[st];
+            }
+            __syncthreads();
+        }
         if constexpr (GR != 1) {
 #pragma unroll
             for (int kbl = 0; kbl < KS; kbl++) {
                 v4i op[P::NTW][T::STEPS];
 #pragma unroll
-                for (int jn = 0; jn < P::NTW; jn++) decode<KIND>(Bs[((wn * P::NTW + jn) * KS + kbl) * 64 + lane], op[jn], L);
+                for (int jn = 0; jn < P::NTW; jn++) {
+                    const int b = (wn * P::NTW + jn) * KS + kbl;
+                    if constexpr (KIND == ORKH_NF4) {
+#pragma unroll
+                        for (int st = 0; st < T::STEPS; st++) op[jn][st] = Dec[(b * T::STEPS + st) * 64 + lane];
+                    } else {
+                        decode<KIND>(Bs[b * 64 + lane], op[jn], L);
+                    }
+                }
 #pragma unroll
                 for (int st = 0; st < T::STEPS; st++)
 #pragma unroll

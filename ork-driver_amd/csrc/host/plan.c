@@ -11,7 +11,8 @@
  *   M <= 64  the streaming kernel (same grid, runs of 1-4 KiB) or the LDS-ring tiled kernel, whichever a
  *            delivery model of both prices lower, each with its best K split (NF4: streaming, by the
  *            occupancy rule of the GEMV).
- *   M >  64  the LDS-ring tiled kernel (k_tiled for NF4): the tile and K split with the least modelled time.
+ *   M >  64  the LDS-ring tiled kernel (k_tiled for NF4 below 256 rows): the tile and K split with the least
+ *            modelled time.
  * Both time models charge a workgroup for a fixed set-up, the operand bytes that must reach its CU and
  * its multiply-accumulates; a K split adds its partials' round trip and the reduce launch.
  * ORK_PLAN=stream|tiled, ORK_TILE=BMxBN and ORK_KSPLIT=n force a kernel, tile or split (tests, A/B). */
@@ -82,6 +83,7 @@ static int stream_rule_ks(int rkind, int M, int KB, int NB, int cu) {
 static double mac_rate(int rkind, int tiled) {
     if (rkind == ORKH_I8) return tiled ? 0.100 : 0.94;
     if (rkind == ORKH_F16) return tiled ? 0.187 : 1.90;
+    if (rkind == ORKH_NF4) return tiled ? 0.40 : 0.91; /* tiled: with the per-stage decode into LDS (12% rms) */
     return tiled ? 0.199 : 0.91;
 }
 
@@ -107,6 +109,9 @@ static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force,
     double best = -1;
     for (int i = cfg_from; i < 4; i++) {
         const int bm = cfg2[i][0], bn = cfg2[i][1];
+        /* NF4's decoded (int8) B doubles the LDS reads of the 3-panel wave tile: 22.3 us at M=512 vs 19.8 on
+         * 128 x 128, which the model does not see */
+        if (rkind == ORKH_NF4 && bn == 192) continue;
         const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);
         for (int ks = ks_force > 0 ? ks_force : 1; ks <= (ks_force > 0 ? ks_force : 8); ks *= (ks_force > 0 ? 8 : 2)) {
             const int kbs = cdiv(KB, ks);
@@ -185,19 +190,20 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
         return 0;
     }
 
-    if (rkind != ORKH_NF4 && !f_tiled) {
+    /* NF4 takes the LDS-ring kernel from 256 rows (its stage decode into LDS beats k_tiled there: 16.7 vs
+     * 20.7 us at M=256, 21.5 vs 22.6 us at M=512, K=2048 N=6144) and k_tiled below (11.3 vs 12.0 us at M=128) */
+    if ((rkind != ORKH_NF4 || M >= 256) && !f_tiled) {
         /* uniform int4 skips the 256 x 256 tile: with the nibble decode its registers spill (20 B per lane) */
         tiled2_best(rkind, M, N, KB, cu, ks_force, rkind == ORKH_I4U, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }
 
-    /* k_tiled (NF4, or ORK_PLAN=tiled): each CU pulls its tiles' A and B rows through L2 at a roughly fixed
+    /* k_tiled (NF4 below 256 rows, or ORK_PLAN=tiled): each CU pulls its tiles' A and B rows through L2 at a roughly fixed
      * rate, so the time of a round of workgroups is about the operand bytes one workgroup loads. K is split
      * across workgroups when that cuts the per-workgroup bytes by more than the partial sums and the extra
      * reduce launch (~2 us) cost. Model units: us at ~48 KB/us per CU (measured order of magnitude),
-     * 5 TB/s for the partials' HBM round trip. NF4 stays here: four waves share each decoded B block, and
-     * the codebook decode is not cheap enough to repeat in every wave as k_tiled2 would. */
+     * 5 TB/s for the partials' HBM round trip. */
     static const int cfg[][2] = {{128, 96}, {128, 128}, {64, 64}};
     const int bpk = 64;                                                  /* B bytes per column per K-block, every kind */
     const int apk = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 128 : 64; /* A bytes per row per K-block */

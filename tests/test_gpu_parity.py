@@ -442,7 +442,7 @@ def test_run_errors(npu):
 @pytest.mark.parametrize("ks", [1, 3])
 def test_lds_ring_tiles_all_kinds(npu, tile, ks):
     """The LDS-ring tiled kernel at every tile shape the planner can choose, unsplit and K-split: exact for
-    int8, uniform-int4 i4a8 and W4A4, within the fp16 bar (and run-to-run identical) for fp16. M, N and K
+    int8, uniform-int4 and NF4 i4a8 and W4A4, within the fp16 bar (and run-to-run identical) for fp16. M, N and K
     tails: M = 300 and 70 are no tile multiple, N = 224 (14 panels) leaves a partial tile for every tile
     width, K = 2080 ends mid K-block for int8 (K % 64 = 32) and the nibble kinds (K % 128 = 32)."""
     _say("lds-ring tile", tile, "ks", ks)
@@ -465,6 +465,15 @@ def test_lds_ring_tiles_all_kinds(npu, tile, ks):
         with _env(ORK_TILE=tile, ORK_KSPLIT=ks):
             rc, C = npu.run_i8(w, A)
         assert rc == 0 and np.array_equal(C, O.gemm_i32(A, codes)), ("i4a8 uniform", M)
+        ork.free(w)
+        with _env(ORK_NF4=1):  # NF4: the stage's blocks decoded once into LDS
+            w, _ = npu.pack_i4a8(W)
+        _, _, codes = O.pack_i4a8(W, nf4=True)
+        with _env(ORK_TILE=tile, ORK_KSPLIT=ks):
+            rc, C = npu.run_i8(w, A)
+            name = npu.plan_name(w, M)
+        assert name.startswith("tiled2_nf4_" + tile), name
+        assert rc == 0 and np.array_equal(C, O.gemm_i32(A, codes)), ("i4a8 nf4", M)
         ork.free(w)
     A4, B4 = O.gen_i4_test(150, 1056, 256)   # W4A4 needs N % 64
     w = npu.pack_i4(B4)
