@@ -72,8 +72,10 @@ struct Lut { uint32_t l0, l1, l2, l3; };
 __device__ __forceinline__ uint32_t nf4_map4(uint32_t idx, const Lut &L) {
     const uint32_t lo = __builtin_amdgcn_perm(L.l1, L.l0, idx);               // entries 0..7
     const uint32_t hi = __builtin_amdgcn_perm(L.l3, L.l2, idx & 0x07070707u); // entries 8..15
-    const uint32_t m = (idx >> 3) & 0x01010101u;                              // bit 3 per byte
-    const uint32_t sel = (m << 8) - m;                                        // 0xff where idx >= 8
+    const uint32_t m8 = idx & 0x08080808u;                                    // bit 3 per byte
+    // 0xff in each byte whose index is >= 8: per byte 0x100 - 1, the top byte's carry wrapping mod 2^32
+    // (not m * 0xff, which compiles to a quarter-rate v_mul_lo_u32)
+    const uint32_t sel = (m8 << 5) - (m8 >> 3);
     return (hi & sel) | (lo & ~sel);
 }
 
