@@ -55,6 +55,7 @@ void       *orkh_malloc(size_t n);                 /* device memory (HBM); NULL 
 int         orkh_free(void *p);
 void       *orkh_host_alloc(size_t n);             /* pinned, device-mapped host memory */
 int         orkh_host_free(void *p);
+void       *orkh_host_devptr(void *p);             /* device address of pinned, device-mapped host memory */
 int         orkh_h2d(void *dst, const void *src, size_t n, void *stream);   /* async; direction inferred */
 int         orkh_d2h(void *dst, const void *src, size_t n, void *stream);   /* async */
 int         orkh_d2d(void *dst, const void *src, size_t n, void *stream);   /* async */

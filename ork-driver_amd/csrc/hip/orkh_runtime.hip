@@ -94,6 +94,13 @@ int orkh_host_free(void *p) {
     return 0;
 }
 
+void *orkh_host_devptr(void *p) {
+    void *d = nullptr;
+    hipError_t e = hipHostGetDevicePointer(&d, p, 0);
+    if (e != hipSuccess) { fail(e, "hipHostGetDevicePointer"); return nullptr; }
+    return d;
+}
+
 int orkh_h2d(void *dst, const void *src, size_t n, void *stream) {
     if (!n) return 0;
     CK(hipMemcpyAsync(dst, src, n, hipMemcpyDefault, (hipStream_t)stream), "hipMemcpyAsync H2D");

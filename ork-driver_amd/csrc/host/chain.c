@@ -7,7 +7,7 @@
  * NULL weight, M < 1, wrong dtype), -1 for A/C overlap; C row stride override (cstride) for int8.
  * What changes: no PC-chained NPU programs, cores or doorbells. Every M = 1 task of one resident kind
  * goes into a grouped GEMV launch (ORKH_GROUP_MAX tasks each), the remaining tasks launch back to back
- * on the context's stream with their normal plans, and host operands move in one staging pass. An
+ * on the context's stream with their normal plans, and host operands move in one pinned staging pass. An
  * offline context returns -1 (the reference falls back to its CPU GEMM; this build has no CPU path). */
 #include <stdio.h>
 #include <stdlib.h>
@@ -65,15 +65,21 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
         if (!t[i].a_dev) ha += al256(t[i].abytes);
         if (!t[i].c_dev) hc += al256((size_t)t[i].M * t[i].w->N * 4);
     }
-    char *sa = NULL, *sc = NULL;
-    if (ha && !(sa = orki_stage(c, &c->sA, ha))) { orki_hip_fail(who); return -1; }
-    if (hc && !(sc = orki_stage(c, &c->sC, hc))) { orki_hip_fail(who); return -1; }
+    /* host A: gathered by the CPU into pinned staging, uploaded by one DMA copy; host C: written by the kernels
+     * into pinned, device-mapped staging when it all fits ORKI_HOST_C_DIRECT (copied out by the CPU after the
+     * sync), else into HBM staging brought back by strided D2H copies */
+    char *sa = NULL, *ha_h = NULL, *sc = NULL, *hc_h = NULL;
+    const int c_pinned = hc && hc <= ORKI_HOST_C_DIRECT;
+    if (ha && (!(sa = orki_stage(c, &c->sA, ha)) || !(ha_h = orki_hstage(c, &c->hA, ha)))) { orki_hip_fail(who); return -1; }
+    if (c_pinned) {
+        if (!(hc_h = orki_hstage(c, &c->hC, hc)) || !(sc = orkh_host_devptr(hc_h))) { orki_hip_fail(who); return -1; }
+    } else if (hc && !(sc = orki_stage(c, &c->sC, hc))) { orki_hip_fail(who); return -1; }
     size_t oa = 0, oc = 0;
     for (int i = 0; i < S; i++) {
         if (t[i].a_dev) t[i].dA = t[i].A;
         else {
             t[i].dA = sa + oa;
-            if (orkh_h2d(sa + oa, t[i].A, t[i].abytes, c->stream)) { orki_hip_fail(who); return -1; }
+            memcpy(ha_h + oa, t[i].A, t[i].abytes);
             oa += al256(t[i].abytes);
         }
         if (t[i].c_dev) t[i].dC = t[i].C;
@@ -82,6 +88,7 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
             oc += al256((size_t)t[i].M * t[i].w->N * 4);
         }
     }
+    if (ha && orkh_h2d(sa, ha_h, oa, c->stream)) { orki_hip_fail(who); return -1; }
 
     /* plans; split-K workspace shared by the individually launched tasks (stream-ordered) */
     orkh_plan *q = calloc((size_t)S, sizeof *q);
@@ -152,7 +159,7 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
         if (t[i].c_dev) continue;
         all_dev = 0;
         const size_t row = (size_t)t[i].w->N * 4;
-        if (orkh_d2h_2d(t[i].C, (size_t)t[i].ldc * 4, t[i].dC, row, row, (size_t)t[i].M, c->stream)) {
+        if (!c_pinned && orkh_d2h_2d(t[i].C, (size_t)t[i].ldc * 4, t[i].dC, row, row, (size_t)t[i].M, c->stream)) {
             orki_hip_fail(who);
             return -1;
         }
@@ -160,6 +167,15 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
     for (int i = 0; i < S; i++) all_dev &= t[i].a_dev;
     if (c->async && all_dev) return 0;
     if (orkh_sync(c->stream)) { orki_hip_fail(who); return -1; }
+    size_t o = 0;
+    if (c_pinned)
+        for (int i = 0; i < S; i++) {
+            if (t[i].c_dev) continue;
+            const size_t row = (size_t)t[i].w->N * 4;
+            for (int m = 0; m < t[i].M; m++)
+                memcpy((char *)t[i].C + (size_t)m * t[i].ldc * 4, hc_h + o + (size_t)m * row, row);
+            o += al256((size_t)t[i].M * row);
+        }
     return 0;
 }
 

@@ -128,6 +128,8 @@ void ork_npu_free(ork_npu *c) {
         orkh_free(c->sC.p);
         orkh_free(c->sW.p);
         orkh_free(c->sS.p);
+        orkh_host_free(c->hA.p);
+        orkh_host_free(c->hC.p);
         for (int i = 0; i < c->dma_n; i++) orkh_host_free(c->dma[i].p);
         for (int i = 0; i < c->devb_n; i++) orkh_free(c->devb[i].p);
         for (int i = 0; i < c->orphan_n; i++) orkh_free(c->orphan[i]);
@@ -170,6 +172,76 @@ void *orki_stage(ork_npu *c, struct ork_buf *b, size_t n) {
     b->n = b->p ? want : 0;
     if (!b->p) orki_hip_fail("staging alloc");
     return b->p;
+}
+
+/* Pinned, device-mapped host staging, grown on demand like orki_stage. */
+void *orki_hstage(ork_npu *c, struct ork_buf *b, size_t n) {
+    if (b->n >= n && b->p) return b->p;
+    size_t want = n < 65536 ? 65536 : n;
+    want = (want + 4095) & ~(size_t)4095;
+    if (b->p) {
+        if (orkh_sync(c->stream) != 0) orki_hip_fail("stage sync");
+        orkh_host_free(b->p);
+    }
+    b->p = orkh_host_alloc(want);
+    b->n = b->p ? want : 0;
+    if (!b->p) orki_hip_fail("pinned staging alloc");
+    return b->p;
+}
+
+/* The [p, p+n) span inside one ork_dma_alloc buffer: its base, or NULL. */
+static const struct ork_buf *dma_span(ork_npu *c, const void *p, size_t n) {
+    for (int i = 0; i < c->dma_n; i++) {
+        const char *b = c->dma[i].p;
+        if ((const char *)p >= b && (const char *)p + n <= b + c->dma[i].n) return &c->dma[i];
+    }
+    return NULL;
+}
+
+/* A pageable host A would be staged a second time inside the runtime's copy, which also blocks the caller; one
+ * CPU memcpy into pinned staging makes the upload a plain DMA on the stream. An A inside an ork_dma_alloc
+ * buffer is already pinned. The staging is reused by the next run: every run with a host A syncs its stream
+ * before returning, so no upload from it is still pending then. */
+const void *orki_host_a(ork_npu *c, const void *A, size_t n) {
+    void *s = orki_stage(c, &c->sA, n);
+    if (!s) return NULL;
+    const void *src = A;
+    if (!dma_span(c, A, n)) {
+        void *h = orki_hstage(c, &c->hA, n);
+        if (!h) return NULL;
+        memcpy(h, A, n);
+        src = h;
+    }
+    return orkh_h2d(s, src, n, c->stream) ? NULL : s;
+}
+
+/* Where the kernels write a host C:
+ *   ORKI_C_INPLACE  C lies in an ork_dma_alloc buffer (pinned, device-mapped): written in place;
+ *   ORKI_C_PINNED   up to ORKI_HOST_C_DIRECT bytes: written across PCIe into pinned staging, copied to C by
+ *                   the CPU after the sync -- no device-to-host copy command and its completion round trip;
+ *   ORKI_C_HBM      larger: HBM staging, brought back by one D2H copy on the stream. */
+void *orki_host_c(ork_npu *c, void *C, size_t n, int *mode) {
+    const struct ork_buf *d = dma_span(c, C, n);
+    if (d) {
+        char *base = orkh_host_devptr(d->p);
+        *mode = ORKI_C_INPLACE;
+        return base ? base + ((char *)C - (char *)d->p) : NULL;
+    }
+    if (n <= ORKI_HOST_C_DIRECT) {
+        void *h = orki_hstage(c, &c->hC, n);
+        *mode = ORKI_C_PINNED;
+        return h ? orkh_host_devptr(h) : NULL;
+    }
+    *mode = ORKI_C_HBM;
+    return orki_stage(c, &c->sC, n);
+}
+
+int orki_host_c_post(ork_npu *c, void *C, const void *dC, size_t n, int mode) {
+    return mode == ORKI_C_HBM ? orkh_d2h(C, dC, n, c->stream) : 0;
+}
+
+void orki_host_c_done(ork_npu *c, void *C, size_t n, int mode) {
+    if (mode == ORKI_C_PINNED) memcpy(C, c->hC.p, n);
 }
 
 void *ork_dma_alloc(ork_npu *c, size_t size) {

@@ -28,6 +28,9 @@ struct ork_npu {
     int async;
     /* device staging for host-side A / C, split-K / grouped partials and grouped-run scales, grown on demand */
     struct ork_buf sA, sC, sW, sS;
+    /* pinned, device-mapped host staging for host-side A (filled by the CPU, uploaded by one DMA copy) and
+     * small host-side C (written by the kernels across PCIe, copied out by the CPU after the sync) */
+    struct ork_buf hA, hC;
     /* ork_dma_alloc (pinned host) and ork_dev_alloc (HBM) registries */
     struct ork_buf dma[ORK_DMA_MAX];
     int dma_n;
@@ -92,8 +95,19 @@ void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB,
 /* ---- context helpers (context.c) ---- */
 int   orki_need_device(const ork_npu *c, const char *who);
 void *orki_stage(ork_npu *c, struct ork_buf *b, size_t n);
+void *orki_hstage(ork_npu *c, struct ork_buf *b, size_t n); /* pinned, device-mapped host memory */
 int   orki_dev_find(ork_npu *c, const void *p, size_t n);   /* 1 if [p,p+n) lies in an ork_dev_alloc buffer */
 int   orki_dma_find(ork_npu *c, const void *p);             /* 1 if p lies in an ork_dma_alloc buffer */
+/* Host operands of a run. orki_host_a: device copy of a host A (async upload on the stream; NULL on failure).
+ * orki_host_c: the device-visible pointer the kernels write a host C through, and how it reaches C (*mode);
+ * orki_host_c_post: after the launches (queues the D2H copy where one is needed);
+ * orki_host_c_done: after the stream sync (the CPU copy-out where one is needed). */
+enum { ORKI_C_INPLACE = 0, ORKI_C_PINNED = 1, ORKI_C_HBM = 2 };
+#define ORKI_HOST_C_DIRECT (1u << 20) /* host C up to this size is written straight into pinned memory */
+const void *orki_host_a(ork_npu *c, const void *A, size_t n);
+void *orki_host_c(ork_npu *c, void *C, size_t n, int *mode);
+int   orki_host_c_post(ork_npu *c, void *C, const void *dC, size_t n, int mode);
+void  orki_host_c_done(ork_npu *c, void *C, size_t n, int mode);
 void  orki_orphan(ork_npu *c, void *dptr);
 ork_w *orki_w_new(ork_npu *c, int K, int N, int dtype, int rkind);
 int   orki_w_upload(ork_w *w, const void *panels);

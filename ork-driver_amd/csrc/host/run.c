@@ -5,8 +5,9 @@
  * (src/npu/core/submit.c:532-539) and its -1. Behaviour kept: run dtype must match the pack dtype,
  * overlapping A and C are refused, C is valid on return. What changes: one HIP launch (plus a split-K
  * reduce when planned) replaces the per-slice NPU submits and the host K-slice accumulate; operands
- * already in HBM (ork_dev_alloc) are used in place, host operands move by async copies on the
- * context's stream. There is no CPU fallback: an offline context or a device error returns -1. */
+ * already in HBM (ork_dev_alloc) are used in place; a host A is uploaded from pinned staging by one DMA
+ * copy on the context's stream, and a host C up to 1 MiB is written by the kernels straight into pinned,
+ * device-mapped memory (larger ones come back by one D2H copy). There is no CPU fallback: an offline context or a device error returns -1. */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -49,15 +50,9 @@ static int run_common(const char *who, ork_npu *c, ork_w *w, int want_dt, int M,
     const int c_dev = orki_dev_find(c, C, cbytes);
     const void *dA = A;
     void *dC = C;
-    if (!a_dev) {
-        void *s = orki_stage(c, &c->sA, abytes);
-        if (!s || orkh_h2d(s, A, abytes, c->stream)) { orki_hip_fail(who); return -1; }
-        dA = s;
-    }
-    if (!c_dev) {
-        dC = orki_stage(c, &c->sC, cbytes);
-        if (!dC) { orki_hip_fail(who); return -1; }
-    }
+    int cmode = ORKI_C_INPLACE;
+    if (!a_dev && !(dA = orki_host_a(c, A, abytes))) { orki_hip_fail(who); return -1; }
+    if (!c_dev && !(dC = orki_host_c(c, C, cbytes, &cmode))) { orki_hip_fail(who); return -1; }
 
     orkh_plan q;
     size_t ws = 0;
@@ -80,9 +75,10 @@ static int run_common(const char *who, ork_npu *c, ork_w *w, int want_dt, int M,
     p.ldc = N;
     memcpy(p.lut, w->lut, sizeof p.lut);
     if (orkh_mm_launch(&p, &q, c->stream)) { orki_hip_fail(who); return -1; }
-    if (!c_dev && orkh_d2h(C, dC, cbytes, c->stream)) { orki_hip_fail(who); return -1; }
+    if (!c_dev && orki_host_c_post(c, C, dC, cbytes, cmode)) { orki_hip_fail(who); return -1; }
     if (c->async && a_dev && c_dev) return 0;
     if (orkh_sync(c->stream)) { orki_hip_fail(who); return -1; }
+    if (!c_dev) orki_host_c_done(c, C, cbytes, cmode);
     return 0;
 }
 
@@ -141,11 +137,7 @@ static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M
     const void *dA = A;
     const float *dAS = aS, *dBS = bS;
     float *dC = C;
-    if (!a_dev) {
-        void *st = orki_stage(c, &c->sA, abytes);
-        if (!st || orkh_h2d(st, A, abytes, c->stream)) { orki_hip_fail(who); return -1; }
-        dA = st;
-    }
+    if (!a_dev && !(dA = orki_host_a(c, A, abytes))) { orki_hip_fail(who); return -1; }
     if (!as_dev || !bs_dev) {
         const size_t boff = (asz + 255) & ~(size_t)255;
         uint8_t *st = orki_stage(c, &c->sS, boff + bsz);
@@ -159,7 +151,8 @@ static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M
             dBS = (const float *)(st + boff);
         }
     }
-    if (!c_dev && !(dC = orki_stage(c, &c->sC, cbytes))) { orki_hip_fail(who); return -1; }
+    int cmode = ORKI_C_INPLACE;
+    if (!c_dev && !(dC = orki_host_c(c, C, cbytes, &cmode))) { orki_hip_fail(who); return -1; }
     orkh_mm p;
     memset(&p, 0, sizeof p);
     p.kind = w->rkind;
@@ -176,9 +169,10 @@ static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M
     orki_plan_grouped(c, w->rkind, M, K, N, w->KB, G, &q);
     const int rc = orkh_mm_launch_grouped(&p, &q, G, dAS, dBS, dC, N, c->stream);
     if (rc) { orki_hip_fail(who); return -1; }
-    if (!c_dev && orkh_d2h(C, dC, cbytes, c->stream)) { orki_hip_fail(who); return -1; }
+    if (!c_dev && orki_host_c_post(c, C, dC, cbytes, cmode)) { orki_hip_fail(who); return -1; }
     if (c->async && a_dev && c_dev && as_dev && bs_dev) return 0;
     if (orkh_sync(c->stream)) { orki_hip_fail(who); return -1; }
+    if (!c_dev) orki_host_c_done(c, C, cbytes, cmode);
     return 0;
 }
 

@@ -101,6 +101,27 @@ def test_i8_chain_cstride_and_device_operands(npu):
     ork.free(w2)
 
 
+@pytest.mark.parametrize("rows_big", [40, 300])
+def test_i8_chain_host_c_staging(npu, rows_big):
+    """Host C of a chain below and above the 1 MiB pinned-staging limit (kernels write pinned memory, or HBM
+    staging with strided copies back), with a C row stride; a second call reuses the grown staging."""
+    _say("chain host C", rows_big)
+    rng = np.random.default_rng(73)
+    K, N, Nw = 256, 1024, 1040
+    Bs = [rng.integers(-128, 128, size=(K, N), dtype=np.int8) for _ in range(3)]
+    ws = [npu.pack_i8(B) for B in Bs]
+    for rep in range(2):
+        Ms = [1, rows_big, 3 + rep]
+        As = [rng.integers(-127, 128, size=(M, K), dtype=np.int8) for M in Ms]
+        Cs = [np.full((M, Nw), 777, np.int32) for M in Ms]
+        t = ork.tasks(ork.TaskI8, [(w, M, A, C, Nw) for w, M, A, C in zip(ws, Ms, As, Cs)])
+        assert ork.lib().ork_i8_mm_run_chain(npu.h, 3, t) == 0
+        for A, B, C in zip(As, Bs, Cs):
+            assert np.array_equal(C[:, :N], O.gemm_i32(A, B)) and np.all(C[:, N:] == 777)
+    for w in ws:
+        ork.free(w)
+
+
 @pytest.mark.parametrize("entry", ["ork_i4_mm_run_chain", "ork_i4_mm_run_stream"])
 def test_i4_chain(npu, entry):
     _say(entry)

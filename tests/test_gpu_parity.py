@@ -418,6 +418,46 @@ def test_dma_buffers(npu):
     ork.free(w)
 
 
+@pytest.mark.parametrize("kind", ["i8", "f16"])
+def test_host_operand_modes(npu, kind):
+    """Host C on either side of the 1 MiB pinned-staging limit (written by the kernels into pinned memory, or
+    staged in HBM and copied back), in both orders so the staging is grown and reused, and C / A placed at
+    offsets inside ork_dma_alloc buffers (written and read in place)."""
+    import ctypes as Ct
+
+    L = ork.lib()
+    rng = _rng(79)
+    K, N = 256, 2048  # one C row is 8 KiB: M=128 is exactly 1 MiB
+    if kind == "i8":
+        B = rng.integers(-127, 128, size=(K, N), dtype=np.int8)
+        w = npu.pack_i8(B)
+        mk = lambda M: rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+        run, ref, ct = npu.run_i8, (lambda A: O.gemm_i32(A, B)), Ct.c_int32
+    else:
+        B = rng.integers(-3, 4, size=(K, N)).astype(np.float16)
+        w = npu.pack_f16(B)
+        mk = lambda M: rng.integers(-3, 4, size=(M, K)).astype(np.float16)  # integer-valued: exact in fp32
+        run, ref, ct = npu.run_f16, (lambda A: (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)), Ct.c_float
+    for M in (1, 128, 129, 7, 300, 3):
+        print(f"[case] host C {kind} M={M} ({M * N * 4} bytes)", flush=True)
+        A = mk(M)
+        rc, C = run(w, A)
+        assert rc == 0
+        assert np.array_equal(C, ref(A)), f"M={M}"
+    M = 5
+    A = mk(M)
+    pa = L.ork_dma_alloc(npu.h, A.nbytes + 256)
+    pc = L.ork_dma_alloc(npu.h, M * N * 4 + 4096)
+    Ct.memmove(pa + 256, A.ctypes.data, A.nbytes)
+    fn = L.ork_i8_mm_run if kind == "i8" else L.ork_f16_mm_run
+    assert fn(npu.h, w, M, pa + 256, pc + 4096) == 0
+    C = np.ctypeslib.as_array(Ct.cast(pc + 4096, Ct.POINTER(ct)), shape=(M, N)).copy()
+    assert np.array_equal(C, ref(A))
+    L.ork_dma_free(npu.h, pa)
+    L.ork_dma_free(npu.h, pc)
+    ork.free(w)
+
+
 def test_run_errors(npu):
     import ctypes as Ct
 
