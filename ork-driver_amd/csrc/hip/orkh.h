@@ -96,6 +96,9 @@ typedef struct orkh_plan {
     int mt, wpg, kbw, kbs, ksplit;
     /* TILED: bm x bn output tile per 256-thread workgroup, K staged through LDS. */
     int bm, bn;
+    /* TILED2: 1 = load A stages as whole 128-byte row lines into a swizzled LDS image where the stage's rows
+     * are one line each (else, and with 0, in MFMA fragment order) */
+    int aline;
     void *ws;             /* split-K partials, >= ksplit*M*N*4 bytes (device) */
 } orkh_plan;
 

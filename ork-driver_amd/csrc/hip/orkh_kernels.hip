@@ -469,8 +469,31 @@ template <int KIND, int BM, int BN, int KS> struct T2 {
     static constexpr int DEC = KIND == ORKH_NF4 ? NIB * T::STEPS * 1024 : 0;
     static constexpr int R = ((163840 - DEC) / SLOT) < 4 ? ((163840 - DEC) / SLOT) : 4; // ring within 160 KiB
     static constexpr size_t LDS = (size_t)R * SLOT + DEC;
+    // A stage whose rows are one 128-byte line each is loaded a line at a time (8 rows x 128 B per instruction)
+    // instead of in MFMA fragment order (16 rows x 64 B: every line fetched by two instructions), and read from
+    // a swizzled image (a_lds)
+    static constexpr bool LINE_OK = KS * T::KPB * T::ESZ == 128;
     static_assert(MB % WM == 0 && NB % WN == 0 && R >= 2 && (R - 2) * IPW < 64, "tile");
+    static_assert(!LINE_OK || NIA * 8 == BM, "line-loaded A: one instruction per 8 rows");
 };
+
+// Index (in 16-byte units) within a stage's A image of lane `lane`'s operand of fragment (mb, kbl, st).
+// Fragment order: fragment f = (mb, kbl, st) is 1 KiB at f, lane-major, as mma() takes it.
+// Line order: 8-row groups of 1 KiB; row r's 128-byte line holds its 16-byte chunk c at slot
+// c ^ (r & 7) ^ ((r >> 3) & 1). The swizzle puts the chunks that any 16 consecutive lanes of a fragment read
+// (16 rows, one chunk) in 16 distinct bank groups, so the 128-bit LDS reads stay conflict-free; the loads
+// write each instruction's 8 lines with the same permutation (lane l of instruction j: row 8j + l/8, slot l % 8).
+template <int KIND, int KS, bool LINE>
+__device__ __forceinline__ int a_lds(int mb, int kbl, int st, int lane) {
+    using T = KT<KIND>;
+    if constexpr (LINE) {
+        const int c = (kbl * T::KPB + a_koff<KIND>(st, lane >> 4)) * T::ESZ / 16;
+        const int r7 = lane & 7, h = (lane >> 3) & 1;
+        return (mb * 2 + h) * 64 + r7 * 8 + (c ^ r7 ^ h);
+    } else {
+        return ((mb * KS + kbl) * T::STEPS + st) * 64 + lane;
+    }
+}
 
 // Quotient and remainder of a wave-uniform x / d (0 <= x, 1 <= d, both < 2^24) on the VALU: the correctly
 // rounded float quotient is within one of the integer one, and one correction fixes it. A scalar integer
@@ -493,13 +516,14 @@ struct T2Group {
     const float *bS;  // [K/G][N]
 };
 
-template <int KIND, int BM, int BN, int KS, int GR>
+template <int KIND, int BM, int BN, int KS, int GR, bool AL>
 __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int ntiles_all, int kbs, void *ws,
                                             const T2Group &gp) {
 #pragma clang fp contract(off)
     using T = KT<KIND>;
     using P = T2<KIND, BM, BN, KS>;
     constexpr int R = P::R;
+    constexpr bool LINE = AL && P::LINE_OK; // A stage as whole row lines (a_lds), else in fragment order
     typedef typename T::acc_t acc_t;
     typedef typename T::c_t c_t;
     extern __shared__ v4i sm[];
@@ -532,7 +556,13 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         const int i = wv + q * P::NW;
         voff[q] = OOB;
         kof[q] = 0;
-        if (i < P::NIA) {
+        if (i < P::NIA && LINE) {
+            // rows 8i .. 8i+7, each a whole 128-byte line; lane l fills slot l % 8 of row 8i + l / 8
+            const int rr = lane >> 3, slot = lane & 7;
+            const int row = m0 + i * 8 + rr;
+            kof[q] = (slot ^ rr ^ (i & 1)) * 16 / T::ESZ;
+            if (row < p.M) voff[q] = (uint32_t)row * lda_b + (uint32_t)kof[q] * T::ESZ;
+        } else if (i < P::NIA) {
             const int mb = i / (KS * T::STEPS), rest = i % (KS * T::STEPS);
             const int kbl = rest / T::STEPS, st = rest % T::STEPS;
             const int row = m0 + mb * 16 + (lane & 15);
@@ -668,7 +698,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                 for (int st = 0; st < T::STEPS; st++)
 #pragma unroll
                     for (int i = 0; i < P::MTW; i++) {
-                        const v4i a = As[(((wm * P::MTW + i) * KS + kbl) * T::STEPS + st) * 64 + lane];
+                        const v4i a = As[a_lds<KIND, KS, LINE>(wm * P::MTW + i, kbl, st, lane)];
 #pragma unroll
                         for (int jn = 0; jn < P::NTW; jn++) acc[i][jn] = mma(a, op[jn][st], acc[i][jn]);
                     }
@@ -694,7 +724,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                 for (int st = 0; st < T::STEPS; st++)
 #pragma unroll
                     for (int i = 0; i < P::MTW; i++)
-                        afr[kbl][st][i] = As[(((wm * P::MTW + i) * KS + kbl) * T::STEPS + st) * 64 + lane];
+                        afr[kbl][st][i] = As[a_lds<KIND, KS, LINE>(wm * P::MTW + i, kbl, st, lane)];
             }
 #pragma unroll
             for (int kbl = 0; kbl < KS; kbl++) {
@@ -748,17 +778,17 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         }
 }
 
-template <int KIND, int BM, int BN, int KS>
+template <int KIND, int BM, int BN, int KS, bool AL>
 __global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntiles_all, int kbs, void *ws) {
-    tiled2_body<KIND, BM, BN, KS, 0>(p, mtiles, ntiles_all, kbs, ws, T2Group{0, nullptr, nullptr});
+    tiled2_body<KIND, BM, BN, KS, 0, AL>(p, mtiles, ntiles_all, kbs, ws, T2Group{0, nullptr, nullptr});
 }
 
 // Grouped runs (never K-split: the groups close in order inside one workgroup). GR 2: every group is whole
 // stages (G % (KS * KPB) == 0), so the stage runs as in the plain kernel and a group closes between stages;
 // GR 1: any G % 32 == 0, walked K-block by K-block.
-template <int KIND, int BM, int BN, int KS, int GR>
+template <int KIND, int BM, int BN, int KS, int GR, bool AL>
 __global__ __launch_bounds__(1024) void k_tiled2g(orkh_mm p, int mtiles, int ntiles_all, T2Group gp) {
-    tiled2_body<KIND, BM, BN, KS, GR>(p, mtiles, ntiles_all, p.KB, nullptr, gp);
+    tiled2_body<KIND, BM, BN, KS, GR, AL>(p, mtiles, ntiles_all, p.KB, nullptr, gp);
 }
 
 // Dynamic LDS of k_tiled: KG groups x 2 stage buffers of A fragments, or (KG > 1) the 4-wave partial
@@ -1035,9 +1065,10 @@ template <int KIND, int BM, int BN>
 int launch_tiled2_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int KS = t2_ks<KIND, BM, BN>();
     using P = T2<KIND, BM, BN, KS>;
-    auto kern = k_tiled2<KIND, BM, BN, KS>;
-    static lds_flags attr; // per instantiation: allow more than the default 64 KiB of dynamic LDS
-    if (lds_limit((const void *)kern, (int)P::LDS, attr)) return -1;
+    const bool al = q->aline && P::LINE_OK;
+    auto kern = al ? k_tiled2<KIND, BM, BN, KS, true> : k_tiled2<KIND, BM, BN, KS, false>;
+    static lds_flags attr[2]; // per instantiation: allow more than the default 64 KiB of dynamic LDS
+    if (lds_limit((const void *)kern, (int)P::LDS, attr[al])) return -1;
     const int mtiles = (p->M + BM - 1) / BM;
     const int ntiles = (p->N / 16 + P::NB - 1) / P::NB;
     const int ksplit = q->ksplit > 1 ? q->ksplit : 1;
@@ -1184,7 +1215,7 @@ int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s) {
     constexpr int KS = t2_ks<KIND, BM, BN>();
     using P = T2<KIND, BM, BN, KS>;
     const bool whole = gp.G % (KS * KT<KIND>::KPB) == 0;
-    auto kern = whole ? k_tiled2g<KIND, BM, BN, KS, 2> : k_tiled2g<KIND, BM, BN, KS, 1>;
+    auto kern = whole ? k_tiled2g<KIND, BM, BN, KS, 2, false> : k_tiled2g<KIND, BM, BN, KS, 1, false>;
     const int Sk = p->K / gp.G;
     const size_t lds = P::LDS + (size_t)((BM * Sk * 4 + 1023) / 1024 + (Sk * BN * 4 + 1023) / 1024) * 1024;
     if (lds > 163840) {
@@ -1276,9 +1307,10 @@ extern "C" const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *q) {
     else if (q->algo == ORKH_ALGO_STREAM)
         snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d", k, q->mt, q->wpg, q->kbw, q->ksplit);
     else if (q->ksplit > 1)
-        snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
-                 q->ksplit);
+        snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
+                 q->ksplit, q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");
     else
-        snprintf(b, sizeof b, "%s_%s_%dx%d", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn);
+        snprintf(b, sizeof b, "%s_%s_%dx%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
+                 q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");
     return b;
 }

@@ -136,7 +136,31 @@ static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force,
     return best;
 }
 
+static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes);
+
+/* A-stage layout of the LDS-ring kernel: whole 128-byte row lines (swizzled LDS image) or MFMA fragment
+ * order. Measured on MI355X, graph-timed, both layouts in one run (us, fragment -> line):
+ *   int8 K=2048 N=6144: M=512 64x192 14.9 -> 14.5, 128x128 15.5 -> 14.5; M=1024 64x192 27.4 -> 26.6,
+ *                       128x128 29.4 -> 27.7; M=256 64x192 13.1 -> 12.6; M=128 64x64 8.54 -> 8.63
+ *   fp16 K=N=2048:      M=512 64x64 13.1 -> 13.3, 128x128 23.7 -> 21.7, 64x192 21.1 -> 20.0
+ *   W4A4 K=N=4096:      M=256 64x64 13.7 -> 14.4, 64x192 21.5 -> 23.0, 128x128 23.0 -> 21.5
+ * so lines everywhere except the 64x64 tile and the nibble kinds' 64-row tiles. ORK_ALINE=0/1 forces it
+ * (tests, A/B timing). */
+static int aline_rule(int rkind, const orkh_plan *q) {
+    const char *e = getenv("ORK_ALINE");
+    if (e) return atoi(e) != 0;
+    if (q->bm == 64 && q->bn == 64) return 0;
+    if ((rkind == ORKH_I4U || rkind == ORKH_NF4) && q->bm == 64) return 0;
+    return 1;
+}
+
 int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes) {
+    const int rc = plan_core(c, rkind, M, K, N, KB, q, ws_bytes);
+    if (q->algo == ORKH_ALGO_TILED2) q->aline = aline_rule(rkind, q);
+    return rc;
+}
+
+static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes) {
     (void)K;
     memset(q, 0, sizeof *q);
     *ws_bytes = 0;

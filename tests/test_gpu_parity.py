@@ -480,13 +480,25 @@ def test_run_errors(npu):
 
 @pytest.mark.parametrize("tile", ["256x256", "128x128", "64x192", "64x64"])
 @pytest.mark.parametrize("ks", [1, 3])
-def test_lds_ring_tiles_all_kinds(npu, tile, ks):
-    """The LDS-ring tiled kernel at every tile shape the planner can choose, unsplit and K-split: exact for
-    int8, uniform-int4 and NF4 i4a8 and W4A4, within the fp16 bar (and run-to-run identical) for fp16. M, N and K
-    tails: M = 300 and 70 are no tile multiple, N = 224 (14 panels) leaves a partial tile for every tile
-    width, K = 2080 ends mid K-block for int8 (K % 64 = 32) and the nibble kinds (K % 128 = 32)."""
-    _say("lds-ring tile", tile, "ks", ks)
-    rng = np.random.default_rng(hash((tile, ks)) % 2**32)
+@pytest.mark.parametrize("aline", [0, 1])
+def test_lds_ring_tiles_all_kinds(npu, tile, ks, aline):
+    """The LDS-ring tiled kernel at every tile shape the planner can choose, unsplit and K-split, with A stages
+    in fragment order and as whole row lines (ORK_ALINE; 256x256 has 64-byte stage rows and always uses
+    fragment order): exact for int8, uniform-int4 and NF4 i4a8 and W4A4, within the fp16 bar (and run-to-run
+    identical) for fp16. M, N and K tails: M = 300 and 70 are no tile multiple, N = 224 (14 panels) leaves a
+    partial tile for every tile width, K = 2080 ends mid K-block for int8 (K % 64 = 32) and the nibble kinds
+    (K % 128 = 32)."""
+    _say("lds-ring tile", tile, "ks", ks, "aline", aline)
+    os.environ["ORK_ALINE"] = str(aline)
+    try:
+        _lds_ring_tiles_all_kinds(npu, tile, ks)
+    finally:
+        os.environ.pop("ORK_ALINE", None)
+
+
+def _lds_ring_tiles_all_kinds(npu, tile, ks):
+    bm, bn = map(int, tile.split("x"))
+    rng = np.random.default_rng(bm * 1000 + bn * 10 + ks)  # fixed per case (str hash() is salted per process)
     K, N = 2080, 224
     for M in (300, 70):
         B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
