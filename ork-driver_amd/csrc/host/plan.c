@@ -11,7 +11,7 @@
  *   M <= 64  the streaming kernel (same grid, runs of 1-4 KiB) or the LDS-ring tiled kernel, whichever a
  *            delivery model of both prices lower, each with its best K split (NF4: streaming, by the
  *            occupancy rule of the GEMV).
- *   M >  64  the LDS-ring tiled kernel (k_tiled for NF4 below 256 rows): the tile and K split with the least
+ *   M >  64  the LDS-ring tiled kernel (k_tiled for NF4 up to 128 rows): the tile and K split with the least
  *            modelled time.
  * Both time models charge a workgroup for a fixed set-up, the operand bytes that must reach its CU and
  * its multiply-accumulates; a K split adds its partials' round trip and the reduce launch.
@@ -214,16 +214,17 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
         return 0;
     }
 
-    /* NF4 takes the LDS-ring kernel from 256 rows (its stage decode into LDS beats k_tiled there: 16.7 vs
-     * 20.7 us at M=256, 21.5 vs 22.6 us at M=512, K=2048 N=6144) and k_tiled below (11.3 vs 12.0 us at M=128) */
-    if ((rkind != ORKH_NF4 || M >= 256) && !f_tiled) {
+    /* NF4 takes the LDS-ring kernel above 128 rows (its stage decode into LDS beats k_tiled there: 16.4 vs
+     * 19.6 us at M=192, 16.7 vs 20.7 us at M=256, 21.5 vs 22.6 us at M=512, K=2048 N=6144) and k_tiled up to
+     * 128 rows, where k_tiled's 64 x 64 tiles still fit one round on the CUs (11.3 vs 11.9 us at M=128) */
+    if ((rkind != ORKH_NF4 || M > 128) && !f_tiled) {
         /* uniform int4 skips the 256 x 256 tile: with the nibble decode its registers spill (20 B per lane) */
         tiled2_best(rkind, M, N, KB, cu, ks_force, rkind == ORKH_I4U, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }
 
-    /* k_tiled (NF4 below 256 rows, or ORK_PLAN=tiled): each CU pulls its tiles' A and B rows through L2 at a roughly fixed
+    /* k_tiled (NF4 up to 128 rows, or ORK_PLAN=tiled): each CU pulls its tiles' A and B rows through L2 at a roughly fixed
      * rate, so the time of a round of workgroups is about the operand bytes one workgroup loads. K is split
      * across workgroups when that cuts the per-workgroup bytes by more than the partial sums and the extra
      * reduce launch (~2 us) cost. Model units: us at ~48 KB/us per CU (measured order of magnitude),
