@@ -114,17 +114,40 @@ def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scale
     return graph, eager
 
 
-def sweep_configs(npu, hip, L, ws_c1, dA, dC):
+def cpu_rows_baseline(fn_rows, M, nbytes, ops, bound, kind, what, budget_s):
+    """One config's CPU baseline in the config's own unit: fn_rows(r) runs the CPU GEMM on the first r rows of
+    the config's A. The reference's CPU GEMMs treat rows independently (a k-outer AXPY per row, or a row loop), so
+    a bounded sample of min(M, 16) rows is timed for ~budget_s seconds and scaled to M rows."""
+    r = min(M, 16)
+    dt, n = _time_calls(lambda: fn_rows(r), budget_s)
+    full = dt * M / r
+    if bound == "hbm":
+        value, unit = nbytes / full / 1e9, "GB/s"
+    else:
+        value, unit = ops / full / 1e12, ("TOP/s" if bound == "mfma_int8" else "TFLOP/s")
+    scaled = f", scaled to M={M}" if r != M else ""
+    return {"value": round(value, 6), "unit": unit, "cores": 1, "kind": kind,
+            "sample": f"{n} calls of {r} row(s): {what}, 1 thread, {dt * 1e3:.2f} ms/call{scaled}; host {cpu_model()}"}
+
+
+def sweep_configs(npu, hip, L, ws_c1, dA, dC, codes1, A512, cpu_s):
     """BASELINE configs 1-4 at their stated shapes, measured like the headline (one HIP graph of
     rotating resident weights, >= 2x the 256 MB MALL, A and C in HBM): throughput and roofline fraction
-    per config. Each result is spot-checked against the oracle on a few rows."""
+    per config. Each result is spot-checked against the oracle on a few rows. With cpu_s > 0 each config
+    also carries its CPU baseline (cpu_rows_baseline, ~cpu_s seconds): the reference's own orki_cpu_gemm_i32 /
+    orki_cpu_gemm_grouped from oracle/_ref for the integer kinds, the oracle's restatement of the reference's
+    fp32-accumulate loop (examples/test_matmul.c:37) for fp16."""
     import ork
     import oracle as O
 
     rng = np.random.default_rng(0x6F726B00 + (9 << 8))
     out = []
+    have_ref = O.ref_available()
+    gemm = O.ref_gemm_i32 if have_ref else O.gemm_i32
+    gkind = "reference" if have_ref else "port"
+    gwhat = "orki_cpu_gemm_i32 as built (-O2)" if have_ref else "oracle restatement of orki_cpu_gemm_i32"
 
-    def rec(name, plan, M, ms, nbytes, ops, bound):
+    def rec(name, plan, M, ms, nbytes, ops, bound, cpu=None):
         us = ms * 1e3
         if bound == "hbm":
             val, unit, peak = nbytes / (ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS
@@ -136,13 +159,20 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
                                                "frac": round(val / peak, 4)}})
         print(f"[bench] {name} M={M}: {us:.2f} us ({val:.1f} {unit}, {val / peak:.1%} of peak) {plan}",
               file=sys.stderr, flush=True)
+        if cpu is not None and cpu_s > 0:
+            fn_rows, kind, what = cpu
+            out[-1]["cpu_baseline"] = cpu_rows_baseline(fn_rows, M, nbytes, ops, bound, kind, what, cpu_s)
+            cb = out[-1]["cpu_baseline"]
+            print(f"[bench]   CPU: {cb['value']:.4g} {cb['unit']} ({cb['kind']}, {cb['sample']})", file=sys.stderr,
+                  flush=True)
 
     def steps_for(ms_guess):
         return max(64, min(2400, int(400.0 / max(ms_guess * 1e3, 1.0))))
 
     # ---- config 1, M=16 (the headline weights)
     g, _ = measure(npu, hip, ws_c1, 16, dA, dC, 960, 48)
-    rec("C1 w8a8 K=2048 N=6144", npu.plan_name(ws_c1[0], 16), 16, g, K * N + 16 * K + 4 * 16 * N, 2 * 16 * N * K, "hbm")
+    rec("C1 w8a8 K=2048 N=6144", npu.plan_name(ws_c1[0], 16), 16, g, K * N + 16 * K + 4 * 16 * N, 2 * 16 * N * K, "hbm",
+        (lambda r: gemm(A512[:r], codes1), gkind, gwhat))
 
     # ---- config 2: fp16, K = N = 2048, M in {1, 16, 128, 512}
     K2 = N2 = 2048
@@ -155,7 +185,9 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
         n = steps_for(0.006 if M < 512 else 0.012)
         g, _ = measure(npu, hip, ws2, M, dA2, dC, n, 16, "ork_f16_mm_run")
         rec("C2 fp16 K=N=2048", npu.plan_name(ws2[0], M), M, g, 2 * M * K2 + 2 * K2 * N2 + 4 * M * N2,
-            2 * M * N2 * K2, "hbm" if M <= 128 else "mfma_fp16")
+            2 * M * N2 * K2, "hbm" if M <= 128 else "mfma_fp16",
+            (lambda r: O.gemm_f16_f32acc(A2[:r], B2), "port",
+             "oracle restatement of the reference's fp32-accumulate fp16 loop (examples/test_matmul.c:37)"))
     L.ork_npu_set_async(npu.h, 0)
     C2 = np.empty((4, N2), np.float32)
     assert L.ork_f16_mm_run(npu.h, ws2[0], 4, dA2, dC) == 0
@@ -179,17 +211,18 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
         blob = ork.dump_i4a8(w0)
         ws3 = [w0] + [npu.load_i4a8(K, N, blob) for _ in range(83)]   # 84 x 6.3 MB
         assert all(ws3)
+        _, codes3 = O.o4n1_decode(K, N, blob)   # the reference's CPU path: inflate at load, then the int8 GEMM
         name = "C3 w4a8 %s K=2048 N=6144" % ("nf4" if nf4 else "uniform")
         for M in (1, 64):
             g, _ = measure(npu, hip, ws3, M, dA, dC, steps_for(0.003), 32)
-            rec(name, npu.plan_name(ws3[0], M), M, g, K * N // 2 + M * K + 4 * M * N, 2 * M * N * K, "hbm")
+            rec(name, npu.plan_name(ws3[0], M), M, g, K * N // 2 + M * K + 4 * M * N, 2 * M * N * K, "hbm",
+                (lambda r, c3=codes3: gemm(A512[:r], c3), gkind, gwhat + " on the inflated codes"))
         L.ork_npu_set_async(npu.h, 0)
         A3 = np.empty((2, K), np.int8)
         assert L.ork_dev_download(npu.h, ork.ptr(A3), dA, A3.nbytes) == 0
         C3 = np.empty((2, N), np.int32)
         assert L.ork_i8_mm_run(npu.h, ws3[-1], 2, dA, dC) == 0
         assert L.ork_dev_download(npu.h, ork.ptr(C3), dC, C3.nbytes) == 0
-        _, codes3 = O.o4n1_decode(K, N, blob)
         assert np.array_equal(C3, O.gemm_i32(A3, codes3)), "w4a8 spot check"
         L.ork_npu_set_async(npu.h, 1)
         for w in ws3:
@@ -204,7 +237,8 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
     assert all(ws4) and dA4 and L.ork_dev_upload(npu.h, dA4, ork.ptr(A4), A4.nbytes) == 0
     g, _ = measure(npu, hip, ws4, 256, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run")
     rec("C4 W4A4 K=N=4096", npu.plan_name(ws4[0], 256), 256, g, 256 * K4 + K4 * N4 // 2 + 4 * 256 * N4,
-        2 * 256 * N4 * K4, "mfma_int8")
+        2 * 256 * N4 * K4, "mfma_int8",
+        (lambda r: gemm(A4[:r], B4), gkind, gwhat + " on the int8 containers (ork_i4_mm_run's offline branch)"))
     L.ork_npu_set_async(npu.h, 0)
     C4 = np.empty((256, N4), np.int32)
     assert L.ork_dev_download(npu.h, ork.ptr(C4), dC, C4.nbytes) == 0
@@ -218,6 +252,8 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
     # grouped int8 shape of examples/test_grouped_i8.c (W4A4 pack loaded as int8, K=2048, N=16384, G=512)
     G4 = 128
     Sk4 = K4 // G4
+    ggemm = O.ref_gemm_grouped if have_ref else O.gemm_grouped
+    ggwhat = "orki_cpu_gemm_grouped as built (-O2)" if have_ref else "oracle restatement of orki_cpu_gemm_grouped"
     aS4 = rng.uniform(1e-3, 1e-2, size=(256, Sk4)).astype(np.float32)
     bS4 = rng.uniform(1e-3, 1e-2, size=(Sk4, N4)).astype(np.float32)
     dS4 = [L.ork_dev_alloc(npu.h, a.nbytes) for a in (aS4, bS4)]
@@ -228,7 +264,8 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
         g, _ = measure(npu, hip, wg4, M, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run_grouped", dS4)
         nbytes = K4 * N4 // 2 + M * K4 + 4 * (M * Sk4 + Sk4 * N4) + 4 * M * N4
         rec("grouped W4A4 K=N=4096 G=128", npu.grouped_plan_name(wg4[0], M), M, g, nbytes, 2 * M * N4 * K4,
-            "hbm" if M <= 16 else "mfma_int8")
+            "hbm" if M <= 16 else "mfma_int8",
+            (lambda r: ggemm(A4[:r], B4, aS4[:r], bS4, G4), gkind, ggwhat))
     L.ork_npu_set_async(npu.h, 0)
     Cg = np.empty((256, N4), np.float32)  # what the timed M=256 launches wrote (every copy holds B4)
     assert L.ork_dev_download(npu.h, ork.ptr(Cg), dC, Cg.nbytes) == 0
@@ -253,7 +290,8 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC):
     assert all(L.ork_dev_upload(npu.h, d, ork.ptr(a), a.nbytes) == 0 for d, a in zip(dS8, (aS8, bS8)))
     g, _ = measure(npu, hip, wg8, M8, dA, dC, steps_for(0.01), 16, "ork_i8_mm_run_grouped", dS8)
     rec("grouped int8 (W4A4 pack) K=2048 N=16384 G=512", npu.grouped_plan_name(wg8[0], M8), M8, g,
-        K8 * N8 // 2 + M8 * K8 + 4 * (M8 * 4 + 4 * N8) + 4 * M8 * N8, 2 * M8 * N8 * K8, "hbm")
+        K8 * N8 // 2 + M8 * K8 + 4 * (M8 * 4 + 4 * N8) + 4 * M8 * N8, 2 * M8 * N8 * K8, "hbm",
+        (lambda r: ggemm(A512[:r], B8, aS8[:r], bS8, G8), gkind, ggwhat))
     for w in wg8:
         L.ork_mm_free(npu.h, w)
     for d in dS4 + dS8:
@@ -335,6 +373,35 @@ def measure_decoder(npu, nf4, prompt_len=128, decode_len=256, graph=True):
                          "frac": round(gbs / HBM_PEAK_GBS, 4)},
             "note": "prefill 128 seeded tokens, 256 greedy decode steps (HIP graph per step), batch 1; bytes per "
                     "token = resident weights + scales + fp32 KV cache read at the mean context"}
+
+
+def cpu_decoder_baseline(budget_s):
+    """Config 5's CPU counterpart on a bounded sample: the per-token matmuls of the Qwen3-1.7B shape (28 layers of
+    q, k, v, o, gate, up, down GEMVs and the LM head) through the reference's own orki_cpu_gemm_i32 at M = 1, each
+    distinct shape timed for ~budget_s / 5 seconds. Attention, norms and sampling are left out, so the tokens/s
+    is an upper bound for a CPU decode. The NF4-FFN variant runs the same GEMMs on the CPU (its codes are
+    inflated to int8 at load), so one number serves both."""
+    import oracle as O
+
+    have_ref = O.ref_available()
+    gemm = O.ref_gemm_i32 if have_ref else O.gemm_i32
+    rng = np.random.default_rng(0x6F726B05)
+    H, KV, F, V, layers = 2048, 8 * 128, 6144, 151936, 28
+    per_layer = [((H, H), 2), ((H, KV), 2), ((H, F), 2), ((F, H), 1)]   # (q, o), (k, v), (gate, up), down
+    ms_tok, parts = 0.0, []
+    for (k, n), cnt in per_layer + [((H, V), None)]:
+        B = np.frombuffer(rng.bytes(k * n), np.int8).reshape(k, n)
+        A = rng.integers(-127, 128, size=(1, k), dtype=np.int8)
+        dt, _ = _time_calls(lambda: gemm(A, B), budget_s / 5)
+        ms_tok += dt * 1e3 * (layers * cnt if cnt else 1)
+        parts.append(f"{k}x{n} {dt * 1e3:.2f} ms")
+        del B
+    return {"value": round(1e3 / ms_tok, 3), "unit": "tokens/s", "cores": 1,
+            "kind": "reference" if have_ref else "port",
+            "sample": f"per-token matmuls only (28 layers x q,k,v,o,gate,up,down + LM head) with "
+                      f"{'orki_cpu_gemm_i32 as built (-O2)' if have_ref else 'the oracle restatement'}, M=1, 1 thread, "
+                      f"each distinct shape timed separately ({'; '.join(parts)}) = {ms_tok:.1f} ms/token; attention and glue left "
+                      f"out (an upper bound); host {cpu_model()}"}
 
 
 def copy_calibration(hip, L, reps=96):
@@ -545,7 +612,8 @@ def main():
         configs = None
         if not args.no_configs:
             L.ork_npu_set_async(npu.h, 1)
-            configs = sweep_configs(npu, hip, L, ws, dA, dC)
+            configs = sweep_configs(npu, hip, L, ws, dA, dC, codes, A512,
+                                    0.0 if args.no_cpu else min(2.0, args.cpu_seconds / 5))
             L.ork_npu_set_async(npu.h, 0)
 
         for w in ws:
@@ -554,7 +622,13 @@ def main():
         L.ork_dev_free(npu.h, dC)
 
         if not args.no_decoder:
-            configs = (configs or []) + [measure_decoder(npu, 0), measure_decoder(npu, 1)]
+            dec = [measure_decoder(npu, 0), measure_decoder(npu, 1)]
+            if not args.no_cpu:
+                cb = cpu_decoder_baseline(min(3.0, args.cpu_seconds / 3))
+                print(f"[bench]   CPU decoder: {cb['value']:.3g} tokens/s ({cb['sample']})", file=sys.stderr, flush=True)
+                for d in dec:
+                    d["cpu_baseline"] = cb
+            configs = (configs or []) + dec
 
     gbs = algo_bytes(1) / (g1 * 1e-3) / 1e9
     tops = algo_ops(512) / (g512 * 1e-3) / 1e12
