@@ -432,7 +432,8 @@ __global__ __launch_bounds__(256) void k_grouped(orkh_mm p, int G, const float *
 }
 
 // ------------------------------------------------------------------------------------------------
-// k_tiled2: one 16-wave workgroup per BM x BN output tile (waves 4 x 4 over the tile). Both operands
+// k_tiled2: one 16-wave workgroup per BM x BN output tile (waves 4 x 4 over the tile; on 32-row tiles, groups
+// of waves that split each stage's K-blocks, see T2). Both operands
 // go HBM/L2 -> LDS with direct-to-LDS buffer loads (no VGPR round trip), issued in MFMA fragment order so
 // the LDS image of a stage is already the operand layout: A fragment (mb, kbl, step) = 16 rows x 16 bytes
 // per lane row/k-group exactly as mma() takes it, B = the 1 KiB panel blocks verbatim. A ring of R stage
@@ -458,8 +459,12 @@ template <int VM> __device__ __forceinline__ void wait_vmcnt() {
 
 template <int KIND, int BM, int BN, int KS> struct T2 {
     using T = KT<KIND>;
-    static constexpr int WM = 4, WN = 4, NW = 16;
-    static constexpr int MB = BM / 16, NB = BN / 16, MTW = MB / WM, NTW = NB / WN;
+    static constexpr int MB = BM / 16, NB = BN / 16, NW = 16;
+    // 16 waves: WM x WN over the tile's 16 x 16 blocks and, on tiles of fewer than 16 blocks (32 x 32, 32 x 64),
+    // WK groups that split each stage's K-blocks; their partial tiles are summed through LDS after the loop, in
+    // group order (deterministic for fp16)
+    static constexpr int WM = MB < 4 ? MB : 4, WN = NB < 4 ? NB : 4, WK = NW / (WM * WN);
+    static constexpr int MTW = MB / WM, NTW = NB / WN, KPW = KS / WK; // blocks and K-blocks per wave
     static constexpr int NIA = MB * KS * T::STEPS, NIB = NB * KS, NI = NIA + NIB;  // loads per stage
     static constexpr int IPW = (NI + NW - 1) / NW;                               // per wave
     static constexpr int JUNK = IPW * NW > NI ? 1 : 0;
@@ -467,13 +472,18 @@ template <int KIND, int BM, int BN, int KS> struct T2 {
     // NF4: a stage's B blocks are decoded once, into int8 MFMA operands in LDS, instead of by each of the
     // WM waves that read a block (the codebook decode is ~8x the VALU work of the uniform-int4 one)
     static constexpr int DEC = KIND == ORKH_NF4 ? NIB * T::STEPS * 1024 : 0;
-    static constexpr int R = ((163840 - DEC) / SLOT) < 4 ? ((163840 - DEC) / SLOT) : 4; // ring within 160 KiB
+    // ring within 160 KiB: 4 slots, 8 for the small stages of the K-group tiles (more bytes in flight per CU)
+    static constexpr int RMAX = WK > 1 ? 8 : 4;
+    static constexpr int R = ((163840 - DEC) / SLOT) < RMAX ? ((163840 - DEC) / SLOT) : RMAX;
     static constexpr size_t LDS = (size_t)R * SLOT + DEC;
+    static constexpr size_t RED = (size_t)(WK - 1) * WM * WN * MTW * NTW * 1024; // K-group partial tiles
     // A stage whose rows are one 128-byte line each is loaded a line at a time (8 rows x 128 B per instruction)
     // instead of in MFMA fragment order (16 rows x 64 B: every line fetched by two instructions), and read from
     // a swizzled image (a_lds)
     static constexpr bool LINE_OK = KS * T::KPB * T::ESZ == 128;
-    static_assert(MB % WM == 0 && NB % WN == 0 && R >= 2 && (R - 2) * IPW < 64, "tile");
+    static_assert(MB % WM == 0 && NB % WN == 0 && WM * WN * WK == NW && KS % WK == 0 && R >= 2 && (R - 2) * IPW < 64,
+                  "tile");
+    static_assert(RED <= (size_t)R * SLOT, "K-group partials must fit the ring");
     static_assert(!LINE_OK || NIA * 8 == BM, "line-loaded A: one instruction per 8 rows");
 };
 
@@ -529,7 +539,9 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     extern __shared__ v4i sm[];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wv % P::WM, wn = wv / P::WM;
+    static_assert(GR == 0 || P::WK == 1, "grouped runs walk every K-block in one wave");
+    const int wk = P::WK > 1 ? wv / (P::WM * P::WN) : 0, wr = P::WK > 1 ? wv % (P::WM * P::WN) : wv;
+    const int wm = wr % P::WM, wn = wr / P::WM;
     // XCD-aware order: WG b runs on XCD b%8; each XCD gets a contiguous run of tiles, M fastest, so every
     // M-tile that reads a given B column panel shares one L2.
     const int nT = gridDim.x, bid = blockIdx.x;
@@ -682,7 +694,8 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         }
         if constexpr (GR != 1) {
 #pragma unroll
-            for (int kbl = 0; kbl < KS; kbl++) {
+            for (int kk = 0; kk < P::KPW; kk++) {
+                const int kbl = wk * P::KPW + kk; // this wave's K-blocks of the stage
                 v4i op[P::NTW][T::STEPS];
 #pragma unroll
                 for (int jn = 0; jn < P::NTW; jn++) {
@@ -756,6 +769,28 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         }
     }
     wait_vmcnt<0>();
+
+    if constexpr (P::WK > 1) {
+        // K groups 1.. park their partial tiles in the ring (every load has landed: vmcnt 0 on every wave, then
+        // the barrier), group 0 adds them in group order and stores
+        acc_t *red = (acc_t *)sm;
+        __syncthreads();
+        if (wk > 0)
+#pragma unroll
+            for (int i = 0; i < P::MTW; i++)
+#pragma unroll
+                for (int jn = 0; jn < P::NTW; jn++)
+                    red[((((wk - 1) * P::WM * P::WN + wr) * P::MTW + i) * P::NTW + jn) * 64 + lane] = acc[i][jn];
+        __syncthreads();
+        if (wk > 0) return;
+#pragma unroll
+        for (int g = 1; g < P::WK; g++)
+#pragma unroll
+            for (int i = 0; i < P::MTW; i++)
+#pragma unroll
+                for (int jn = 0; jn < P::NTW; jn++)
+                    acc[i][jn] += red[((((g - 1) * P::WM * P::WN + wr) * P::MTW + i) * P::NTW + jn) * 64 + lane];
+    }
 
     // epilogue: one 64-bit base per lane (its first row and column), 32-bit offsets from it
     const int mr0 = m0 + wm * P::MTW * 16 + (lane >> 4) * 4, nc0 = (nb0 + wn * P::NTW) * 16 + (lane & 15);
@@ -1055,10 +1090,11 @@ int launch_tiled_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
 }
 
 // K-blocks per stage of k_tiled2: ~128 bytes of each activation row per stage for small tiles, ~64 for the
-// 256 x 256 tile (whose ring would not fit otherwise).
+// 256 x 256 tile (whose ring would not fit otherwise); at least one per K group of waves.
 template <int KIND, int BM, int BN> constexpr int t2_ks() {
-    if (KIND == ORKH_I4U || KIND == ORKH_NF4) return 1;
-    return BM * BN >= 65536 ? 1 : 2;
+    constexpr int mb = BM / 16 < 4 ? BM / 16 : 4, nb = BN / 16 < 4 ? BN / 16 : 4, wk = 16 / (mb * nb);
+    constexpr int base = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 1 : (BM * BN >= 65536 ? 1 : 2);
+    return base > wk ? base : wk;
 }
 
 template <int KIND, int BM, int BN>
@@ -1094,6 +1130,8 @@ int launch_tiled(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
         if (q->bm == 128 && q->bn == 128) return launch_tiled2_v<KIND, 128, 128>(p, q, s);
         if (q->bm == 64 && q->bn == 192) return launch_tiled2_v<KIND, 64, 192>(p, q, s);
         if (q->bm == 64 && q->bn == 64) return launch_tiled2_v<KIND, 64, 64>(p, q, s);
+        if (q->bm == 32 && q->bn == 64) return launch_tiled2_v<KIND, 32, 64>(p, q, s);
+        if (q->bm == 32 && q->bn == 32) return launch_tiled2_v<KIND, 32, 32>(p, q, s);
         snprintf(g_lerr, sizeof g_lerr, "tiled2 plan: %dx%d unsupported", q->bm, q->bn);
         return -2;
     }
