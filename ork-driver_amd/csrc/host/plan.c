@@ -153,6 +153,12 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
  * so lines everywhere except the 64x64 tile and the nibble kinds' 64-row tiles. ORK_ALINE=0/1 forces it
  * (tests, A/B timing). */
 static int aline_rule(int rkind, const orkh_plan *q) {
+    /* the kernel has the line layout only where a stage row is one 128-byte line: K-blocks per stage as
+     * k_tiled2's t2_ks (1 for int4 kinds, 1 for 256 x 256, else 2; at least the tile's K groups of waves) */
+    const int mb = q->bm / 16 < 4 ? q->bm / 16 : 4, nb = q->bn / 16 < 4 ? q->bn / 16 : 4, wk = 16 / (mb * nb);
+    const int base = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 1 : (q->bm * q->bn >= 65536 ? 1 : 2);
+    const int ks = base > wk ? base : wk;
+    if (ks * a_bytes_per_kb(rkind) != 128) return 0;
     const char *e = getenv("ORK_ALINE");
     if (e) return atoi(e) != 0;
     if (q->bm == 64 && q->bn == 64) return 0;
@@ -193,6 +199,17 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
     }
 
     if (M <= 64 && !f_tiled) {
+        /* NF4 at 49-64 rows: the 32 x 64 K-group tile (its stage's blocks decoded once into LDS) beats streaming,
+         * whose four row tiles re-read A per panel, when its tiles fill one round: 9.7 vs 10.5 us at M=64, but
+         * 9.4 vs 8.4 at M=48 (K=2048 N=6144) */
+        if (rkind == ORKH_NF4 && M > 48 && !f_stream && ks_force <= 0 && 2L * cdiv(NB, 4) <= cu) {
+            q->algo = ORKH_ALGO_TILED2;
+            q->bm = 32;
+            q->bn = 64;
+            q->ksplit = 1;
+            q->kbs = KB;
+            return 0;
+        }
         int ks;
         if (M == 1 || f_stream || ks_force > 0 || rkind == ORKH_NF4) {
             ks = ks_force > 0 ? ks_force : stream_rule_ks(rkind, M, KB, NB, cu);
