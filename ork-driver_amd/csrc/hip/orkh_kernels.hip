@@ -460,7 +460,7 @@ template <int VM> __device__ __forceinline__ void wait_vmcnt() {
 template <int KIND, int BM, int BN, int KS> struct T2 {
     using T = KT<KIND>;
     static constexpr int MB = BM / 16, NB = BN / 16, NW = 16;
-    // 16 waves: WM x WN over the tile's 16 x 16 blocks and, on tiles of fewer than 16 blocks (32 x 32, 32 x 64),
+    // 16 waves: WM x WN over the tile's 16 x 16 blocks and, on tiles of fewer than 16 blocks (32- and 16-row tiles),
     // WK groups that split each stage's K-blocks; their partial tiles are summed through LDS after the loop, in
     // group order (deterministic for fp16)
     static constexpr int WM = MB < 4 ? MB : 4, WN = NB < 4 ? NB : 4, WK = NW / (WM * WN);
@@ -1132,6 +1132,8 @@ int launch_tiled(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
         if (q->bm == 64 && q->bn == 64) return launch_tiled2_v<KIND, 64, 64>(p, q, s);
         if (q->bm == 32 && q->bn == 64) return launch_tiled2_v<KIND, 32, 64>(p, q, s);
         if (q->bm == 32 && q->bn == 32) return launch_tiled2_v<KIND, 32, 32>(p, q, s);
+        if (q->bm == 16 && q->bn == 64) return launch_tiled2_v<KIND, 16, 64>(p, q, s);
+        if (q->bm == 16 && q->bn == 32) return launch_tiled2_v<KIND, 16, 32>(p, q, s);
         snprintf(g_lerr, sizeof g_lerr, "tiled2 plan: %dx%d unsupported", q->bm, q->bn);
         return -2;
     }

@@ -105,7 +105,7 @@ static double stream_us(int rkind, int M, int N, int KB, int cu, int ks) {
 static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force, int cfg_from, orkh_plan *q) {
     /* 32-row tiles split each stage's K-blocks over groups of waves; the model prices them unchanged (measured:
      * fp16 M=128 K=N=2048 32x32 9.0 us vs 9.04 modelled, W4A8 M=64 K=2048 N=6144 32x64 7.27 vs 7.28) */
-    static const int cfg2[][2] = {{256, 256}, {128, 128}, {64, 192}, {64, 64}, {32, 64}, {32, 32}};
+    static const int cfg2[][2] = {{256, 256}, {128, 128}, {64, 192}, {64, 64}, {32, 64}, {32, 32}, {16, 64}, {16, 32}};
     const int NB = N / 16;
     const int abpk = a_bytes_per_kb(rkind), kpb = kpb_of(rkind);
     double best = -1;
@@ -114,7 +114,7 @@ static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force,
         /* NF4's decoded (int8) B doubles the LDS reads of the 3-panel wave tile: 22.3 us at M=512 vs 19.8 on
          * 128 x 128, which the model does not see; on 32-row tiles its per-block decode is shared by half the
          * rows the model assumes (not timed: not offered) */
-        if (rkind == ORKH_NF4 && (bn == 192 || bm == 32)) continue;
+        if (rkind == ORKH_NF4 && (bn == 192 || bm <= 32)) continue;
         const long tiles = (long)cdiv(M, bm) * cdiv(NB, bn / 16);
         for (int ks = ks_force > 0 ? ks_force : 1; ks <= (ks_force > 0 ? ks_force : 8); ks *= (ks_force > 0 ? 8 : 2)) {
             const int kbs = cdiv(KB, ks);
@@ -122,7 +122,7 @@ static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force,
             const long wgs = tiles * ks;
             /* the model underprices several rounds of the K-group tiles (W4A8 M=256 K=2048 N=6144 32x64: 18.2 us
              * measured, 14.3 modelled; int8 M=128 N=6144 32x32: 16.4 vs 12.2), so they are offered for one round */
-            if (bm == 32 && wgs > cu) continue;
+            if (bm <= 32 && wgs > cu) continue;
             const double per = (double)((wgs + cu - 1) / cu);
             const double busy = (double)(wgs < cu ? wgs : cu) / cu;
             const double kib = ((double)bm * abpk * kbs + (double)bn / 16 * 1024 * kbs + (double)bm * bn * 4) / 1024;
