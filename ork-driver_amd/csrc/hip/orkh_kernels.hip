@@ -457,13 +457,13 @@ template <int VM> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int KIND, int BM, int BN, int KS> struct T2 {
+template <int KIND, int BM, int BN, int KS, bool XGW = false> struct T2 {
     using T = KT<KIND>;
     static constexpr int MB = BM / 16, NB = BN / 16, NW = 16;
     // 16 waves: WM x WN over the tile's 16 x 16 blocks and, on tiles of fewer than 16 blocks (32- and 16-row tiles),
     // WK groups that split each stage's K-blocks; their partial tiles are summed through LDS after the loop, in
     // group order (deterministic for fp16)
-    static constexpr int WM = MB < 4 ? MB : 4, WN = NB < 4 ? NB : 4, WK = NW / (WM * WN);
+    static constexpr int WM = XGW ? 2 : (MB < 4 ? MB : 4), WN = NB < 4 ? NB : 4, WK = NW / (WM * WN);
     static constexpr int MTW = MB / WM, NTW = NB / WN, KPW = KS / WK; // blocks and K-blocks per wave
     static constexpr int NIA = MB * KS * T::STEPS, NIB = NB * KS, NI = NIA + NIB;  // loads per stage
     static constexpr int IPW = (NI + NW - 1) / NW;                               // per wave
@@ -486,6 +486,14 @@ template <int KIND, int BM, int BN, int KS> struct T2 {
     static_assert(RED <= (size_t)R * SLOT, "K-group partials must fit the ring");
     static_assert(!LINE_OK || NIA * 8 == BM, "line-loaded A: one instruction per 8 rows");
 };
+
+// Wave grid 2 x 4 with 2 K groups instead of 4 x 4 (each B block decoded by two waves instead of four), for the
+// uniform-int4 64 x 192 tile. Measured against 4 x 4 (us): W4A8 K=2048 N=6144 M=512 14.7 -> 13.4, M=256 13.3 ->
+// 12.5; W4A4 M=512 K=N=4096 22.0 -> 19.9. Not kept elsewhere: int8 M=512 64 x 192 13.9 -> 14.7, fp16 M=1024
+// 20.5 -> 21.1, uniform int4 128 x 128 21.9 -> 22.4 (W4A4 M=256), 64 x 64 unchanged.
+template <int KIND, int BM, int BN, int GR> constexpr bool t2_xg() {
+    return GR == 0 && KIND == ORKH_I4U && BM == 64 && BN == 192;
+}
 
 // Index (in 16-byte units) within a stage's A image of lane `lane`'s operand of fragment (mb, kbl, st).
 // Fragment order: fragment f = (mb, kbl, st) is 1 KiB at f, lane-major, as mma() takes it.
@@ -531,7 +539,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                                             const T2Group &gp) {
 #pragma clang fp contract(off)
     using T = KT<KIND>;
-    using P = T2<KIND, BM, BN, KS>;
+    using P = T2<KIND, BM, BN, KS, t2_xg<KIND, BM, BN, GR>()>;
     constexpr int R = P::R;
     constexpr bool LINE = AL && P::LINE_OK; // A stage as whole row lines (a_lds), else in fragment order
     typedef typename T::acc_t acc_t;
@@ -1091,16 +1099,17 @@ int launch_tiled_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
 
 // K-blocks per stage of k_tiled2: ~128 bytes of each activation row per stage for small tiles, ~64 for the
 // 256 x 256 tile (whose ring would not fit otherwise); at least one per K group of waves.
-template <int KIND, int BM, int BN> constexpr int t2_ks() {
-    constexpr int mb = BM / 16 < 4 ? BM / 16 : 4, nb = BN / 16 < 4 ? BN / 16 : 4, wk = 16 / (mb * nb);
+template <int KIND, int BM, int BN, bool XGW = false> constexpr int t2_ks() {
+    constexpr int mb = XGW ? 2 : (BM / 16 < 4 ? BM / 16 : 4), nb = BN / 16 < 4 ? BN / 16 : 4, wk = 16 / (mb * nb);
     constexpr int base = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 1 : (BM * BN >= 65536 ? 1 : 2);
     return base > wk ? base : wk;
 }
 
 template <int KIND, int BM, int BN>
 int launch_tiled2_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
-    constexpr int KS = t2_ks<KIND, BM, BN>();
-    using P = T2<KIND, BM, BN, KS>;
+    constexpr bool XGW = t2_xg<KIND, BM, BN, 0>();
+    constexpr int KS = t2_ks<KIND, BM, BN, XGW>();
+    using P = T2<KIND, BM, BN, KS, XGW>;
     const bool al = q->aline && P::LINE_OK;
     auto kern = al ? k_tiled2<KIND, BM, BN, KS, true> : k_tiled2<KIND, BM, BN, KS, false>;
     static lds_flags attr[2]; // per instantiation: allow more than the default 64 KiB of dynamic LDS
