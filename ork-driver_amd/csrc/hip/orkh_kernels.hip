@@ -68,15 +68,17 @@ template <int KIND> __device__ __forceinline__ int a_koff(int s, int g) {
 
 struct Lut { uint32_t l0, l1, l2, l3; };
 
-// 4 NF4 indices (one per byte, 0..15) -> 4 int8 codebook values.
-__device__ __forceinline__ uint32_t nf4_map4(uint32_t idx, const Lut &L) {
-    const uint32_t lo = __builtin_amdgcn_perm(L.l1, L.l0, idx);               // entries 0..7
-    const uint32_t hi = __builtin_amdgcn_perm(L.l3, L.l2, idx & 0x07070707u); // entries 8..15
-    const uint32_t m8 = idx & 0x08080808u;                                    // bit 3 per byte
-    // 0xff in each byte whose index is >= 8: per byte 0x100 - 1, the top byte's carry wrapping mod 2^32
-    // (not m * 0xff, which compiles to a quarter-rate v_mul_lo_u32)
-    const uint32_t sel = (m8 << 5) - (m8 >> 3);
-    return (hi & sel) | (lo & ~sel);
+// One dword of NF4 codes (8 nibbles) -> the int8 codebook values of its low nibbles (lo) and of its high
+// nibbles (hi), byte for byte. Both 8-entry halves of the codebook are looked up with the code's low 3 bits
+// (v_perm: selector bytes 0-3 pick from its second operand, 4-7 from its first), then a third v_perm takes
+// byte j from the upper half where bit 3 of code j is set: its selector byte is j + 4 * bit3. Six VALU
+// operations per four codes (the select mask built from bit 3 by shift-and-subtract took eight).
+__device__ __forceinline__ void nf4_map8(uint32_t x, const Lut &L, uint32_t &lo, uint32_t &hi) {
+    const uint32_t i0 = x & 0x07070707u, i1 = (x >> 4) & 0x07070707u;
+    const uint32_t s0 = ((x >> 1) & 0x04040404u) | 0x03020100u; // bit 3 of each low nibble -> byte select
+    const uint32_t s1 = ((x >> 5) & 0x04040404u) | 0x03020100u; // bit 7 (bit 3 of the high nibble)
+    lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L.l3, L.l2, i0), __builtin_amdgcn_perm(L.l1, L.l0, i0), s0);
+    hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L.l3, L.l2, i1), __builtin_amdgcn_perm(L.l1, L.l0, i1), s1);
 }
 
 // Raw 16-byte panel chunk -> STEPS MFMA B operands.
@@ -90,11 +92,13 @@ template <int KIND> __device__ __forceinline__ void decode(v4i raw, v4i *op, con
         op[1] = v4i{(int)((x2 << 4) & 0xf0f0f0f0u), (int)(x2 & 0xf0f0f0f0u),
                     (int)((x3 << 4) & 0xf0f0f0f0u), (int)(x3 & 0xf0f0f0f0u)};
     } else {
-        const uint32_t x0 = raw.x, x1 = raw.y, x2 = raw.z, x3 = raw.w;
-        op[0] = v4i{(int)nf4_map4(x0 & 0x0f0f0f0fu, L), (int)nf4_map4((x0 >> 4) & 0x0f0f0f0fu, L),
-                    (int)nf4_map4(x1 & 0x0f0f0f0fu, L), (int)nf4_map4((x1 >> 4) & 0x0f0f0f0fu, L)};
-        op[1] = v4i{(int)nf4_map4(x2 & 0x0f0f0f0fu, L), (int)nf4_map4((x2 >> 4) & 0x0f0f0f0fu, L),
-                    (int)nf4_map4(x3 & 0x0f0f0f0fu, L), (int)nf4_map4((x3 >> 4) & 0x0f0f0f0fu, L)};
+        uint32_t a0, b0, a1, b1, a2, b2, a3, b3;
+        nf4_map8((uint32_t)raw.x, L, a0, b0);
+        nf4_map8((uint32_t)raw.y, L, a1, b1);
+        nf4_map8((uint32_t)raw.z, L, a2, b2);
+        nf4_map8((uint32_t)raw.w, L, a3, b3);
+        op[0] = v4i{(int)a0, (int)b0, (int)a1, (int)b1};
+        op[1] = v4i{(int)a2, (int)b2, (int)a3, (int)b3};
     }
 }
 
