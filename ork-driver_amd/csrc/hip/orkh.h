@@ -99,6 +99,8 @@ typedef struct orkh_plan {
     /* TILED2: 1 = load A stages as whole 128-byte row lines into a swizzled LDS image where the stage's rows
      * are one line each (else, and with 0, in MFMA fragment order) */
     int aline;
+    /* STREAM: np = 2 pairs panels: npg workgroups, the first N/16 - npg owning two adjacent panels each */
+    int np, npg;
     void *ws;             /* split-K partials, >= ksplit*M*N*4 bytes (device) */
 } orkh_plan;
 

@@ -129,15 +129,21 @@ __device__ __forceinline__ v4i bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // ------------------------------------------------------------------------------------------------
 // k_stream: grid (N/16, ksplit), WPG waves. Workgroup (nb, ks) owns panel nb and K-blocks
 // [ks*kbs, ks*kbs+kbs); wave w takes kbw of them. KU blocks are loaded before any is consumed.
-template <int KIND, int MT, int WPG, int KU>
+// NP = 2 (paired panels): grid (G, 1) with N/16 / 2 <= G < N/16; the first N/16 - G workgroups own two
+// adjacent panels each and the rest one, so every CU holds about the same bytes; a wave loads each A chunk
+// once for both of its panels.
+template <int KIND, int MT, int WPG, int KU, int NP = 1>
 __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs, int ksplit, void *ws) {
     using T = KT<KIND>;
     typedef typename T::acc_t acc_t;
     typedef typename T::c_t c_t;
-    __shared__ c_t red[WPG][MT * 256];
+    __shared__ c_t red[WPG][NP][MT * 256];
 
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nb = blockIdx.x, ks = blockIdx.y;
+    const int ks = blockIdx.y, NBtot = p.N / 16;
+    const int two = NP == 2 ? NBtot - (int)gridDim.x : 0;   // workgroups that own two panels
+    const int nb = NP == 2 ? ((int)blockIdx.x < two ? 2 * (int)blockIdx.x : two + (int)blockIdx.x) : (int)blockIdx.x;
+    const int np = NP == 2 && (int)blockIdx.x < two ? 2 : 1;
     const int kb_hi = min(ks * kbs + kbs, p.KB);
     const int kb0 = ks * kbs + w * kbw;
     const int kb1 = min(kb0 + kbw, kb_hi);
@@ -146,10 +152,13 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
     const int lda_b = p.lda * T::ESZ;
     const Lut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
     const v4i *bp = (const v4i *)p.B + (size_t)nb * p.KB * 64 + lane;
+    const size_t pstride = (size_t)p.KB * 64; // the second panel's blocks (paired workgroups only)
 
-    acc_t acc[MT];
+    acc_t acc[NP][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) acc[mt] = acc_t{0, 0, 0, 0};
+    for (int pi = 0; pi < NP; pi++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[pi][mt] = acc_t{0, 0, 0, 0};
 
     // One batch of U blocks: every A chunk (L2-resident, short latency) is requested first, then every
     // B block (HBM), and only then is anything consumed, so the wave has all its loads in flight at once.
@@ -169,21 +178,28 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
                     const bool ok = row < p.M && k < p.K;
                     av[u][s][mt] = *(const v4i *)(A + (size_t)(ok ? row : 0) * lda_b + (size_t)(ok ? k : 0) * T::ESZ);
                 }
-        v4i raw[U];
+        v4i raw[NP][U];
 #pragma unroll
-        for (int u = 0; u < U; u++) raw[u] = __builtin_nontemporal_load(bp + (size_t)(kb + u) * 64);
+        for (int pi = 0; pi < NP; pi++)
+            if (pi == 0 || np == 2) // workgroup-uniform
+#pragma unroll
+                for (int u = 0; u < U; u++) raw[pi][u] = __builtin_nontemporal_load(bp + pi * pstride + (size_t)(kb + u) * 64);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            v4i op[T::STEPS];
-            decode<KIND>(raw[u], op, L);
 #pragma unroll
-            for (int s = 0; s < T::STEPS; s++)
+            for (int pi = 0; pi < NP; pi++) {
+                if (pi == 1 && np == 1) continue;
+                v4i op[T::STEPS];
+                decode<KIND>(raw[pi][u], op, L);
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    const int row = mt * 16 + r16, k = (kb + u) * T::KPB + a_koff<KIND>(s, g);
-                    const v4i a = (row < p.M && k < p.K) ? av[u][s][mt] : v4i{0, 0, 0, 0};
-                    acc[mt] = mma(a, op[s], acc[mt]);
-                }
+                for (int s = 0; s < T::STEPS; s++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        const int row = mt * 16 + r16, k = (kb + u) * T::KPB + a_koff<KIND>(s, g);
+                        const v4i a = (row < p.M && k < p.K) ? av[u][s][mt] : v4i{0, 0, 0, 0};
+                        acc[pi][mt] = mma(a, op[s], acc[pi][mt]);
+                    }
+            }
         }
     };
 
@@ -194,20 +210,23 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
     for (; kb < kb1; kb++) batch(kb, std::integral_constant<int, 1>{});
 
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+    for (int pi = 0; pi < NP; pi++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) red[w][mt * 256 + r * 64 + lane] = acc[mt][r];
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[w][pi][mt * 256 + r * 64 + lane] = acc[pi][mt][r];
     __syncthreads();
 
     c_t *C = (c_t *)p.C;
     c_t *W = (c_t *)ws;
-    for (int e = threadIdx.x; e < MT * 256; e += WPG * 64) {
-        c_t s = red[0][e];
+    for (int e = threadIdx.x; e < np * MT * 256; e += WPG * 64) {
+        const int pi = e / (MT * 256), el = e - pi * (MT * 256);
+        c_t s = red[0][pi][el];
 #pragma unroll
-        for (int ww = 1; ww < WPG; ww++) s += red[ww][e];
-        const int mt = e >> 8, r = (e >> 6) & 3, ln = e & 63;
+        for (int ww = 1; ww < WPG; ww++) s += red[ww][pi][el];
+        const int mt = el >> 8, r = (el >> 6) & 3, ln = el & 63;
         const int m = mt * 16 + (ln >> 4) * 4 + r;
-        const int n = nb * 16 + (ln & 15);
+        const int n = (nb + pi) * 16 + (ln & 15);
         if (m < p.M) {
             if (ksplit == 1) C[(size_t)m * p.ldc + n] = finish<KIND>(s);
             else W[((size_t)ks * p.M + m) * p.N + n] = finish<KIND>(s);
@@ -1041,6 +1060,15 @@ template <int KIND, int MT, int WPG>
 int launch_stream_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int KU = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 4 : 8;
     dim3 grid(p->N / 16, q->ksplit), block(WPG * 64);
+    if (q->np == 2 && MT <= 2) {
+        const int NB = p->N / 16, G = q->npg;
+        if (q->ksplit != 1 || G < (NB + 1) / 2 || G >= NB) {
+            snprintf(g_lerr, sizeof g_lerr, "stream plan: paired panels need ksplit 1 and N/32 <= %d < N/16", G);
+            return -2;
+        }
+        hipLaunchKernelGGL((k_stream<KIND, MT, WPG, KU, 2>), dim3(G, 1), block, 0, s, *p, q->kbw, q->kbs, 1, q->ws);
+        return 0;
+    }
     hipLaunchKernelGGL((k_stream<KIND, MT, WPG, KU>), grid, block, 0, s, *p, q->kbw, q->kbs, q->ksplit, q->ws);
     return 0;
 }
@@ -1358,7 +1386,7 @@ extern "C" const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *q) {
     if (q->algo == ORKH_ALGO_GEMV)
         snprintf(b, sizeof b, "gemv_%s_w%d_kbw%d_ks%d", k, q->wpg, q->kbw, q->ksplit);
     else if (q->algo == ORKH_ALGO_STREAM)
-        snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d", k, q->mt, q->wpg, q->kbw, q->ksplit);
+        snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d%s", k, q->mt, q->wpg, q->kbw, q->ksplit, q->np == 2 ? "_p2" : "");
     else if (q->ksplit > 1)
         snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
                  q->ksplit, q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");

@@ -32,6 +32,19 @@ static int kpb_of(int rkind) { return rkind == ORKH_I8 ? 64 : rkind == ORKH_F16 
  * wave for the int8/fp16 GEMV (M = 1); more waves with shorter runs where each block costs more issue
  * (more rows, int4 decode). Measured on the K=2048, N=6144 panels; the run lengths on either side were
  * within 2-4%. */
+/* Paired panels for the streaming kernel: with more panels than CUs (but fewer than two per CU), one round of
+ * cu workgroups, the first NB - cu owning two adjacent panels, balances the bytes per CU, and each wave loads
+ * an A chunk once for both panels. Measured (K=2048 N=6144, us, single -> paired): int8 M=16 4.81 -> 4.43,
+ * M=32 7.39 -> 5.60; fp16 M=16 8.17 -> 6.71; W4A8 M=16 4.25 -> 3.96, M=32 6.65 -> 4.85; M <= 8 no gain (M=2
+ * 4.25 -> 4.43). The kernel holds up to two row tiles per panel. ORK_STREAM_NP=1 / 2 turns it off / on
+ * wherever it applies (tests). */
+static int stream_paired(int M, int mt, int NB, int cu, int ks) {
+    if (ks != 1 || mt > 2 || NB <= cu || NB >= 2 * cu || M < 2) return 0;
+    const char *e = getenv("ORK_STREAM_NP");
+    if (e) return atoi(e) == 2;
+    return M > 8;
+}
+
 static void stream_geom(int rkind, int M, int KB, int NB, int cu, int ks, orkh_plan *q) {
     const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
     const int need = cdiv(KB, kbw_target); /* waves per panel at the target run length */
@@ -49,6 +62,8 @@ static void stream_geom(int rkind, int M, int KB, int NB, int cu, int ks, orkh_p
     q->kbs = kbs;
     q->kbw = cdiv(kbs, wpg);
     q->ksplit = cdiv(KB, kbs);
+    q->np = stream_paired(M, q->mt, NB, cu, q->ksplit) ? 2 : 1;
+    q->npg = q->np == 2 ? cu : NB;
 }
 
 /* The GEMV's split rule: split only when the panels leave the machine underfilled (< 4 waves per CU) AND
@@ -90,10 +105,11 @@ static double mac_rate(int rkind, int tiled) {
 static double stream_us(int rkind, int M, int N, int KB, int cu, int ks) {
     orkh_plan g;
     stream_geom(rkind, M, KB, N / 16, cu, ks, &g);
-    const long wgs = (long)(N / 16) * g.ksplit;
+    const int pp = g.np == 2 ? 2 : 1; /* panels of the busiest workgroup */
+    const long wgs = g.np == 2 ? g.npg : (long)(N / 16) * g.ksplit;
     const double per = (double)((wgs + cu - 1) / cu);
-    const double kib = ((double)M * a_bytes_per_kb(rkind) * g.kbs + 1024.0 * g.kbs + 64.0 * M) / 1024;
-    const double mmac = (double)g.mt * 16 * 16 * g.kbs * kpb_of(rkind) / 1e6;
+    const double kib = ((double)M * a_bytes_per_kb(rkind) * g.kbs + pp * (1024.0 * g.kbs + 64.0 * M)) / 1024;
+    const double mmac = (double)pp * g.mt * 16 * 16 * g.kbs * kpb_of(rkind) / 1e6;
     double t = 1.74 + per * (0.103 + 0.017 * kib + mac_rate(rkind, 0) * mmac);
     if (g.ksplit > 1) t += 2.81 + 0.327 * g.ksplit * (double)M * N * 4 / 1e6;
     return t;

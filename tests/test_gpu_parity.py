@@ -573,6 +573,53 @@ def test_lds_ring_small_m(npu, tile, M):
     ork.free(w)
 
 
+@pytest.mark.parametrize("np_", [1, 2])
+@pytest.mark.parametrize("kind", ["i8", "i4a8", "nf4", "f16", "w4a4"])
+def test_stream_paired_panels(npu, kind, np_):
+    """The streaming kernel with paired panels (one round of as many workgroups as CUs, the first N/16 - CUs
+    owning two adjacent panels and sharing each A chunk between them) and without (ORK_STREAM_NP): exact for
+    the integer kinds, within the fp16 bar for fp16. N/16 = 260 and 400 panels (both pairings uneven), M from 2
+    to 32 (one and two row tiles), K tails."""
+    _say("stream paired", kind, np_)
+    rng = np.random.default_rng(91 + np_)
+    for (K, N, M) in [(1056, 4160, 2), (2080, 4160, 17), (512, 6400, 32), (2048, 6400, 9)]:
+        if kind == "w4a4":
+            B = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
+            A = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+            w = npu.pack_i4(B)
+            ref = O.gemm_i32(A, B)
+            run = npu.run_i4
+        elif kind == "f16":
+            B = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+            A = rng.standard_normal((M, K)).astype(np.float16)
+            w = npu.pack_f16(B)
+            ref = O.gemm_f16_f64acc(A, B)
+            run = npu.run_f16
+        elif kind == "i8":
+            B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+            A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            w = npu.pack_i8(B)
+            ref = O.gemm_i32(A, B)
+            run = npu.run_i8
+        else:
+            W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+            with _env(**({"ORK_NF4": 1} if kind == "nf4" else {})):
+                w, _ = npu.pack_i4a8(W)
+            _, _, codes = O.pack_i4a8(W, nf4=kind == "nf4")
+            A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            ref = O.gemm_i32(A, codes)
+            run = npu.run_i8
+        with _env(ORK_PLAN="stream", ORK_STREAM_NP=np_):
+            rc, C = run(w, A)
+            name = npu.plan_name(w, M)
+        assert rc == 0 and name.startswith("stream_") and name.endswith("_p2") == (np_ == 2), name
+        if kind == "f16":
+            assert O.fp16_err(C, ref) <= FP16_TOL, name
+        else:
+            assert np.array_equal(C, ref), (name, K, N, M)
+        ork.free(w)
+
+
 @pytest.mark.parametrize("kind,K,N,M", [("i8", 2048, 6144, 48), ("i8", 6144, 2048, 64), ("i4a8", 2048, 6144, 64),
                                         ("f16", 2048, 6144, 32), ("i8", 2048, 22016, 24)])
 def test_planner_mid_m_default(npu, kind, K, N, M):
