@@ -6,7 +6,10 @@
  * kind shares a single grouped kernel launch (up to 16 tasks per launch) and the other tasks launch
  * back to back on the context's stream, so a decode step pays one launch, not S.
  * Returns 0 on success; -2 on bad arguments (NULL context/tasks/weight, S outside 1..1024, M < 1,
- * dtype mismatch, a bad cstride); -1 on A/C overlap, an offline context or a device failure.
+ * dtype mismatch, a bad cstride); -1 on A/C overlap or a device failure. On an offline context the int8
+ * chain and the int4 chain / stream run every task exactly on the CPU from its host codes (C rows packed at
+ * stride N, as the reference's CPU chain), -1 if a weight is not an offline one; the int8 and fp16 streams
+ * have no offline path (-1), as in the reference.
  * A and C may be host memory, ork_dma_alloc buffers or ork_dev_alloc buffers, per task. */
 #ifndef ORK_CHAIN_H
 #define ORK_CHAIN_H

@@ -12,10 +12,11 @@ uint32_t     ork_pack_format_version(void);
  * one HIP stream, staging buffers. NULL if no HIP device is present. ORK_USE_ORKD is ignored (there
  * is no daemon: single-process ownership). */
 ork_npu     *ork_npu_init(void);
-/* reference include/ork/context.h:73. No device: only the CPU-side surfaces work
- * (ork_i4a8_pack_cpu_blob(_qerr), pack/load keep host codes readable via ork_w_codes). Every run on an
- * offline context fails with -1 -- this build has no CPU compute fallback. soc_id: "gfx950", "mi355x"
- * (or the reference's "rk3588"/"rk3576", accepted for blob tooling). NULL on an unknown id. */
+/* reference include/ork/context.h:73. No device: packs and loads keep the int8 codes [K][N] on the host
+ * (ork_w_codes), and runs of those weights compute the exact result on the CPU, as the reference's offline
+ * branches do (int8 / int4 runs, grouped runs, the int8 chain, the int4 chain and stream); fp16 runs and
+ * the int8 / fp16 streams fail with -1 there. soc_id: "gfx950", "mi355x" (or the reference's
+ * "rk3588"/"rk3576", accepted for blob tooling). NULL on an unknown id. */
 ork_npu     *ork_npu_init_offline(const char *soc_id);
 /* reference include/ork/context.h:83. Frees every device buffer the context still owns, including the
  * device memory of weights released with ork_w_free. */
@@ -33,5 +34,8 @@ int          ork_npu_validated(const ork_npu *ctx);
 void         ork_npu_set_core_budget(ork_npu *ctx, int n);
 /* reference include/ork/context.h:148. Count of unexpected HIP failures in this process. */
 long         ork_io_failures(void);
+/* reference include/ork/context.h:149. Failures a recovery path provokes on purpose (the reference's
+ * permitted ioctl failures). This build provokes none: always 0. */
+long         ork_io_expected_failures(void);
 
 #endif

@@ -21,14 +21,20 @@
  *                            bound, the reference's 3% RMS gate (test_matmul.c:280-306)
  *   oracle_i4_quant_chan     the reference's own compiled orki_i4_quant_chan (oracle/_ref), RN and SR
  *   oracle_nf4_lut, oracle_nf4_quant_chan (RN)
- *                            the int8 codebook, nearest level by brute force, the NF4 < uniform gate
+ *                            the int8 codebook, nearest level by brute force, the exact float32 ties
+ *                            t == 0.5f -> upper level (quant.c:84), the NF4 < uniform gate
  *                            (test_matmul.c:402-427)
- *   oracle_nf4_quant_chan (SR)  bracket and P(hi) = t; PARITY UNPINNED for the exact NF4 draw coupling
- *                            across channels (src/npu.c, which holds the NF4 levels, does not compile
- *                            on x86, so no compiled reference NF4 exists here)
+ *   oracle_nf4_quant_chan (SR)  bracket, P(hi) = t, the xorshift32 stream (the same generator the
+ *                            compiled reference's uniform SR draws, oracle/_ref) and which elements draw;
+ *                            PARITY UNPINNED against a compiled reference for the NF4 draw coupling across
+ *                            channels (src/npu.c, which holds the NF4 levels, does not compile on x86, so
+ *                            no compiled reference NF4 exists here: that order is the source read as text)
  *   oracle_wq_err_chan, oracle_wq_best_absmax
- *                            grid membership and float64 argmin, NULL path = absmax/7, the importance
- *                            gate (test_matmul.c:430-500); PARITY UNPINNED for float32 near-ties
+ *                            grid membership and float64 argmin, every candidate's error equal to an
+ *                            independent float32 sequential sum bit for bit, exact ties keep the first
+ *                            candidate, NULL path = absmax/7, the importance gate (test_matmul.c:430-500);
+ *                            PARITY UNPINNED against a reference build that contracts `e += im*d*d` into a
+ *                            fused multiply-add (GCC's default on aarch64): its float32 near-ties may differ
  *   oracle_i4a8_blob, oracle_o4n1_decode
  *                            header bytes, offsets, size (test_matmul.c:528), round trip, rejections,
  *                            qerr recomputed in float64

@@ -48,14 +48,17 @@ $(OUT)/omp/ref_driver.o: $(HERE)ref_driver.c
 	mkdir -p $(OUT)/omp
 	$(CLANG) $(CFLAGS) -fopenmp -c $< -o $@
 
-# The reference's own example/test program examples/quant.c, compiled UNMODIFIED from the reference tree
-# against this repository's drop-in header (include/ork_npu.h) and linked to libork_npu.so: a C consumer
-# of the reference API running on the MI355X engine, checked by its own embedded FNV-64 goldens.
+# The reference's own example / test programs, compiled UNMODIFIED from the reference tree against this
+# repository's drop-in headers (include/ork_npu.h) and linked to libork_npu.so: C consumers of the reference API
+# running on the MI355X engine, each checked by its own embedded goldens and assertions (tests/test_gpu_dropin.py
+# runs the device ones on the GPU, tests/test_host.py the offline one here).
 ROOT    := $(abspath $(HERE)..)
-$(OUT)/quant_on_mi355x: $(REF)/examples/quant.c $(ROOT)/ork-driver_amd/libork_npu.so $(wildcard $(ROOT)/include/*.h $(ROOT)/include/ork/*.h)
+EXAMPLES := quant test_matmul i4 test_sn3 test_grouped_i8 test_i4_dump_cpu test_pack_gate test_offline_load
+DROPINS := $(addprefix $(OUT)/,$(addsuffix _on_mi355x,$(EXAMPLES)))
+$(OUT)/%_on_mi355x: $(REF)/examples/%.c $(ROOT)/ork-driver_amd/libork_npu.so $(wildcard $(ROOT)/include/*.h $(ROOT)/include/ork/*.h)
 	mkdir -p $(OUT)
 	$(CLANG) -O2 -std=gnu11 -w -I$(ROOT)/include $< -o $@ -L$(ROOT)/ork-driver_amd -lork_npu \
 	    -Wl,-rpath,'$$ORIGIN/../../ork-driver_amd' -lm
 
-dropin: $(OUT)/quant_on_mi355x
+dropin: $(DROPINS)
 .PHONY: dropin

@@ -1060,14 +1060,20 @@ template <int KIND, int MT, int WPG>
 int launch_stream_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int KU = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 4 : 8;
     dim3 grid(p->N / 16, q->ksplit), block(WPG * 64);
-    if (q->np == 2 && MT <= 2) {
-        const int NB = p->N / 16, G = q->npg;
-        if (q->ksplit != 1 || G < (NB + 1) / 2 || G >= NB) {
-            snprintf(g_lerr, sizeof g_lerr, "stream plan: paired panels need ksplit 1 and N/32 <= %d < N/16", G);
+    if (q->np == 2) {
+        // paired panels are built for one or two row tiles only (acc[2][MT] and both panels' raw blocks in registers)
+        if constexpr (MT <= 2) {
+            const int NB = p->N / 16, G = q->npg;
+            if (q->ksplit != 1 || G < (NB + 1) / 2 || G >= NB) {
+                snprintf(g_lerr, sizeof g_lerr, "stream plan: paired panels need ksplit 1 and N/32 <= %d < N/16", G);
+                return -2;
+            }
+            hipLaunchKernelGGL((k_stream<KIND, MT, WPG, KU, 2>), dim3(G, 1), block, 0, s, *p, q->kbw, q->kbs, 1, q->ws);
+            return 0;
+        } else {
+            snprintf(g_lerr, sizeof g_lerr, "stream plan: paired panels need mt <= 2 (got %d)", MT);
             return -2;
         }
-        hipLaunchKernelGGL((k_stream<KIND, MT, WPG, KU, 2>), dim3(G, 1), block, 0, s, *p, q->kbw, q->kbs, 1, q->ws);
-        return 0;
     }
     hipLaunchKernelGGL((k_stream<KIND, MT, WPG, KU>), grid, block, 0, s, *p, q->kbw, q->kbs, q->ksplit, q->ws);
     return 0;

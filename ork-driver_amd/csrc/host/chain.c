@@ -8,7 +8,8 @@
  * What changes: no PC-chained NPU programs, cores or doorbells. Every M = 1 task of one resident kind
  * goes into a grouped GEMV launch (ORKH_GROUP_MAX tasks each), the remaining tasks launch back to back
  * on the context's stream with their normal plans, and host operands move in one pinned staging pass. An
- * offline context returns -1 (the reference falls back to its CPU GEMM; this build has no CPU path). */
+ * offline context runs each task's host codes on the CPU (cpu_chain below), as the reference's int8 chain
+ * and int4 chain / stream do; its int8 stream and fp16 stream have no offline branch and return -1 here too. */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -42,8 +43,8 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
             orki_err("%s: task %d: cstride %d < N %d", who, i, t[i].ldc, w->N);
             return -2;
         }
-        if ((w->rkind == ORKH_I4U || w->rkind == ORKH_NF4) && w->K > 131072) {
-            orki_err("%s: task %d: K=%d exceeds the int4 path's exact-accumulation bound (131072)", who, i, w->K);
+        if ((w->rkind == ORKH_I4U || w->rkind == ORKH_NF4) && w->K > ORKI_I4_K_MAX) {
+            orki_err("%s: task %d: K=%d exceeds the int4 path's exact-accumulation bound (K <= 131040)", who, i, w->K);
             return -2;
         }
         t[i].abytes = (size_t)t[i].M * w->K * esz_a;
@@ -181,6 +182,21 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
 
 static ctask *tasks_new(int S) { return calloc((size_t)S, sizeof(ctask)); }
 
+/* OFFLINE chain (src/npu/core/buf.c:483-487, :560-564): each task exactly on the CPU, in task order, from the
+ * weight's host codes; -1 if a task's weight is not an offline one. As the reference's CPU chain, C is written
+ * with row stride N (an int8 task's cstride applies on the device only). */
+static int cpu_chain(int S, const void *tasks, size_t tsz) {
+    /* ork_mm_task_i8 begins with the four fields of ork_mm_task_i4 (w, M, A, C), in the same order */
+    if (S < 1) return 0; /* the reference's task loop runs nothing */
+    if (!tasks) return -2;
+    for (int i = 0; i < S; i++) {
+        const ork_mm_task_i4 *t = (const ork_mm_task_i4 *)((const char *)tasks + (size_t)i * tsz);
+        if (!t->w || !t->w->codes) return -1;
+        if (t->M > 0) ork_i8_mm_run_cpu(t->M, t->w->K, t->w->N, t->A, t->w->codes, t->C);
+    }
+    return 0;
+}
+
 static int i8_chain(const char *who, ork_npu *c, int S, const ork_mm_task_i8 *tasks) {
     if (!c) return -1;
     if (S < 1 || S > 1024 || !tasks) return -2;
@@ -216,6 +232,7 @@ static int i4_chain(const char *who, ork_npu *c, int S, const ork_mm_task_i4 *ta
 }
 
 int ork_i8_mm_run_chain(ork_npu *c, int S, const ork_mm_task_i8 *tasks) {
+    if (c && c->offline) return cpu_chain(S, tasks, sizeof *tasks);
     return i8_chain("ork_i8_mm_run_chain", c, S, tasks);
 }
 
@@ -225,10 +242,12 @@ int ork_i8_mm_run_stream(ork_npu *c, int S, const ork_mm_task_i8 *tasks) {
 }
 
 int ork_i4_mm_run_chain(ork_npu *c, int S, const ork_mm_task_i4 *tasks) {
+    if (c && c->offline) return cpu_chain(S, tasks, sizeof *tasks);
     return i4_chain("ork_i4_mm_run_chain", c, S, tasks);
 }
 
 int ork_i4_mm_run_stream(ork_npu *c, int S, const ork_mm_task_i4 *tasks) {
+    if (c && c->offline) return cpu_chain(S, tasks, sizeof *tasks);
     if (!c) return -2;
     return i4_chain("ork_i4_mm_run_stream", c, S, tasks);
 }

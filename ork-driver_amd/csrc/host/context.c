@@ -32,6 +32,9 @@ void orki_hip_fail(const char *what) {
 }
 
 long ork_io_failures(void) { return atomic_load(&g_io_fail); }
+/* reference include/ork/context.h:149, src/npu/core/submit.c:74: failures a recovery path provokes on purpose.
+ * No path of this build provokes one, so the count stays 0. */
+long ork_io_expected_failures(void) { return 0; }
 
 const char *ork_npu_version(void) { return ORK_NPU_VERSION "+mi355x"; }
 uint32_t ork_pack_format_version(void) { return ORK_PACK_FORMAT_VERSION; }
@@ -71,6 +74,8 @@ static ork_npu *ctx_new(void) {
     ork_npu *c = calloc(1, sizeof *c);
     if (!c) return NULL;
     pthread_mutex_init(&c->mu, NULL);
+    const char *dbg = getenv("ORK_PLAN_DEBUG");
+    c->plan_knobs = dbg && *dbg && strcmp(dbg, "0") != 0;
     return c;
 }
 

@@ -15,6 +15,11 @@
 /* Public dtypes (include/ork/run.h ork_dtype; reference DT_* values, src/npu/internal.h). */
 enum { DT_F16 = 0, DT_I8 = 1, DT_I4 = 2 };
 
+/* Largest K an int4-resident weight (uniform or NF4 panels) runs at. The uniform kernels widen a nibble v to
+ * 16*v in an int8 lane, so the int32 sum is 16x the true one: |16*v*a| <= 16384 per product, and at
+ * K = 131072 (the next multiple of 32) the worst case reaches 2^31 and wraps before the >>4. */
+#define ORKI_I4_K_MAX 131040
+
 #define ORK_DMA_MAX 64 /* zero-copy table size, as the reference (src/npu/internal.h:94-96) */
 
 struct ork_buf { void *p; size_t n; };
@@ -26,6 +31,10 @@ struct ork_npu {
     orkh_dev dev;
     void *stream;
     int async;
+    /* ORK_PLAN_DEBUG set when the context was made: the planner then honours its test overrides (ORK_PLAN,
+     * ORK_TILE, ORK_KSPLIT, ORK_ALINE, ORK_STREAM_NP, ORK_WPG), read at each plan so a test can switch them
+     * between runs. Without it the planner reads no environment at all. */
+    int plan_knobs;
     /* device staging for host-side A / C, split-K / grouped partials and grouped-run scales, grown on demand */
     struct ork_buf sA, sC, sW, sS;
     /* pinned, device-mapped host staging for host-side A (filled by the CPU, uploaded by one DMA copy) and
@@ -111,6 +120,10 @@ void  orki_host_c_done(ork_npu *c, void *C, size_t n, int mode);
 void  orki_orphan(ork_npu *c, void *dptr);
 ork_w *orki_w_new(ork_npu *c, int K, int N, int dtype, int rkind);
 int   orki_w_upload(ork_w *w, const void *panels);
+
+/* ---- host GEMMs of an offline context (cpu_gemm.c): exact int32, and the grouped float accumulate ---- */
+int orki_cpu_gemm_grouped(int M, int K, int N, int G, const int8_t *A, const int8_t *B_kn, const float *aS,
+                          const float *bS, float *C);
 
 /* ---- overlap guard (run.c), reference src/npu/core/submit.c:532-539 ---- */
 int orki_check_overlap(const char *name, uintptr_t a0, uintptr_t a1, uintptr_t c0, uintptr_t c1);

@@ -15,7 +15,9 @@
  *            modelled time.
  * Both time models charge a workgroup for a fixed set-up, the operand bytes that must reach its CU and
  * its multiply-accumulates; a K split adds its partials' round trip and the reduce launch.
- * ORK_PLAN=stream|tiled, ORK_TILE=BMxBN and ORK_KSPLIT=n force a kernel, tile or split (tests, A/B). */
+ * ORK_PLAN=stream|tiled, ORK_TILE=BMxBN and ORK_KSPLIT=n force a kernel, tile or split (tests, A/B); they and
+ * the other overrides below are read only on a context made with ORK_PLAN_DEBUG set (knob()), so a stray
+ * variable cannot change the kernels of a production context. */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -23,6 +25,9 @@
 #include "internal.h"
 
 static int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+/* A planner test override: the environment variable on a context made with ORK_PLAN_DEBUG, else nothing. */
+static const char *knob(const ork_npu *c, const char *name) { return (c && c->plan_knobs) ? getenv(name) : NULL; }
 
 /* A bytes per activation row per 1 KiB weight block (K-block of the panel layout) */
 static int a_bytes_per_kb(int rkind) { return rkind == ORKH_F16 ? 64 : (rkind == ORKH_I8 ? 64 : 128); }
@@ -38,21 +43,21 @@ static int kpb_of(int rkind) { return rkind == ORKH_I8 ? 64 : rkind == ORKH_F16 
  * M=32 7.39 -> 5.60; fp16 M=16 8.17 -> 6.71; W4A8 M=16 4.25 -> 3.96, M=32 6.65 -> 4.85; M <= 8 no gain (M=2
  * 4.25 -> 4.43). The kernel holds up to two row tiles per panel. ORK_STREAM_NP=1 / 2 turns it off / on
  * wherever it applies (tests). */
-static int stream_paired(int M, int mt, int NB, int cu, int ks) {
+static int stream_paired(const ork_npu *c, int M, int mt, int NB, int cu, int ks) {
     if (ks != 1 || mt > 2 || NB <= cu || NB >= 2 * cu || M < 2) return 0;
-    const char *e = getenv("ORK_STREAM_NP");
+    const char *e = knob(c, "ORK_STREAM_NP");
     if (e) return atoi(e) == 2;
     return M > 8;
 }
 
-static void stream_geom(int rkind, int M, int KB, int NB, int cu, int ks, orkh_plan *q) {
+static void stream_geom(const ork_npu *c, int rkind, int M, int KB, int NB, int cu, int ks, orkh_plan *q) {
     const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
     const int need = cdiv(KB, kbw_target); /* waves per panel at the target run length */
     int wpg = need <= 4 ? 4 : 8;
     /* an int8 GEMV with fewer panels than CUs runs 8 shorter waves per panel: 2.94 -> 2.84 us at K=N=2048,
      * 2.80 -> 2.67 us at N=1024; with more panels than CUs 4 stay ahead (3.94 vs 4.04 us at N=6144) */
     if (M == 1 && rkind == ORKH_I8 && NB < cu) wpg = 8;
-    const char *fw = getenv("ORK_WPG"); /* testing / A-B: waves per panel of the GEMV (4 or 8) */
+    const char *fw = knob(c, "ORK_WPG"); /* testing / A-B: waves per panel of the GEMV (4 or 8) */
     if (M == 1 && fw && (atoi(fw) == 4 || atoi(fw) == 8)) wpg = atoi(fw);
     if (ks > KB) ks = KB;
     if (ks < 1) ks = 1;
@@ -62,16 +67,16 @@ static void stream_geom(int rkind, int M, int KB, int NB, int cu, int ks, orkh_p
     q->kbs = kbs;
     q->kbw = cdiv(kbs, wpg);
     q->ksplit = cdiv(KB, kbs);
-    q->np = stream_paired(M, q->mt, NB, cu, q->ksplit) ? 2 : 1;
+    q->np = stream_paired(c, M, q->mt, NB, cu, q->ksplit) ? 2 : 1;
     q->npg = q->np == 2 ? cu : NB;
 }
 
 /* The GEMV's split rule: split only when the panels leave the machine underfilled (< 4 waves per CU) AND
  * each wave would otherwise stream more than two runs back to back; the split costs a second launch
  * (the fixed-order reduce), which a one-run wave never repays. */
-static int stream_rule_ks(int rkind, int M, int KB, int NB, int cu) {
+static int stream_rule_ks(const ork_npu *c, int rkind, int M, int KB, int NB, int cu) {
     orkh_plan g;
-    stream_geom(rkind, M, KB, NB, cu, 1, &g);
+    stream_geom(c, rkind, M, KB, NB, cu, 1, &g);
     const int kbw_target = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 2 : (M > 1 ? 4 : 8);
     const int runs = cdiv(cdiv(KB, g.wpg), kbw_target);
     int ks = 1;
@@ -102,9 +107,9 @@ static double mac_rate(int rkind, int tiled) {
     return tiled ? 0.199 : 0.91;
 }
 
-static double stream_us(int rkind, int M, int N, int KB, int cu, int ks) {
+static double stream_us(const ork_npu *c, int rkind, int M, int N, int KB, int cu, int ks) {
     orkh_plan g;
-    stream_geom(rkind, M, KB, N / 16, cu, ks, &g);
+    stream_geom(c, rkind, M, KB, N / 16, cu, ks, &g);
     const int pp = g.np == 2 ? 2 : 1; /* panels of the busiest workgroup */
     const long wgs = g.np == 2 ? g.npg : (long)(N / 16) * g.ksplit;
     const double per = (double)((wgs + cu - 1) / cu);
@@ -168,14 +173,14 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
  *   W4A4 K=N=4096:      M=256 64x64 13.7 -> 14.4, 64x192 21.5 -> 23.0, 128x128 23.0 -> 21.5
  * so lines everywhere except the 64x64 tile and the nibble kinds' 64-row tiles. ORK_ALINE=0/1 forces it
  * (tests, A/B timing). */
-static int aline_rule(int rkind, const orkh_plan *q) {
+static int aline_rule(const ork_npu *c, int rkind, const orkh_plan *q) {
     /* the kernel has the line layout only where a stage row is one 128-byte line: K-blocks per stage as
      * k_tiled2's t2_ks (1 for int4 kinds, 1 for 256 x 256, else 2; at least the tile's K groups of waves) */
     const int mb = q->bm / 16 < 4 ? q->bm / 16 : 4, nb = q->bn / 16 < 4 ? q->bn / 16 : 4, wk = 16 / (mb * nb);
     const int base = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 1 : (q->bm * q->bn >= 65536 ? 1 : 2);
     const int ks = base > wk ? base : wk;
     if (ks * a_bytes_per_kb(rkind) != 128) return 0;
-    const char *e = getenv("ORK_ALINE");
+    const char *e = knob(c, "ORK_ALINE");
     if (e) return atoi(e) != 0;
     if (q->bm == 64 && q->bn == 64) return 0;
     if ((rkind == ORKH_I4U || rkind == ORKH_NF4) && q->bm == 64) return 0;
@@ -184,7 +189,7 @@ static int aline_rule(int rkind, const orkh_plan *q) {
 
 int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes) {
     const int rc = plan_core(c, rkind, M, K, N, KB, q, ws_bytes);
-    if (q->algo == ORKH_ALGO_TILED2) q->aline = aline_rule(rkind, q);
+    if (q->algo == ORKH_ALGO_TILED2) q->aline = aline_rule(c, rkind, q);
     return rc;
 }
 
@@ -194,14 +199,14 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
     *ws_bytes = 0;
     const int cu = (c && c->cores > 0) ? c->cores : 256;
     const int NB = N / 16;
-    const char *force = getenv("ORK_PLAN");
+    const char *force = knob(c, "ORK_PLAN");
     const int f_stream = force && !strcmp(force, "stream"), f_tiled = force && !strcmp(force, "tiled");
-    const char *fks = getenv("ORK_KSPLIT");
+    const char *fks = knob(c, "ORK_KSPLIT");
     int ks_force = fks ? atoi(fks) : 0;
     if (ks_force > KB) ks_force = KB;
     if (ks_force > 0) ks_force = cdiv(KB, cdiv(KB, ks_force)); /* as a split can realise it */
 
-    const char *tf = getenv("ORK_TILE"); /* "BMxBN": that tile of the LDS-ring kernel, at any M */
+    const char *tf = knob(c, "ORK_TILE"); /* "BMxBN": that tile of the LDS-ring kernel, at any M */
     int fbm, fbn;
     if (tf && sscanf(tf, "%dx%d", &fbm, &fbn) == 2) {
         const int ks = ks_force > 0 ? ks_force : 1;
@@ -228,14 +233,14 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
         }
         int ks;
         if (M == 1 || f_stream || ks_force > 0 || rkind == ORKH_NF4) {
-            ks = ks_force > 0 ? ks_force : stream_rule_ks(rkind, M, KB, NB, cu);
+            ks = ks_force > 0 ? ks_force : stream_rule_ks(c, rkind, M, KB, NB, cu);
         } else {
             /* both kernels priced, each at its best split; the streaming kernel wins ties */
             ks = 1;
-            double ts = stream_us(rkind, M, N, KB, cu, 1);
+            double ts = stream_us(c, rkind, M, N, KB, cu, 1);
             for (int k = 2; k <= 8; k *= 2) {
                 if (cdiv(KB, cdiv(KB, k)) != k || cdiv(KB, k) < 4) continue;
-                const double t = stream_us(rkind, M, N, KB, cu, k);
+                const double t = stream_us(c, rkind, M, N, KB, cu, k);
                 if (t < ts - 1e-9) { ts = t; ks = k; }
             }
             orkh_plan t2;
@@ -248,7 +253,7 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
         }
         /* M = 1 takes the VALU-dot GEMV (same grid and fields); ORK_PLAN=stream keeps the MFMA kernel. */
         q->algo = (M == 1 && !f_stream) ? ORKH_ALGO_GEMV : ORKH_ALGO_STREAM;
-        stream_geom(rkind, M, KB, NB, cu, ks, q);
+        stream_geom(c, rkind, M, KB, NB, cu, ks, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }
@@ -310,12 +315,12 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
 void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB, int G, orkh_plan *q) {
     memset(q, 0, sizeof *q);
     const int cu = (c && c->cores > 0) ? c->cores : 256;
-    const char *force = getenv("ORK_PLAN");
+    const char *force = knob(c, "ORK_PLAN");
     int tiled = M >= (G % 128 == 0 ? ORKI_GROUPED_TILED_M : ORKI_GROUPED_TILED_M_PARTIAL);
     if (force && !strcmp(force, "stream")) tiled = 0;
     if (force && !strcmp(force, "tiled")) tiled = 1;
     if (tiled && rkind != ORKH_NF4) {
-        const char *tf = getenv("ORK_TILE");
+        const char *tf = knob(c, "ORK_TILE");
         int fbm, fbn;
         if (tf && sscanf(tf, "%dx%d", &fbm, &fbn) == 2 && fbm == 64 && (fbn == 64 || fbn == 192)) {
             q->algo = ORKH_ALGO_TILED2;

@@ -159,6 +159,7 @@ float orki_wq_best_absmax(const float *fr, int K, float rawabsmax, int nf4, cons
 
 struct i4q {
     int K, nf4;
+    _Atomic int fail;  /* set by a worker that could not allocate its scratch: the whole quant fails */
     const float *f32, *im;
     float *bscale;
     uint8_t *nib;
@@ -190,7 +191,12 @@ static void i4q_range(int lo, int hi, void *a) {
     struct i4q *q = a;
     int8_t *tmp = malloc((size_t)q->K);
     uint8_t *idx = malloc((size_t)q->K);
-    if (!tmp || !idx) { free(tmp); free(idx); return; }
+    if (!tmp || !idx) {
+        free(tmp);
+        free(idx);
+        q->fail = 1; /* its channels stay unquantised: the caller must not use the store */
+        return;
+    }
     for (int n = lo; n < hi; n++) i4q_chan(q, n, 0, NULL, tmp, idx);
     free(tmp);
     free(idx);
@@ -198,11 +204,11 @@ static void i4q_range(int lo, int hi, void *a) {
 
 int orki_i4a8_quant(int K, int N, const float *f32, const float *imatrix, int nf4, int sr,
                     float *bscale, uint8_t *nib, int8_t *codes_nk) {
-    struct i4q q = {K, nf4 ? 1 : 0, f32, imatrix, bscale, nib, codes_nk, {0}};
+    struct i4q q = {K, nf4 ? 1 : 0, 0, f32, imatrix, bscale, nib, codes_nk, {0}};
     orki_nf4_lut(q.lut);
     if (!sr) {
         orki_parallel_for(N, i4q_range, &q);
-        return 0;
+        return q.fail ? -1 : 0;
     }
     /* Stochastic rounding draws one xorshift value per element from a stream that runs across
      * channels in order (src/npu/i4/pack.c:32, :74, :77), so the channels run in sequence. */

@@ -7,7 +7,9 @@
  * reduce when planned) replaces the per-slice NPU submits and the host K-slice accumulate; operands
  * already in HBM (ork_dev_alloc) are used in place; a host A is uploaded from pinned staging by one DMA
  * copy on the context's stream, and a host C up to 1 MiB is written by the kernels straight into pinned,
- * device-mapped memory (larger ones come back by one D2H copy). There is no CPU fallback: an offline context or a device error returns -1. */
+ * device-mapped memory (larger ones come back by one D2H copy). An offline context (no device) runs an offline
+ * weight's host codes on the CPU, exactly, as the reference's offline branches do (src/npu/i8/run.c:140,
+ * src/npu/i4/run.c:236, :368-369); a device context never falls back: a device error returns -1. */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -28,6 +30,11 @@ static const char *dt_name(int dt) { return dt == DT_F16 ? "fp16" : dt == DT_I8 
 /* esz_a: bytes per A element; C is always 4 bytes per element. */
 static int run_common(const char *who, ork_npu *c, ork_w *w, int want_dt, int M, const void *A, void *C, int esz_a) {
     if (!c || !w || !A || !C) { orki_err("%s: NULL argument", who); return -1; }
+    if (c->offline && w->codes && want_dt != DT_F16) {
+        /* OFFLINE: the exact CPU MAC on the weight's codes [K][N], whatever its pack dtype, as the reference */
+        if (M > 0) ork_i8_mm_run_cpu(M, w->K, w->N, (const int8_t *)A, w->codes, (int32_t *)C);
+        return 0;
+    }
     if (orki_need_device(c, who)) return -1;
     if (w->dtype != want_dt || !w->dB) {
         orki_err("%s: weight is %s, run needs %s", who, w->dB ? dt_name(w->dtype) : "offline", dt_name(want_dt));
@@ -35,8 +42,8 @@ static int run_common(const char *who, ork_npu *c, ork_w *w, int want_dt, int M,
     }
     if (M < 1) { orki_err("%s: M=%d", who, M); return -1; }
     const int K = w->K, N = w->N;
-    if ((w->rkind == ORKH_I4U || w->rkind == ORKH_NF4) && K > 131072) {
-        orki_err("%s: K=%d exceeds the int4 path's exact-accumulation bound (131072)", who, K);
+    if ((w->rkind == ORKH_I4U || w->rkind == ORKH_NF4) && K > ORKI_I4_K_MAX) {
+        orki_err("%s: K=%d exceeds the int4 path's exact-accumulation bound (K <= 131040)", who, K);
         return -1;
     }
     const size_t abytes = (size_t)M * K * esz_a, cbytes = (size_t)M * N * 4;
@@ -104,6 +111,11 @@ int ork_f16_mm_run(ork_npu *c, ork_w *w, int M, const ork_f16 *A, float *C) {
 static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M, const int8_t *A, const float *aS,
                        const float *bS, float *C) {
     if (!c || !w || !A || !aS || !bS || !C || M < 1) { orki_err("%s: NULL argument or M < 1", who); return -1; }
+    if (c->offline && w->codes) {
+        /* OFFLINE: the per-group accumulate on the CPU (src/npu/i8/run.c:48-49, src/npu/i4/run.c:368-369) */
+        if (w->gsize < 1 || w->K % w->gsize) { orki_err("%s: weight has no group size", who); return -1; }
+        return orki_cpu_gemm_grouped(M, w->K, w->N, w->gsize, A, w->codes, aS, bS, C);
+    }
     if (orki_need_device(c, who)) return -1;
     if (w->dtype != want_dt || !w->dB || w->rkind == ORKH_F16) {
         orki_err("%s: weight is %s, this run needs %s", who, w->dB ? dt_name(w->dtype) : "offline", dt_name(want_dt));
@@ -118,8 +130,8 @@ static int run_grouped(const char *who, ork_npu *c, ork_w *w, int want_dt, int M
         orki_err("%s: G=%d unsupported on the device: a group must be whole 32-k chunks", who, G);
         return -3;
     }
-    if ((w->rkind == ORKH_I4U || w->rkind == ORKH_NF4) && K > 131072) {
-        orki_err("%s: K=%d exceeds the int4 path's exact-accumulation bound (131072)", who, K);
+    if ((w->rkind == ORKH_I4U || w->rkind == ORKH_NF4) && K > ORKI_I4_K_MAX) {
+        orki_err("%s: K=%d exceeds the int4 path's exact-accumulation bound (K <= 131040)", who, K);
         return -1;
     }
     const int Sk = K / G;

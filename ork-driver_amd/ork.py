@@ -28,6 +28,7 @@ API = {
     "ork_npu_validated": (C.c_int, [_P]),
     "ork_npu_set_core_budget": (None, [_P, C.c_int]),
     "ork_io_failures": (C.c_long, []),
+    "ork_io_expected_failures": (C.c_long, []),
     "ork_dma_alloc": (_P, [_P, C.c_size_t]),
     "ork_dma_free": (None, [_P, _P]),
     "ork_f16_mm_pack": (_P, [_P, C.c_int, C.c_int, _P]),

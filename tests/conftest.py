@@ -4,6 +4,9 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+# The planner honours its test overrides (ORK_PLAN, ORK_TILE, ORK_KSPLIT, ORK_ALINE, ORK_STREAM_NP, ORK_WPG) only on
+# a context made while ORK_PLAN_DEBUG is set; the forced-plan parity tests rely on it.
+os.environ.setdefault("ORK_PLAN_DEBUG", "1")
 for p in (os.path.join(ROOT, "ork-driver_amd"), os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")):
     if p not in sys.path:
         sys.path.insert(0, p)

@@ -1,30 +1,88 @@
-"""Drop-in check: the reference's own C test program runs on this engine.
+"""Drop-in check: the reference's own C test programs run on this engine.
 
-oracle/_ref/quant_on_mi355x is examples/quant.c from the reference, compiled unmodified against
-include/ork_npu.h and linked to libork_npu.so (oracle/ref.mk). It packs with ork_i8_mm_pack, runs
-ork_i8_mm_run at 7 shapes (M=1..512) and compares an FNV-64 of C with its embedded goldens
-(examples/quant.c:72-81); with ORK_TEST_DMA set, A and C live in ork_dma_alloc buffers (:39-44).
-The binary is built where the reference tree exists and travels with the repository.
+oracle/_ref/<name>_on_mi355x is examples/<name>.c from the reference, compiled unmodified against
+include/ork_npu.h and linked to libork_npu.so (oracle/ref.mk). Each program checks itself: embedded FNV-64
+goldens, exact integer references computed in C, byte comparisons of dumps, and its own pass line. The
+binaries are built where the reference tree exists and travel with the repository.
+
+  quant            ork_i8_mm_pack / run at 7 shapes vs its goldens (examples/quant.c:72-81); ORK_TEST_DMA puts A
+                   and C in ork_dma_alloc buffers (:39-44)
+  test_matmul      fp16 goldens, chains / streams, pack_i8_f32, i4a8, NF4, imatrix, O4N1 dump / load, the overlap
+                   guard, int8 goldens (examples/test_matmul.c:590-656)
+  i4               W4A4 pack / run exact, the K=2048 saturation case, grouped W4A4 (examples/i4.c)
+  test_sn3         int8 at N spanning several 8192-wide NPU output slices (examples/test_sn3.c)
+  test_grouped_i8  grouped int8 runs of a W4A4 pack loaded as int8 (examples/test_grouped_i8.c)
+  test_i4_dump_cpu ork_i4_w_dump_cpu byte-identical to pack + ork_w_dump (examples/test_i4_dump_cpu.c)
+  test_pack_gate   OAPK loaders refuse foreign / damaged packs and load honest ones (examples/test_pack_gate.c)
+
+One check of the reference's encodes a limit of its NPU, not of the matmul: test_matmul's check_chain_envelope
+(examples/test_matmul.c:244-262) expects an int8 chain / stream of K=768, M=8 to be REFUSED with -3, because
+the NPU's chained K-reduction schedule needs K % 512 == 0. This engine computes that chain exactly (its part
+(b) and every other chain check verify results), so the two "expected -3" lines are the only failures
+tolerated, and only in that program.
 """
 import os
+import re
 import subprocess
 
 import pytest
 
 pytestmark = pytest.mark.gpu
 
-BIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "_ref", "quant_on_mi355x")
+REF_BIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "_ref")
+
+# program -> (its pass line, failure lines tolerated because they encode an RK3588 NPU limit)
+PROGRAMS = {
+    "test_matmul": ("ALL OK", ("ENVELOPE: run_chain_i8 K=768 M=8 expected -3, got 0",
+                               "ENVELOPE: run_stream_i8 K=768 M=8 expected -3, got 0")),
+    "i4": ("ALL W4A4 API TESTS PASSED", ()),
+    "test_sn3": ("SN3 GATE: PASS", ()),
+    "test_grouped_i8": ("test_grouped_i8: PASS", ()),
+    "test_i4_dump_cpu": ("ALL BYTE-IDENTICAL", ()),
+    "test_pack_gate": ("PACK GATE OK", ()),
+}
 
 
-@pytest.mark.skipif(not os.path.exists(BIN), reason="oracle/_ref/quant_on_mi355x not built (needs the reference tree)")
+def _bin(name):
+    return os.path.join(REF_BIN, name + "_on_mi355x")
+
+
+def _run(name, env=None, timeout=300):
+    print(f"[case] reference examples/{name}.c", flush=True)
+    r = subprocess.run([_bin(name)], capture_output=True, text=True, timeout=timeout, env=env)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    return r
+
+
+@pytest.mark.skipif(not os.path.exists(_bin("quant")), reason="oracle/_ref/quant_on_mi355x not built (needs the reference tree)")
 @pytest.mark.parametrize("dma", [0, 1])
 def test_reference_quant_example_runs_unmodified(dma):
     env = dict(os.environ)
     if dma:
         env["ORK_TEST_DMA"] = "1"
-    print("[case] reference examples/quant.c, ORK_TEST_DMA=%d" % dma, flush=True)
-    r = subprocess.run([BIN], capture_output=True, text=True, timeout=120, env=env)
-    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    r = _run("quant", env)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "ALL OK" in r.stdout
     assert r.stdout.count("golden") == 7  # every case took the golden (bit-exact) branch
+
+
+@pytest.mark.parametrize("name", sorted(PROGRAMS))
+def test_reference_example_runs_unmodified(name):
+    if not os.path.exists(_bin(name)):
+        pytest.skip(f"oracle/_ref/{name}_on_mi355x not built (needs the reference tree)")
+    ok_line, tolerated = PROGRAMS[name]
+    r = _run(name)
+    out = r.stdout
+    words = ("FAIL", "WRONG", "MISMATCH", "failed", "expected ", "mism @", "mism at", "ENVELOPE:", "differs")
+    fail_lines = [ln.strip() for ln in out.splitlines()
+                  if (any(w in ln for w in words) or re.search(r"mism=[1-9]", ln)) and ln.strip() not in tolerated]
+    if tolerated and r.returncode != 0:
+        # the program's only failures are the NPU-limit lines named above (and its closing verdict line)
+        assert all(t in out for t in tolerated), out
+        assert fail_lines == ["FAIL"], fail_lines
+        assert out.strip().splitlines()[-1] == "FAIL"
+    else:
+        assert r.returncode == 0, out + r.stderr
+        assert ok_line in out
+        assert not fail_lines, fail_lines
+    assert "UNEXPECTED" not in out + r.stderr

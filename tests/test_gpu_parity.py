@@ -578,11 +578,16 @@ def test_lds_ring_small_m(npu, tile, M):
 def test_stream_paired_panels(npu, kind, np_):
     """The streaming kernel with paired panels (one round of as many workgroups as CUs, the first N/16 - CUs
     owning two adjacent panels and sharing each A chunk between them) and without (ORK_STREAM_NP): exact for
-    the integer kinds, within the fp16 bar for fp16. N/16 = 260 and 400 panels (both pairings uneven), M from 2
-    to 32 (one and two row tiles), K tails."""
+    the integer kinds, within the fp16 bar for fp16. N is derived from the device's CU count so that
+    cu < N/16 < 2*cu (the range where pairing applies; 260 and 400 panels on 256 CUs, both pairings uneven), M
+    from 2 to 32 (one and two row tiles), K tails."""
     _say("stream paired", kind, np_)
     rng = np.random.default_rng(91 + np_)
-    for (K, N, M) in [(1056, 4160, 2), (2080, 4160, 17), (512, 6400, 32), (2048, 6400, 9)]:
+    cu = ork.lib().ork_npu_cores(npu.h)
+    n1 = (16 * cu // 64 + 1) * 64        # just above cu panels (a multiple of 64 for W4A4)
+    n2 = (25 * cu // 64) * 64            # ~1.56 cu panels
+    assert cu < n1 // 16 < 2 * cu and cu < n2 // 16 < 2 * cu
+    for (K, N, M) in [(1056, n1, 2), (2080, n1, 17), (512, n2, 32), (2048, n2, 9)]:
         if kind == "w4a4":
             B = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
             A = rng.integers(-8, 8, size=(M, K), dtype=np.int8)

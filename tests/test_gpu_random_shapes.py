@@ -37,6 +37,14 @@ def _cases(n=60, seed=0x6F726B52):
         while N > step and (K * N > (1 << 22) or M * K * N > 400_000_000):
             N = max(step, (N // 2) // step * step)
         out.append((i, kind, M, K, N))
+    # the streaming kernel's paired-panel range at default plans: cu < N/16 < 2*cu panels (cu = 256 on MI355X)
+    # and 9 <= M <= 32; N is a multiple of 64 there, so every kind packs
+    for j in range(8):
+        kind = kinds[j % len(kinds)]
+        M = int(rng.integers(9, 33))
+        N = 64 * int(rng.integers(16 * 256 // 64 + 1, 32 * 256 // 64))
+        K = 32 * int(rng.integers(1, 33))
+        out.append((n + len(fixed) + j, kind, M, K, N))
     return out
 
 

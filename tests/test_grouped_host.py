@@ -1,6 +1,9 @@
 """Grouped-scale surfaces on the host (no GPU): pack / set-group gates, the tiled int4 -> int8 load on an
-offline context, and the rule that offline contexts do not run (no CPU fallback)."""
+offline context, and grouped runs on an offline context, which compute the per-group accumulate on the CPU as
+the reference's offline branches do (src/npu/i8/run.c:48-49, src/npu/i4/run.c:368-369)."""
 import numpy as np
+
+import oracle as O
 
 import ork
 from test_persist_host import HDR, _load
@@ -16,13 +19,14 @@ def test_grouped_gates_offline():
         assert not L.ork_i4_mm_pack_grouped(off.h, K, 96, ork.ptr(B[:, :96].copy()), 64)   # N % 64
         w = L.ork_i4_mm_pack_grouped(off.h, K, N, ork.ptr(B), 64)
         assert w and np.array_equal(ork.codes(w, K, N), B)
-        A = np.zeros((1, K), np.int8)
-        aS = np.ones((1, K // 64), np.float32)
-        bS = np.ones((K // 64, N), np.float32)
-        C = np.zeros((1, N), np.float32)
-        args = (1, ork.ptr(A), ork.ptr(aS), ork.ptr(bS), ork.ptr(C))
-        assert L.ork_i4_mm_run_grouped(off.h, w, *args) == -1      # offline: no CPU fallback
-        assert L.ork_i8_mm_run_grouped(off.h, w, *args) == -1
+        rng = np.random.default_rng(3)
+        A = rng.integers(-8, 8, size=(2, K), dtype=np.int8)
+        aS = rng.uniform(1e-3, 2e-2, size=(2, K // 64)).astype(np.float32)
+        bS = rng.uniform(1e-3, 2e-2, size=(K // 64, N)).astype(np.float32)
+        for fn in (L.ork_i4_mm_run_grouped, L.ork_i8_mm_run_grouped):   # offline: the CPU accumulate, any dtype
+            C = np.zeros((2, N), np.float32)
+            assert fn(off.h, w, 2, ork.ptr(A), ork.ptr(aS), ork.ptr(bS), ork.ptr(C)) == 0
+            assert np.array_equal(C, O.gemm_grouped(A, B, aS, bS, 64))
         L.ork_mm_free(off.h, w)
         wi = off.pack_i8(B)
         assert L.ork_w_set_group(wi, 64) == 0

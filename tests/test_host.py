@@ -2,7 +2,8 @@
 
 - libork_npu.so loads and exports every function include/*.h declares
 - offline-context surfaces: ork_i4a8_pack_cpu_blob(_qerr) byte-identical to the oracle, offline
-  pack / load keep the oracle's codes, every run on an offline context fails (-1, no CPU fallback)
+  pack / load keep the oracle's codes, and runs on an offline context compute the exact result on the CPU
+  as the reference's offline branches do (int8 / int4 / grouped runs, int8 chain, int4 chain and stream)
 - dims gates, O4N1 validation cases, ork_i8_mm_run_cpu vs the oracle
 """
 import ctypes as C
@@ -116,10 +117,10 @@ def test_offline_pack_i4a8_codes_and_dump(off, nf4):
     w2 = off.load_i4a8(K, N, blob)
     assert np.array_equal(ork.codes(w2, K, N), codes_ref)
     assert np.array_equal(ork.dump_i4a8(w2), blob)
-    # and a run on an offline context is refused, not computed on the CPU
-    A = np.ones((1, K), np.int8)
-    rc, _ = off.run_i8(w, A)
-    assert rc == -1
+    # and a run on an offline context is the exact CPU MAC on those codes (src/npu/i8/run.c:140)
+    A = np.random.default_rng(5).integers(-127, 128, size=(3, K), dtype=np.int8)
+    rc, Cg = off.run_i8(w, A)
+    assert rc == 0 and np.array_equal(Cg, O.gemm_i32(A, codes_ref))
     ork.free(w)
     ork.free(w2)
 
@@ -184,17 +185,40 @@ def test_dims_gates(off):
     L.ork_w_free(w)
 
 
-def test_offline_runs_fail(off):
+def test_offline_runs_compute_exactly(off):
+    """The reference's offline branches (src/npu/i8/run.c:140, src/npu/i4/run.c:236, grouped :48-49 and
+    src/npu/i4/run.c:368-369): an offline weight's runs are the exact CPU result, here checked against the
+    oracle. The product computes them with its own cpu_gemm.c, never the oracle."""
     L = ork.lib()
-    B = np.ones((64, 64), np.int8)
+    rng = np.random.default_rng(12)
+    K, N, M = 256, 96, 5
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
     w = off.pack_i8(B)
-    A = np.ones((2, 64), np.int8)
-    Cm = np.zeros((2, 64), np.int32)
-    assert L.ork_i8_mm_run(off.h, w, 2, ork.ptr(A), ork.ptr(Cm)) == -1
-    assert np.all(Cm == 0)
+    rc, Cm = off.run_i8(w, A)
+    assert rc == 0 and np.array_equal(Cm, O.gemm_i32(A, B))
+    # W4A4 (int4 values in int8 containers), N % 64
+    B4 = rng.integers(-8, 8, size=(K, 128), dtype=np.int8)
+    A4 = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    w4 = off.pack_i4(B4)
+    rc, C4 = off.run_i4(w4, A4)
+    assert rc == 0 and np.array_equal(C4, O.gemm_i32(A4, B4))
+    # grouped: per-group exact partials scaled and summed in group order, bit for bit
+    G = 64
+    aS = rng.uniform(1e-3, 2e-2, size=(M, K // G)).astype(np.float32)
+    bS = rng.uniform(1e-3, 2e-2, size=(K // G, 128)).astype(np.float32)
+    assert L.ork_w_set_group(w4, G) == 0
+    Cg = np.zeros((M, 128), np.float32)
+    assert L.ork_i4_mm_run_grouped(off.h, w4, M, ork.ptr(A4), ork.ptr(aS), ork.ptr(bS), ork.ptr(Cg)) == 0
+    assert np.array_equal(Cg, O.gemm_grouped(A4, B4, aS, bS, G))
+    if O.ref_available():
+        assert np.array_equal(Cg, O.ref_gemm_grouped(A4, B4, aS, bS, G))
+    # an offline context still has no device memory and no fp16 weights
     assert L.ork_dma_alloc(off.h, 64) is None
     assert L.ork_dev_alloc(off.h, 64) is None
+    assert not L.ork_f16_mm_pack(off.h, 64, 64, ork.ptr(np.zeros(64 * 64, np.float16)))
     ork.free(w)
+    ork.free(w4)
 
 
 def test_cpu_gemm_api_matches_oracle():
@@ -207,24 +231,39 @@ def test_cpu_gemm_api_matches_oracle():
         assert np.array_equal(Cm, O.gemm_i32(A, B))
 
 
-def test_chain_argument_checks_offline(off):
-    """ork/chain.h: bad arguments are -2 before anything else; an offline context cannot run (-1,
-    no CPU fallback in this build)."""
+def test_chain_offline(off):
+    """ork/chain.h on an offline context, as the reference's CPU chains (src/npu/core/buf.c:483-487, :560-564,
+    entered before any argument check): the int8 chain and the int4 chain / stream compute each task exactly
+    (C rows at stride N), S <= 0 runs nothing and returns 0; the int8 and fp16 streams have no offline path."""
     L = ork.lib()
-    B = np.zeros((64, 64), np.int8)
-    w = L.ork_i8_mm_pack(off.h, 64, 64, ork.ptr(B))
-    A = np.zeros((1, 64), np.int8)
-    Cb = np.zeros((1, 64), np.int32)
-    t = ork.tasks(ork.TaskI8, [(w, 1, A, Cb)])
-    assert L.ork_i8_mm_run_chain(off.h, 0, t) == -2
-    assert L.ork_i8_mm_run_chain(off.h, 1025, t) == -2
+    rng = np.random.default_rng(44)
+    K = 128
+    B1 = rng.integers(-128, 128, size=(K, 64), dtype=np.int8)
+    B2 = rng.integers(-8, 8, size=(K, 128), dtype=np.int8)
+    w1 = off.pack_i8(B1)
+    w2 = off.pack_i4(B2)
+    A1 = rng.integers(-128, 128, size=(3, K), dtype=np.int8)
+    A2 = rng.integers(-8, 8, size=(2, K), dtype=np.int8)
+    C1 = np.zeros((3, 64), np.int32)
+    C2 = np.zeros((2, 128), np.int32)
+    t = ork.tasks(ork.TaskI8, [(w1, 3, A1, C1), (w2, 2, A2, C2)])
+    assert L.ork_i8_mm_run_chain(off.h, 2, t) == 0
+    assert np.array_equal(C1, O.gemm_i32(A1, B1)) and np.array_equal(C2, O.gemm_i32(A2, B2))
+    C1[:] = 0
+    C2[:] = 0
+    t4 = ork.tasks(ork.TaskI4, [(w2, 2, A2, C2), (w1, 3, A1, C1)])
+    for fn in (L.ork_i4_mm_run_chain, L.ork_i4_mm_run_stream):
+        assert fn(off.h, 2, t4) == 0
+        assert np.array_equal(C1, O.gemm_i32(A1, B1)) and np.array_equal(C2, O.gemm_i32(A2, B2))
+    assert L.ork_i8_mm_run_chain(off.h, 0, t) == 0
     assert L.ork_i8_mm_run_chain(off.h, 1, None) == -2
+    # the streams without an offline branch, and contexts that are NULL
+    assert L.ork_i8_mm_run_stream(off.h, 1, t) == -1
     assert L.ork_i8_mm_run_chain(None, 1, t) == -1
     assert L.ork_i8_mm_run_stream(None, 1, t) == -2
-    assert L.ork_i8_mm_run_chain(off.h, 1, t) == -1
-    assert L.ork_i4_mm_run_stream(off.h, 0, ork.tasks(ork.TaskI4, [(w, 1, A, Cb)])) == -2
-    assert L.ork_f16_mm_run_stream(off.h, 0, ork.tasks(ork.TaskF16, [(w, 1, A, Cb)])) == -2
-    ork.free(w)
+    assert L.ork_f16_mm_run_stream(off.h, 0, ork.tasks(ork.TaskF16, [(w1, 1, A1, C1)])) == -2
+    ork.free(w1)
+    ork.free(w2)
 
 
 def test_accessors_null_safe():
@@ -236,3 +275,18 @@ def test_accessors_null_safe():
     assert L.ork_w_quant_kind(None) == -1
     assert L.ork_w_bscale(None) is None
     assert L.ork_i4a8_w_dump(None, None, 0) == 0
+
+
+def test_reference_offline_load_example_runs_unmodified():
+    """examples/test_offline_load.c from the reference, compiled unmodified against include/ and linked to
+    libork_npu.so (oracle/ref.mk): offline packs and loads of i4a8 blobs recover the exact codes, and
+    pack_cpu_blob(_qerr) is byte-identical to the device-context pack. Needs no GPU."""
+    import subprocess
+
+    exe = os.path.join(ROOT, "oracle", "_ref", "test_offline_load_on_mi355x")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref/test_offline_load_on_mi355x not built (needs the reference tree)")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "test_offline_load: PASS" in r.stdout
+    assert "FAIL" not in r.stdout

@@ -6,10 +6,12 @@ oracle's code, chosen so that a plausible slip fails it:
   the dequantisation error bound, the 1e-9 floor, max|q| = 127, and the reference's own RMS gate
   (examples/test_matmul.c:280-306)
 - NF4 (src/npu/i4/quant.c:70-90, src/npu/i4/pack.c:57): the int8 codebook, nearest-level by brute
-  force (ties to the upper level), the reference's accuracy gate (examples/test_matmul.c:402-427), and
-  for stochastic rounding the bracket and the hit frequency P(hi) = t
+  force, the exact float32 ties t == 0.5f (the upper level, :84 and :138) with the neighbours either
+  side, the reference's accuracy gate (examples/test_matmul.c:402-427), and for stochastic rounding the
+  bracket, the hit frequency P(hi) = t and the draw stream (which elements draw, channel order)
 - imatrix clip search (src/npu/i4/quant.c:26, :130-161): the chosen scale is on the clip grid and is
-  the grid's minimum of the weighted error (brute force in float64, up to float32 near-ties), the
+  the grid's minimum of the weighted error (brute force in float64), each candidate's error equals an
+  independent numpy float32 sequential sum bit for bit, exact ties keep the first candidate, the
   NULL path is absmax/7 exactly (examples/test_matmul.c:467-471), and the reference's importance gate
   (examples/test_matmul.c:430-500)
 - O4N1 (src/npu/i4/pack.c:91-103, :115-122; src/npu/internal.h:584, :597): header bytes, section
@@ -103,16 +105,206 @@ def test_nf4_nearest_level_brute_force():
     d = np.abs(W.astype(np.float64)[:, :, None] - L[None, None, :])
     chosen = d[np.arange(N)[:, None], np.arange(K)[None, :], idx]
     assert np.all(chosen <= d.min(axis=2) + 1e-6)
-    # a weight exactly on a level selects that level; a midpoint selects one of its two neighbours
+    # a weight exactly on a level selects that level (the exact float32 midpoints: the next test)
     Wl = np.zeros((32, 64), np.float32)  # N % 32 == 0 (pack gate); rows 1.. are all-zero channels
     Wl[0, 0:16] = L.astype(np.float32)
-    Wl[0, 16:31] = ((L[:-1] + L[1:]) / 2).astype(np.float32)
     _, nibl, _ = O.pack_i4a8(Wl, nf4=True)
     il = np.empty(64, np.int64)
     il[0::2] = nibl[0] & 0xF
     il[1::2] = nibl[0] >> 4
     assert list(il[0:16]) == list(range(16))
-    assert all(il[16 + i] in (i, i + 1) for i in range(15))
+
+
+def _nf4_tie_points():
+    """For every adjacent NF4 level pair (lo, hi = lo + 1): float32 normalised weights wn strictly inside the
+    bracket at which the reference's float32 position t = (wn - L[lo]) / (L[hi] - L[lo])
+    (src/npu/i4/quant.c:80-81, one float32 subtraction then one float32 division) is exactly 0.5f, and the
+    nearest weights on either side where t < 0.5f and t > 0.5f. Found by walking float32 neighbours of the
+    real midpoint; every step below is one IEEE binary32 operation (numpy float32 scalars)."""
+    L32 = NF4_LEVELS.astype(np.float32)
+    pts = []
+    for lo in range(15):
+        hi = lo + 1
+        d = np.float32(L32[hi] - L32[lo])
+        mid = np.float32((NF4_LEVELS[lo] + NF4_LEVELS[hi]) / 2)
+        ties, below, above = [], None, None
+        x = mid
+        for _ in range(64):                     # walk down to the last t < 0.5
+            x = np.nextafter(x, np.float32(-2), dtype=np.float32)
+        for _ in range(128):
+            t = np.float32(np.float32(x - L32[lo]) / d)
+            if t == np.float32(0.5):
+                ties.append(x)
+            elif t < np.float32(0.5):
+                below = x
+            elif above is None:
+                above = x
+            x = np.nextafter(x, np.float32(2), dtype=np.float32)
+        pts.append((lo, hi, ties, below, above))
+    return pts
+
+
+def test_nf4_exact_tie_takes_the_upper_level():
+    """src/npu/i4/quant.c:84 (and :138 in the clip search's error): idx = (t >= 0.5f) ? hi : lo. Where t is
+    exactly 0.5f the upper level wins; a flipped rule (t > 0.5f) or a nearest-level choice in real
+    arithmetic picks lo at some of these points. Checked on the oracle's packer, on its clip-search error
+    (the dequantised values it returns), and on the product's own quantiser (offline cpu_blob)."""
+    import ork
+
+    pts = _nf4_tie_points()
+    assert sum(len(t) for _, _, t, _, _ in pts) >= 5    # exact float32 ties exist for 6 of the 15 level pairs
+    vals, want = [1.0], [15]                           # absmax 1 -> inv = 1.0f, so wn == w exactly
+    for lo, hi, ties, below, above in pts:
+        for x in ties:
+            vals.append(float(x)); want.append(hi)
+        vals.append(float(below)); want.append(lo)
+        vals.append(float(above)); want.append(hi)
+    K = (len(vals) + 31) // 32 * 32
+    W = np.zeros((32, K), np.float32)
+    W[0, :len(vals)] = vals
+    W[0, len(vals):] = 0.0                             # exactly on level 7
+    want += [7] * (K - len(vals))
+    _, nib, _ = O.pack_i4a8(W, nf4=True)
+    idx = np.empty(K, np.int64)
+    idx[0::2] = nib[0] & 0xF
+    idx[1::2] = nib[0] >> 4
+    assert list(idx) == want
+    # the clip search's error path: dq[k] = (float)lut[idx] * (absmax / 127.0f), absmax 1
+    dq = np.zeros(K, np.float32)
+    O.lib().oracle_wq_err_chan(O._ptr(W[0]), K, 1.0, 1, None, O._ptr(dq))
+    lut32 = np.array(NF4_LUT, np.float32) * np.float32(np.float32(1.0) / np.float32(127.0))
+    assert np.array_equal(dq, lut32[want])
+    # the product's quantiser (its own quant.c, on an offline context) makes the same choice
+    with ork.Npu(offline="gfx950") as off:
+        blob = ork.cpu_blob(K, 32, W, None, nf4=1, ctx=off.h)
+    assert np.array_equal(blob[20 + 4 * 32:20 + 4 * 32 + K // 2], nib[0])
+
+
+def _wq_err32(fr, absmax, nf4, im):
+    """The clip search's weighted error (src/npu/i4/quant.c:130-149) restated in numpy float32, op by op:
+    the per-element dequantisation, d = w - dq, the term (im * d) * d, and a SEQUENTIAL float32 sum from
+    0.0f (np.add.accumulate on float32 is sequential), no fused multiply-add."""
+    f = np.float32
+    fr = fr.astype(np.float32)
+    if nf4:
+        sc = f(f(absmax) / f(127.0))
+        inv = f(f(1.0) / f(absmax)) if absmax > 0 else f(0.0)
+        wn = np.clip((fr * inv).astype(np.float32), f(-1.0), f(1.0))
+        L32 = NF4_LEVELS.astype(np.float32)
+        hi = np.minimum(np.searchsorted(L32, wn, side="left"), 15)   # first level >= wn
+        lo = np.maximum(hi - 1, 0)
+        with np.errstate(invalid="ignore", divide="ignore"):
+            t = ((wn - L32[lo]).astype(np.float32) / (L32[hi] - L32[lo]).astype(np.float32)).astype(np.float32)
+        idx = np.where(lo == hi, hi, np.where(t >= f(0.5), hi, lo))
+        dq = (np.array(NF4_LUT, np.float32)[idx] * sc).astype(np.float32)
+    else:
+        scale = f(f(absmax) / f(7.0))
+        inv = f(f(1.0) / scale) if scale > 0 else f(0.0)
+        q = np.clip(np.rint((fr * inv).astype(np.float32)), -7, 7).astype(np.float32)
+        dq = (q * scale).astype(np.float32)
+    d = (fr - dq).astype(np.float32)
+    w = im.astype(np.float32) if im is not None else np.ones_like(fr)
+    terms = ((w * d).astype(np.float32) * d).astype(np.float32)
+    return np.add.accumulate(np.concatenate([[f(0.0)], terms]).astype(np.float32), dtype=np.float32)[-1]
+
+
+@pytest.mark.parametrize("nf4", [0, 1])
+def test_imatrix_error_is_float32_sequential(nf4):
+    """The clip search's error value is the float32 sequential sum, bit for bit, for every grid candidate of
+    random channels (a float64 or pairwise accumulation, or a fused multiply-add, changes the low bits of
+    most of these sums), and the chosen scale is the FIRST strict minimum of those float32 values
+    (src/npu/i4/quant.c:155-158) -- also where every candidate's error is exactly equal (a channel that
+    is zero wherever the importance is non-zero), where `<=` would pick the last candidate."""
+    rng = np.random.default_rng(60 + nf4)
+    N, K = 48, 2048
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    W[:, ::53] *= 6
+    im = rng.uniform(0.5, 2.0, K).astype(np.float32)
+    im_sparse = np.zeros(K, np.float32)
+    im_sparse[7] = 1.0
+    Wt = W.copy()
+    Wt[:8, 7] = 0.0        # channels 0..7: zero wherever im_sparse is non-zero -> every candidate's error is 0
+    dq = np.zeros(K, np.float32)
+    L = O.lib()
+    for n in range(N):
+        fr = np.ascontiguousarray(W[n])
+        mx = np.float32(max(np.float32(1e-9), np.max(np.abs(fr))))
+        errs = []
+        for g in CLIP_GRID:
+            cand = np.float32(mx * np.float32(g))
+            e = L.oracle_wq_err_chan(O._ptr(fr), K, float(cand), nf4, O._ptr(im), O._ptr(dq))
+            assert np.float32(e) == _wq_err32(fr, cand, nf4, im), (n, g)
+            errs.append(np.float32(e))
+        best = 0
+        for g in range(1, 7):
+            if errs[g] < errs[best]:
+                best = g
+        got = L.oracle_wq_best_absmax(O._ptr(fr), K, float(mx), nf4, O._ptr(im), O._ptr(dq))
+        assert np.float32(got) == np.float32(mx * np.float32(CLIP_GRID[best])), n
+    for n in range(8):
+        fr = np.ascontiguousarray(Wt[n])
+        mx = np.float32(np.max(np.abs(fr)))
+        assert _wq_err32(fr, mx, nf4, im_sparse) == 0.0
+        got = L.oracle_wq_best_absmax(O._ptr(fr), K, float(mx), nf4, O._ptr(im_sparse), O._ptr(dq))
+        assert np.float32(got) == mx, n    # the first candidate (raw absmax) survives an exact tie
+    # the same pack through the product's quantiser (offline cpu_blob) and the oracle: byte-identical
+    import ork
+    with ork.Npu(offline="gfx950") as off:
+        for wv, iv in ((W, im), (Wt, im_sparse)):
+            blob = ork.cpu_blob(K, N, wv, iv, nf4=nf4, ctx=off.h)
+            assert np.array_equal(blob, O.i4a8_blob(wv, iv, nf4=bool(nf4)))
+
+
+def _xs32_stream(seed, n):
+    """xorshift32 (src/npu/internal.h:589): x ^= x << 13; x ^= x >> 17; x ^= x << 5, on uint32."""
+    out = np.empty(n, np.uint32)
+    x = np.uint32(seed)
+    for i in range(n):
+        x ^= np.uint32((int(x) << 13) & 0xFFFFFFFF)
+        x ^= np.uint32(int(x) >> 17)
+        x ^= np.uint32((int(x) << 5) & 0xFFFFFFFF)
+        out[i] = x
+    return out
+
+
+def test_nf4_stochastic_rounding_draw_stream():
+    """NF4 stochastic rounding (src/npu/i4/quant.c:78-84, seed src/npu/i4/pack.c:32): one xorshift32 draw
+    u = (x >> 8) / 2^24 per element INSIDE a bracket (wn == -1 has lo == hi and draws nothing), idx = hi iff
+    t > u, one stream running across the channels in order. The generator itself is pinned where the
+    reference builds (its uniform-int4 SR through oracle/_ref draws the same stream); the draw-skip and
+    cross-channel order are the reference's source read as text: a channel that starts with absmax-scaled
+    -1 weights must shift no draws (while wn == +1 sits in the bracket (L[14], L[15]] and draws one), and
+    channel 1 must continue channel 0's stream."""
+    N, K = 32, 64
+    L32 = NF4_LEVELS.astype(np.float32)
+    W = np.zeros((N, K), np.float32)
+    rng = np.random.default_rng(8)
+    for n in range(2):
+        W[n] = L32[7] + np.float32(0.5) * rng.uniform(0.05, 0.95, K).astype(np.float32) * (L32[8] - L32[7])
+        W[n, 0] = 1.0                       # absmax 1: wn = +1, bracket (14, 15], t = 1 > u: one draw, idx 15
+        W[n, 1:5] = -1.0                    # wn == -1: lo == hi == 0, no draw
+    _, nib, _ = O.pack_i4a8(W, nf4=True, sr=True)
+    u = (_xs32_stream(0x2545F491, 2 * K) >> np.uint32(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+    j = 0
+    for n in range(2):
+        idx = np.empty(K, np.int64)
+        idx[0::2] = nib[n] & 0xF
+        idx[1::2] = nib[n] >> 4
+        assert idx[0] == 15 and list(idx[1:5]) == [0] * 4
+        j += 1                              # the draw of element 0; elements 1..4 draw nothing
+        for k in range(5, K):
+            t = np.float32(np.float32(W[n, k] - L32[7]) / np.float32(L32[8] - L32[7]))
+            assert idx[k] == (8 if t > u[j] else 7), (n, k)
+            j += 1
+    if O.ref_available():
+        # the generator: the reference's own uniform SR consumes the same stream, one draw per element
+        fr = np.full(K, 0.3, np.float32)
+        seed = np.array([0x2545F491], np.uint32)
+        nibr = np.zeros(K // 2, np.uint8)
+        qf = np.zeros(K, np.float32)
+        O.ref().ref_i4_quant_chan(O._ptr(fr), K, 1.0, 1, O._ptr(seed), O._ptr(nibr), O._ptr(qf))
+        assert int(seed[0]) == int(_xs32_stream(0x2545F491, K)[-1])
+        assert np.array_equal(qf, np.floor(fr * np.float32(1.0) + u[:K]).astype(np.float32))
 
 
 def test_nf4_accuracy_gate():
