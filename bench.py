@@ -4,10 +4,13 @@
 Metric (BASELINE.json): "w8a8 M=1 GEMV HBM GB/s (% peak); M=512 int8 GEMM TOPS (% MFMA peak)".
 Workload (BASELINE config 1 shape): W f32[6144][2048] ~ N(0,0.02) seeded, packed once with
 ork_i8_mm_pack_f32 (per-channel int8); A int8 ~ U[-127,127]; C int32. A step is one ork_i8_mm_run
-call (M=1 for the headline value). The weight is packed into R=48 resident copies (48 x 12.6 MB =
-605 MB > 2 x the 256 MB MALL) and consecutive steps rotate through them, so every step streams its
-weight from HBM. A and C live in HBM (ork_dev_alloc); the steps are captured into one HIP graph and
-timed with HIP events on the library's stream, bracketed by device synchronisation.
+call (M=1 for the headline value). The weight is packed into R=64 resident copies (64 x 12.6 MB =
+805 MB > 3 x the 256 MB MALL) and consecutive steps rotate through them; when fewer steps than copies
+are timed, the copies outside the timed set are streamed by the same kernel just before the timed
+replay. Either way every timed step reads a weight that was last read more than 2 x MALL (512 MB) of
+other weights earlier, so it streams from HBM. A and C live in HBM (ork_dev_alloc); the steps are
+captured into one HIP graph and timed with HIP events on the library's stream, bracketed by device
+synchronisation.
 
 Also reported on the same line: the M=512 int8 GEMM (TOPS, % of dense int8 MFMA peak) as "m512",
 the eager (non-graph) launch rate, the reference's own calling convention (host A and C, one
@@ -29,7 +32,8 @@ sys.path.insert(0, os.path.join(ROOT, "ork-driver_amd"))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 K, N = 2048, 6144
-R = 48                          # rotated resident weight copies
+R = 64                          # rotated resident weight copies (64 x 12.6 MB = 805 MB)
+MALL_BYTES = 256 << 20          # MI355X Infinity Cache
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
 INT8_PEAK_TOPS = 5000.0         # MI355X dense int8 MFMA, TOP/s
 FP16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 MFMA, TFLOP/s
@@ -88,7 +92,9 @@ class Hip:
 
 def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scales=None):
     """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % len(ws)] through `entry`; the
-    grouped entry points also take the device scale buffers `scales` = (aScale, bScale)."""
+    grouped entry points also take the device scale buffers `scales` = (aScale, bScale). With fewer timed
+    steps than weights, a second graph streams the weights outside the timed set (ws[steps:]) right before
+    the timed replay, so the timed weights are as cold as in a full rotation."""
     import ork
 
     L = ork.lib()
@@ -105,13 +111,52 @@ def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scale
     for i in range(warmup):
         run(i)
     eager = hip.time_ms(stream, lambda: [run(i) for i in range(steps)]) / steps
-    # graph: one graph of exactly `steps` launches; warm it, then time one replay
+    # graph: one graph of exactly `steps` launches; warm it, stream the other weights, then time one replay
     g, ex = hip.capture(stream, lambda: [run(i) for i in range(steps)])
     hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")
+    flush = None
+    if steps < len(ws):
+        flush = hip.capture(stream, lambda: [run(i) for i in range(steps, len(ws))])
+        hip.ck(hip.L.hipGraphLaunch(flush[1], C.c_void_p(stream)), "hipGraphLaunch")
     graph = hip.time_ms(stream, lambda: hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")) / steps
+    for gg, ee in [(g, ex)] + ([flush] if flush else []):
+        hip.L.hipGraphExecDestroy(ee)
+        hip.L.hipGraphDestroy(gg)
+    return graph, eager
+
+
+def cold_distance(ws_bytes, n_ws, steps):
+    """Bytes of other weights read between a timed weight's previous read and its timed read."""
+    return (n_ws - 1) * ws_bytes if steps >= n_ws else (n_ws - steps) * ws_bytes
+
+
+def measure_copy(hip, L, npu, nbytes, steps, warmup=8):
+    """ms per device-to-device copy of nbytes (hipMemcpyAsync: the runtime's copy kernel, nbytes read + nbytes
+    written), graph-timed like measure() over R rotated source buffers: the data-movement reference beside the
+    GEMV, which reads the same nbytes of weight."""
+    stream = L.ork_npu_stream(npu.h)
+    bufs = [L.ork_dev_alloc(npu.h, nbytes) for _ in range(R)]
+    dst = L.ork_dev_alloc(npu.h, nbytes)
+    assert all(bufs) and dst
+    hip.L.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+
+    def run(i):
+        hip.ck(hip.L.hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(bufs[i % R]), nbytes, 3, C.c_void_p(stream)),
+               "hipMemcpyAsync")
+
+    for i in range(warmup):
+        run(i)
+    g, ex = hip.capture(stream, lambda: [run(i) for i in range(steps)])
+    hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")
+    if steps < R:
+        fl = hip.capture(stream, lambda: [run(i) for i in range(steps, R)])
+        hip.ck(hip.L.hipGraphLaunch(fl[1], C.c_void_p(stream)), "hipGraphLaunch")
+    ms = hip.time_ms(stream, lambda: hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")) / steps
     hip.L.hipGraphExecDestroy(ex)
     hip.L.hipGraphDestroy(g)
-    return graph, eager
+    for b in bufs + [dst]:
+        L.ork_dev_free(npu.h, b)
+    return ms
 
 
 def cpu_rows_baseline(fn_rows, M, nbytes, ops, bound, kind, what, budget_s):
@@ -554,7 +599,7 @@ def main():
         print(f"[bench] packed {R} x {K}x{N} int8 weights ({pack_s * 1e3:.1f} ms/pack); plans M=1 {gemv_plan}, "
               f"M=512 {gemm_plan}", file=sys.stderr, flush=True)
 
-        g1 = e1 = g512 = e512 = float("nan")
+        g1 = e1 = g512 = e512 = floor_ms = copy_ms = float("nan")
         if args.only == "chain":
             ms = measure_chain(npu, hip, L, ws, dA, dC, 8, 300)
             print(f"[bench] chain of 8: {ms * 1e3:.2f} us/call", file=sys.stderr, flush=True)
@@ -564,6 +609,16 @@ def main():
         if args.only not in ("m512",):
             g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup)
             print(f"[bench] M=1: graph {g1 * 1e3:.2f} us/step, eager {e1 * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+        if not args.only:
+            # the same graph harness around a launch that moves almost nothing (K=32, N=32), and around the runtime's
+            # copy kernel moving the weight's bytes: what one launch costs on this box before any data
+            tiny = npu.pack_i8(np.ones((32, 32), np.int8))
+            floor_ms, _ = measure(npu, hip, [tiny], 1, dA, dC, args.steps, args.warmup)
+            ork.lib().ork_mm_free(npu.h, tiny)
+            copy_ms = measure_copy(hip, L, npu, K * N, args.steps)
+            print(f"[bench] launch floor (K=32 N=32 GEMV): {floor_ms * 1e3:.2f} us/step; D2D copy of {K * N} B: "
+                  f"{copy_ms * 1e3:.2f} us ({2 * K * N / (copy_ms * 1e-3) / 1e9:.0f} GB/s read+write)",
+                  file=sys.stderr, flush=True)
         if args.only != "gemv":
             g512, e512 = measure(npu, hip, ws, 512, dA, dC, args.m512_steps, max(args.warmup // 8, 8))
             print(f"[bench] M=512: graph {g512 * 1e3:.2f} us/step, eager {e512 * 1e3:.2f} us/step",
@@ -644,12 +699,20 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights, U[-127,127] activations); 48 rotated resident weight copies",
+        "data": f"synthetic (seeded N(0,0.02) weights, U[-127,127] activations); {R} rotated resident weight copies: "
+                f"each timed step reads a weight last read {cold_distance(K * N, R, args.steps) / 1e6:.0f} MB of other "
+                f"weights earlier (> 2 x the 256 MB MALL)",
         "config": {"workload": "w8a8 GEMV ork_i8_mm_run M=1 K=2048 N=6144 (BASELINE config 1)",
                    "kernel": gemv_plan, "timing": "HIP graph of `steps` launches, HIP events"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_i8_m1")},
         "eager_value": round(algo_bytes(1) / (e1 * 1e-3) / 1e9, 1),
+        "launch_floor": {"gemv_k32_n32_us": round(floor_ms * 1e3, 3),
+                         "d2d_copy_us": round(copy_ms * 1e3, 3),
+                         "d2d_copy_gbs": round(2 * K * N / (copy_ms * 1e-3) / 1e9, 1),
+                         "note": "same HIP-graph harness and step count as `value`: ork_i8_mm_run on a K=32, N=32 weight "
+                                 "(a launch that moves almost nothing), and hipMemcpyAsync device-to-device of the "
+                                 "weight's 12,582,912 bytes from the same rotation (read + write counted)"},
         "chain8": {"value": round(chain_gbs, 1), "unit": "GB/s", "us_per_call": round(chain_ms * 1e3, 3),
                    "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("chain8_i8_m1"),
                    "note": "ork_i8_mm_run_chain: 8 M=1 GEMVs of the same shape (distinct resident weights) per call, "

@@ -248,10 +248,16 @@ def test_i4a8_vs_oracle(npu, nf4, imatrix, M):
     ork.free(w2)
 
 
-def test_i4a8_stochastic_rounding(npu):
+@pytest.mark.parametrize("nf4", [0, 1])
+@pytest.mark.parametrize("imatrix", [0, 1])
+def test_i4a8_stochastic_rounding(npu, nf4, imatrix):
+    """ORK_SR (src/npu/i4/pack.c:32, quant.c:32-33 / :82-83): one xorshift32 stream across the channels in order;
+    the device pack's bscale, nibble store (O4N1 bytes) and results equal the oracle's, uniform and NF4."""
+    _say("i4a8 SR", nf4, imatrix)
     K, N, M = 512, 128, 8
-    W, im, w, bs, bs_ref, codes, rng = _i4a8_case(npu, K, N, M, 0, 0, 1, 9)
+    W, im, w, bs, bs_ref, codes, rng = _i4a8_case(npu, K, N, M, nf4, imatrix, 1, 9 + nf4 + 2 * imatrix)
     assert np.array_equal(bs, bs_ref)
+    assert np.array_equal(ork.dump_i4a8(w), O.i4a8_blob(W, im, nf4=bool(nf4), sr=True))
     A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
     rc, C = npu.run_i8(w, A)
     assert rc == 0 and np.array_equal(C, O.gemm_i32(A, codes))
