@@ -19,6 +19,12 @@ void         ork_npu_set_async(ork_npu *ctx, int on);
 int          ork_npu_sync(ork_npu *ctx);
 /* The context's hipStream_t, for callers that order their own work after a run (or time it). */
 void        *ork_npu_stream(ork_npu *ctx);
+/* No counterpart in the reference: ork_i8_mm_run (include/ork/run.h:21) for callers that cannot allocate --
+ * code under HIP graph capture, serving loops and harnesses that forbid hipMalloc. A and C must be device memory
+ * (ork_dev_alloc or any hipMalloc); a split-K plan keeps its partials in a static 8 MiB per-GPU scratch array
+ * instead of a grown workspace, and a plan needing more is refused (-1). No call allocates. Calls that overlap
+ * on one GPU share that array and race. Same results and return codes as ork_i8_mm_run otherwise. */
+int          ork_i8_mm_run_noalloc(ork_npu *ctx, ork_w *w, int M, const int8_t *A, int32_t *C);
 /* Name of the kernel variant the planner picks for (kind of w, M); for diagnostics and profiling. */
 const char  *ork_w_plan_name(ork_npu *ctx, const ork_w *w, int M);
 /* The same for a grouped-scale run (ork_i8_mm_run_grouped / ork_i4_mm_run_grouped) of w at M rows:

@@ -44,7 +44,13 @@ typedef struct orkh_dev {
     int l2_bytes;
     char arch[64];        /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
     char name[256];
+    void *scratch;        /* this device's copy of the library's static scratch array (ORKH_SCRATCH_BYTES) */
 } orkh_dev;
+
+/* Device scratch of fixed size that needs no allocation: a file-scope __device__ array in orkh_runtime.hip, one
+ * copy per GPU, held until the process ends. orkh_init resolves this device's address of it (orkh_dev.scratch).
+ * Calls that use it on one GPU share it, so overlapping calls race; nothing in it starts at zero. */
+#define ORKH_SCRATCH_BYTES (8u << 20)
 
 /* ---- runtime ---- */
 int         orkh_device_count(void);

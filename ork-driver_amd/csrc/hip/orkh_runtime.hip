@@ -12,6 +12,11 @@
 
 static thread_local char g_err[256];
 
+// The split-K workspace of the no-allocation run (ork_i8_mm_run_noalloc): one copy per GPU, 256-byte aligned like
+// hipMalloc memory. Host code never uses this name as an address (on the host it is only a stand-in for the
+// symbol): orkh_init resolves each device's copy with hipGetSymbolAddress and hands that pointer out.
+static __device__ __align__(256) unsigned char scratch[ORKH_SCRATCH_BYTES];
+
 static int fail(hipError_t e, const char *what) {
     snprintf(g_err, sizeof g_err, "%s: %s", what, hipGetErrorString(e));
     return -1;
@@ -42,6 +47,13 @@ int orkh_init(int ordinal, orkh_dev *out, void **stream_out) {
     CK(hipSetDevice(ordinal), "hipSetDevice");
     hipDeviceProp_t p;
     CK(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
+    // this device's address of the scratch array, with the device current (each GPU holds its own copy)
+    void *scr = nullptr;
+    CK(hipGetSymbolAddress(&scr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!scr) {
+        snprintf(g_err, sizeof g_err, "hipGetSymbolAddress(scratch): NULL on device %d", ordinal);
+        return -1;
+    }
     if (out) {
         memset(out, 0, sizeof *out);
         out->ordinal = ordinal;
@@ -54,6 +66,7 @@ int orkh_init(int ordinal, orkh_dev *out, void **stream_out) {
         out->l2_bytes = p.l2CacheSize;
         snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
         snprintf(out->name, sizeof out->name, "%s", p.name);
+        out->scratch = scr;
     }
     if (stream_out) {
         hipStream_t s;

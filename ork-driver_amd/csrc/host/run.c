@@ -93,6 +93,62 @@ int ork_i8_mm_run(ork_npu *c, ork_w *w, int M, const int8_t *A, int32_t *C) {
     return run_common("ork_i8_mm_run", c, w, DT_I8, M, A, C, 1);
 }
 
+/* ork_i8_mm_run for callers that cannot allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc): A and C must already be device memory, and a split-K plan's partials go to the library's static
+ * per-GPU scratch array (ORKH_SCRATCH_BYTES) instead of the context's grown-on-demand workspace. Nothing here
+ * allocates, frees or calls an allocating routine. -1 on a NULL argument, an offline context, a weight that
+ * is not an int8-run weight, host A or C, A/C overlap, a plan whose partials exceed the scratch array, or a
+ * device failure. Returns after the launch in async mode, else after the stream sync, like ork_i8_mm_run.
+ * Calls that overlap on one GPU share its scratch array and race. */
+int ork_i8_mm_run_noalloc(ork_npu *c, ork_w *w, int M, const int8_t *A, int32_t *C) {
+    const char *who = "ork_i8_mm_run_noalloc";
+    if (!c || !w || !A || !C) { orki_err("%s: NULL argument", who); return -1; }
+    if (orki_need_device(c, who)) return -1;
+    if (w->dtype != DT_I8 || !w->dB) { orki_err("%s: weight is not a resident int8-run weight", who); return -1; }
+    if (M < 1) { orki_err("%s: M=%d", who, M); return -1; }
+    const int K = w->K, N = w->N;
+    if ((w->rkind == ORKH_I4U || w->rkind == ORKH_NF4) && K > ORKI_I4_K_MAX) {
+        orki_err("%s: K=%d exceeds the int4 path's exact-accumulation bound (K <= 131040)", who, K);
+        return -1;
+    }
+    const size_t abytes = (size_t)M * K, cbytes = (size_t)M * N * 4;
+    if (abytes >= ORKH_MAX_OPERAND_BYTES || w->dbytes >= ORKH_MAX_OPERAND_BYTES) {
+        orki_err("%s: operand too large for 32-bit buffer offsets (A %zu B, weight %zu B)", who, abytes, w->dbytes);
+        return -1;
+    }
+    if ((uintptr_t)A % 16 || !orkh_ptr_is_device(A) || !orkh_ptr_is_device(C)) {
+        orki_err("%s: A (16-byte aligned) and C must be device memory", who);
+        return -1;
+    }
+    if (orki_check_overlap(who, (uintptr_t)A, (uintptr_t)A + abytes, (uintptr_t)C, (uintptr_t)C + cbytes)) return -1;
+    orkh_plan q;
+    size_t ws = 0;
+    orki_plan(c, w->rkind, M, K, N, w->KB, &q, &ws);
+    if (ws > ORKH_SCRATCH_BYTES) {
+        orki_err("%s: the plan's split-K partials need %zu B, above the %u B scratch array", who, ws,
+                 (unsigned)ORKH_SCRATCH_BYTES);
+        return -1;
+    }
+    if (ws) q.ws = c->dev.scratch;
+    orkh_mm p;
+    memset(&p, 0, sizeof p);
+    p.kind = w->rkind;
+    p.M = M;
+    p.K = K;
+    p.N = N;
+    p.KB = w->KB;
+    p.A = A;
+    p.lda = K;
+    p.B = w->dB;
+    p.C = C;
+    p.ldc = N;
+    memcpy(p.lut, w->lut, sizeof p.lut);
+    if (orkh_mm_launch(&p, &q, c->stream)) { orki_hip_fail(who); return -1; }
+    if (c->async) return 0;
+    if (orkh_sync(c->stream)) { orki_hip_fail(who); return -1; }
+    return 0;
+}
+
 int ork_i4_mm_run(ork_npu *c, ork_w *w, int M, const int8_t *A, int32_t *C) {
     return run_common("ork_i4_mm_run", c, w, DT_I4, M, A, C, 1);
 }

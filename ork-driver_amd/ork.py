@@ -65,6 +65,7 @@ API = {
     "ork_i4a8_pack_cpu_blob_qerr": (C.c_size_t, [_P, C.c_int, C.c_int, _P, _P, C.c_int, _P, C.c_size_t, _P]),
     "ork_f16_mm_run": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "ork_i8_mm_run": (C.c_int, [_P, _P, C.c_int, _P, _P]),
+    "ork_i8_mm_run_noalloc": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "ork_i4_mm_run": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "ork_i8_mm_run_cpu": (None, [C.c_int, C.c_int, C.c_int, _P, _P, _P]),
     "ork_i8_mm_run_chain": (C.c_int, [_P, C.c_int, _P]),
