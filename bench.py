@@ -90,11 +90,15 @@ class Hip:
         return ms.value
 
 
-def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scales=None):
+def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scales=None, outer=None):
     """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % len(ws)] through `entry`; the
     grouped entry points also take the device scale buffers `scales` = (aScale, bScale). With fewer timed
     steps than weights, a second graph streams the weights outside the timed set (ws[steps:]) right before
-    the timed replay, so the timed weights are as cold as in a full rotation."""
+    the timed replay, so the timed weights are as cold as in a full rotation.
+    The graph ms/step is timed on the device: the graph's first and last nodes write the GPU wall clock
+    (ork_npu_mark), so the timed region is exactly the `steps` steps; the host's submission of the graph (one per
+    replay) falls outside it. The same replay is also timed by events recorded around the graph launch; that
+    launch-inclusive ms/step goes to outer[0] when a list is given."""
     import ork
 
     L = ork.lib()
@@ -111,18 +115,44 @@ def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scale
     for i in range(warmup):
         run(i)
     eager = hip.time_ms(stream, lambda: [run(i) for i in range(steps)]) / steps
-    # graph: one graph of exactly `steps` launches; warm it, stream the other weights, then time one replay
-    g, ex = hip.capture(stream, lambda: [run(i) for i in range(steps)])
+    # graph: timestamp node, exactly `steps` launches, timestamp node; warm it, stream the other weights, then time
+    # one replay
+    ts = L.ork_dev_alloc(npu.h, 16)
+    assert ts
+
+    def body():
+        if L.ork_npu_mark(npu.h, ts) or any(run(i) for i in range(steps)) or L.ork_npu_mark(npu.h, ts + 8):
+            raise RuntimeError("ork_npu_mark failed")
+
+    g, ex = hip.capture(stream, body)
     hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")
     flush = None
     if steps < len(ws):
         flush = hip.capture(stream, lambda: [run(i) for i in range(steps, len(ws))])
         hip.ck(hip.L.hipGraphLaunch(flush[1], C.c_void_p(stream)), "hipGraphLaunch")
-    graph = hip.time_ms(stream, lambda: hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")) / steps
+    launch_incl = hip.time_ms(stream, lambda: hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch"))
+    inner = graph_stamps_ms(npu, L, ts)
+    if not (0.0 < inner <= launch_incl * 1.001):
+        raise RuntimeError(f"in-graph timing {inner} ms outside (0, {launch_incl}] ms")
     for gg, ee in [(g, ex)] + ([flush] if flush else []):
         hip.L.hipGraphExecDestroy(ee)
         hip.L.hipGraphDestroy(gg)
-    return graph, eager
+    L.ork_dev_free(npu.h, ts)
+    if outer is not None:
+        outer.append(launch_incl / steps)
+    return inner / steps, eager
+
+
+def graph_stamps_ms(npu, L, ts):
+    """ms between the two wall-clock stamps (ork_npu_mark) the timed graph wrote to ts[0], ts[1]."""
+    import ork
+
+    t = np.zeros(2, np.uint64)
+    assert L.ork_dev_download(npu.h, ork.ptr(t), ts, 16) == 0
+    khz = L.ork_npu_wallclock_khz(npu.h)
+    if khz <= 0 or t[1] <= t[0]:
+        raise RuntimeError(f"bad wall-clock stamps {t} at {khz} kHz")
+    return float(t[1] - t[0]) / khz
 
 
 def cold_distance(ws_bytes, n_ws, steps):
@@ -361,12 +391,25 @@ def measure_chain(npu, hip, L, ws, dA, dC, S, steps):
 
     for i in range(2 * nsets):
         run(i)
-    g, ex = hip.capture(stream, lambda: [run(i) for i in range(steps)])
+    ts = L.ork_dev_alloc(npu.h, 16)
+    assert ts
+
+    def body():
+        if L.ork_npu_mark(npu.h, ts):
+            raise RuntimeError("ork_npu_mark failed")
+        for i in range(steps):
+            run(i)
+        if L.ork_npu_mark(npu.h, ts + 8):
+            raise RuntimeError("ork_npu_mark failed")
+
+    g, ex = hip.capture(stream, body)
     hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")
-    ms = hip.time_ms(stream, lambda: hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch")) / steps
+    hip.time_ms(stream, lambda: hip.ck(hip.L.hipGraphLaunch(ex, C.c_void_p(stream)), "hipGraphLaunch"))
+    ms = graph_stamps_ms(npu, L, ts)
     hip.L.hipGraphExecDestroy(ex)
     hip.L.hipGraphDestroy(g)
-    return ms
+    L.ork_dev_free(npu.h, ts)
+    return ms / steps
 
 
 def measure_decoder(npu, nf4, prompt_len=128, decode_len=256, graph=True):
@@ -606,8 +649,9 @@ def main():
             for w in ws:
                 ork.lib().ork_mm_free(npu.h, w)
             return
+        o1, o512 = [], []
         if args.only not in ("m512",):
-            g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup)
+            g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup, outer=o1)
             print(f"[bench] M=1: graph {g1 * 1e3:.2f} us/step, eager {e1 * 1e3:.2f} us/step", file=sys.stderr, flush=True)
         if not args.only:
             # the same graph harness around a launch that moves almost nothing (K=32, N=32), and around the runtime's
@@ -620,7 +664,7 @@ def main():
                   f"{copy_ms * 1e3:.2f} us ({2 * K * N / (copy_ms * 1e-3) / 1e9:.0f} GB/s read+write)",
                   file=sys.stderr, flush=True)
         if args.only != "gemv":
-            g512, e512 = measure(npu, hip, ws, 512, dA, dC, args.m512_steps, max(args.warmup // 8, 8))
+            g512, e512 = measure(npu, hip, ws, 512, dA, dC, args.m512_steps, max(args.warmup // 8, 8), outer=o512)
             print(f"[bench] M=512: graph {g512 * 1e3:.2f} us/step, eager {e512 * 1e3:.2f} us/step",
                   file=sys.stderr, flush=True)
         if args.only:
@@ -703,7 +747,14 @@ def main():
                 f"each timed step reads a weight last read {cold_distance(K * N, R, args.steps) / 1e6:.0f} MB of other "
                 f"weights earlier (> 2 x the 256 MB MALL)",
         "config": {"workload": "w8a8 GEMV ork_i8_mm_run M=1 K=2048 N=6144 (BASELINE config 1)",
-                   "kernel": gemv_plan, "timing": "HIP graph of `steps` launches, HIP events"},
+                   "kernel": gemv_plan,
+                   "timing": "one HIP graph of `steps` launches between two device wall-clock stamps written by its "
+                             "first and last nodes (ork_npu_mark: the timed region is exactly the steps on the device), "
+                             "device-synchronised before and after"},
+        "graph_launch_inclusive": {"ms_per_step": round(o1[0], 6) if o1 else None,
+                                   "value": round(algo_bytes(1) / (o1[0] * 1e-3) / 1e9, 1) if o1 else None,
+                                   "note": "the same replay timed by events recorded around hipGraphLaunch: adds the "
+                                           "host's one submission of the graph, spread over `steps`"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_i8_m1")},
         "eager_value": round(algo_bytes(1) / (e1 * 1e-3) / 1e9, 1),
@@ -716,12 +767,13 @@ def main():
         "chain8": {"value": round(chain_gbs, 1), "unit": "GB/s", "us_per_call": round(chain_ms * 1e3, 3),
                    "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("chain8_i8_m1"),
                    "note": "ork_i8_mm_run_chain: 8 M=1 GEMVs of the same shape (distinct resident weights) per call, "
-                           "one grouped launch; A and C in HBM; HIP graph of 300 calls"},
+                           "one grouped launch; A and C in HBM; HIP graph of 300 calls timed by in-graph wall-clock stamps"},
         "host_api": {"value": round(algo_bytes(1) / (host_us * 1e-6) / 1e9, 1), "unit": "GB/s",
                      "us_per_call": round(host_us, 2),
                      "note": "ork_i8_mm_run(M=1) with host A and C: H2D of A, launch, D2H of C, stream sync"},
         "m512": {"workload": "int8 GEMM ork_i8_mm_run M=512 K=2048 N=6144", "kernel": gemm_plan,
                  "value": round(tops, 1), "unit": "TOP/s", "ms_per_step": round(g512, 6), "steps": args.m512_steps,
+                 "graph_launch_inclusive_ms_per_step": round(o512[0], 6) if o512 else None,
                  "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                               "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": traffic_from_profiles("gemm_i8_m512")},
                  "hbm_gbs": round(algo_bytes(512) / (g512 * 1e-3) / 1e9, 1),

@@ -25,6 +25,11 @@ void        *ork_npu_stream(ork_npu *ctx);
  * instead of a grown workspace, and a plan needing more is refused (-1). No call allocates. Calls that overlap
  * on one GPU share that array and race. Same results and return codes as ork_i8_mm_run otherwise. */
 int          ork_i8_mm_run_noalloc(ork_npu *ctx, ork_w *w, int M, const int8_t *A, int32_t *C);
+/* Profiling: enqueue on the context's stream a timestamp of the device wall clock, written to 8-byte aligned
+ * device memory dev_u64 when the stream reaches it (a tiny kernel, so it also works inside a captured HIP graph,
+ * where event timestamps are not available). ork_npu_wallclock_khz gives the clock's constant rate. 0 / -1. */
+int          ork_npu_mark(ork_npu *ctx, void *dev_u64);
+int          ork_npu_wallclock_khz(const ork_npu *ctx);
 /* Name of the kernel variant the planner picks for (kind of w, M); for diagnostics and profiling. */
 const char  *ork_w_plan_name(ork_npu *ctx, const ork_w *w, int M);
 /* The same for a grouped-scale run (ork_i8_mm_run_grouped / ork_i4_mm_run_grouped) of w at M rows:

@@ -45,6 +45,7 @@ typedef struct orkh_dev {
     char arch[64];        /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
     char name[256];
     void *scratch;        /* this device's copy of the library's static scratch array (ORKH_SCRATCH_BYTES) */
+    int wall_khz;         /* rate of the device's constant wall clock (orkh_mark) */
 } orkh_dev;
 
 /* Device scratch of fixed size that needs no allocation: a file-scope __device__ array in orkh_runtime.hip, one
@@ -68,6 +69,9 @@ int         orkh_d2d(void *dst, const void *src, size_t n, void *stream);   /* a
 /* async strided copy: rows x width bytes, row pitches dpitch / spitch */
 int         orkh_d2h_2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t rows, void *stream);
 int         orkh_sync(void *stream);
+/* Enqueue on the stream one 1-thread kernel that writes the device wall clock (a 64-bit counter at
+ * orkh_dev.wall_khz) to dev_u64: a timestamp taken where the stream reaches it, also inside a captured graph. */
+int         orkh_mark(void *dev_u64, void *stream);
 int         orkh_device_sync(void);
 /* 1 if p is device (or device-mapped) memory known to the HIP runtime, 0 if plain host memory. */
 int         orkh_ptr_is_device(const void *p);

@@ -27,9 +27,22 @@ static int fail(hipError_t e, const char *what) {
         if (e_ != hipSuccess) return fail(e_, what);    \
     } while (0)
 
+// One thread stores the device wall clock (constant rate, orkh_dev.wall_khz): a timestamp in stream order.
+__global__ void k_mark(unsigned long long *p) { *p = wall_clock64(); }
+
 extern "C" {
 
 const char *orkh_last_error(void) { return g_err; }
+
+int orkh_mark(void *dev_u64, void *stream) {
+    if (!dev_u64 || (uintptr_t)dev_u64 % 8) {
+        snprintf(g_err, sizeof g_err, "orkh_mark: destination must be 8-byte aligned device memory");
+        return -1;
+    }
+    hipLaunchKernelGGL(k_mark, dim3(1), dim3(1), 0, (hipStream_t)stream, (unsigned long long *)dev_u64);
+    CK(hipGetLastError(), "k_mark launch");
+    return 0;
+}
 
 int orkh_device_count(void) {
     int n = 0;
@@ -67,6 +80,9 @@ int orkh_init(int ordinal, orkh_dev *out, void **stream_out) {
         snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
         snprintf(out->name, sizeof out->name, "%s", p.name);
         out->scratch = scr;
+        int wk = 0;
+        if (hipDeviceGetAttribute(&wk, hipDeviceAttributeWallClockRate, ordinal) != hipSuccess) wk = 0;
+        out->wall_khz = wk;
     }
     if (stream_out) {
         hipStream_t s;

@@ -327,6 +327,14 @@ int ork_dev_upload(ork_npu *c, void *dst, const void *src, size_t n) {
     return 0;
 }
 
+int ork_npu_mark(ork_npu *c, void *dev_u64) {
+    if (orki_need_device(c, "ork_npu_mark")) return -1;
+    if (orkh_mark(dev_u64, c->stream)) { orki_err("ork_npu_mark: %s", orkh_last_error()); return -1; }
+    return 0;
+}
+
+int ork_npu_wallclock_khz(const ork_npu *c) { return (c && !c->offline) ? c->dev.wall_khz : 0; }
+
 int ork_dev_download(ork_npu *c, void *dst, const void *src, size_t n) {
     if (orki_need_device(c, "ork_dev_download")) return -1;
     if (orkh_d2h(dst, src, n, c->stream) || orkh_sync(c->stream)) { orki_hip_fail("ork_dev_download"); return -1; }

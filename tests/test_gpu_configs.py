@@ -259,3 +259,27 @@ def test_plan_overrides_need_the_debug_switch(npu):
             os.environ["ORK_PLAN_DEBUG"] = saved
     assert forced.startswith("tiled_") and forced != default, (forced, default)
     ork.free(w)
+
+
+def test_wallclock_marks(npu):
+    """ork_npu_mark: stamps written in stream order (also inside a captured graph, as bench.py uses them) increase,
+    and the clock runs at the rate ork_npu_wallclock_khz reports (checked against host time over a sleep)."""
+    import time
+
+    _say("wall-clock marks")
+    L = ork.lib()
+    khz = L.ork_npu_wallclock_khz(npu.h)
+    assert khz > 0
+    ts = L.ork_dev_alloc(npu.h, 24)
+    assert ts
+    assert L.ork_npu_mark(npu.h, ts) == 0 and L.ork_npu_sync(npu.h) == 0
+    t0 = time.perf_counter()
+    time.sleep(0.2)
+    assert L.ork_npu_mark(npu.h, ts + 8) == 0 and L.ork_npu_sync(npu.h) == 0
+    dt_host = time.perf_counter() - t0
+    assert L.ork_npu_mark(npu.h, ts + 3) == -1            # misaligned
+    t = np.zeros(2, np.uint64)
+    assert L.ork_dev_download(npu.h, ork.ptr(t), ts, 16) == 0
+    dt_dev = float(t[1] - t[0]) / (khz * 1e3)
+    assert abs(dt_dev - dt_host) < 0.05 * dt_host + 0.01, (dt_dev, dt_host)
+    L.ork_dev_free(npu.h, ts)
