@@ -30,6 +30,11 @@ int          ork_i8_mm_run_noalloc(ork_npu *ctx, ork_w *w, int M, const int8_t *
  * where event timestamps are not available). ork_npu_wallclock_khz gives the clock's constant rate. 0 / -1. */
 int          ork_npu_mark(ork_npu *ctx, void *dev_u64);
 int          ork_npu_wallclock_khz(const ork_npu *ctx);
+/* The resident form of a device weight, for callers that run their own kernels on it (the decoder harness fuses
+ * its per-row operators into M = 1 matmul launches): the device address of its panels, the K-blocks per panel and
+ * the panel kind (0 int8, 1 uniform int4, 2 NF4, 3 fp16), laid out as ork-driver_amd/csrc/hip/orkh.h documents,
+ * and the NF4 codebook words (entry e in byte e % 4 of lut[e / 4]). 0, or -1 for NULL or an offline weight. */
+int          ork_w_device_panels(const ork_w *w, const void **panels, int *KB, int *kind, uint32_t lut[4]);
 /* Name of the kernel variant the planner picks for (kind of w, M); for diagnostics and profiling. */
 const char  *ork_w_plan_name(ork_npu *ctx, const ork_w *w, int M);
 /* The same for a grouped-scale run (ork_i8_mm_run_grouped / ork_i4_mm_run_grouped) of w at M rows:

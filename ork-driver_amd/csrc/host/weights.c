@@ -78,6 +78,15 @@ size_t ork_w_bytes(const ork_w *w) {
     return w->dbytes;
 }
 
+int ork_w_device_panels(const ork_w *w, const void **panels, int *KB, int *kind, uint32_t lut[4]) {
+    if (!w || !w->dB) return -1;
+    if (panels) *panels = w->dB;
+    if (KB) *KB = w->KB;
+    if (kind) *kind = w->rkind;
+    if (lut) memcpy(lut, w->lut, sizeof w->lut);
+    return 0;
+}
+
 void ork_w_dims(const ork_w *w, int *K, int *N) {
     if (K) *K = w ? w->K : 0;
     if (N) *N = w ? w->N : 0;

@@ -26,6 +26,9 @@ struct q3_lin {
     ork_w *w;
     float *ws; /* device: per-output-channel scales */
     int K, N;
+    const void *pan; /* the weight's resident panels (ork_w_device_panels), for the fused decode kernels */
+    int KB, kind;
+    unsigned lut[4];
 };
 
 struct q3_layer {
@@ -44,6 +47,7 @@ struct q3_model {
     q3_half *emb;
     float *nf;
     float *x, *q, *part, *rcos, *rsin;
+    float *att, *yffn; /* fused decode: the attention row [heads * head_dim] and silu(g) * u [ffn] */
     int8_t *a8x, *a8att, *a8ffn;
     float *asx, *asatt, *asffn;
     int32_t *cq, *ck, *cv, *co, *cg, *cu, *cd, *clog;
@@ -53,6 +57,7 @@ struct q3_model {
     int pos;      /* positions filled */
     int sampled;  /* a next token is waiting in best */
     int last_row; /* row of the last LM-head input in asx */
+    int fused;    /* decode with the fused M = 1 kernels where the weights allow (default 1) */
     void *graph;  /* captured decode step */
     void **dev;   /* every device buffer of the model */
     int ndev, capdev;
@@ -161,7 +166,8 @@ static int lin_dims(const q3_cfg *c, int layer, int which, int *K, int *N) {
 static int cfg_ok(const q3_cfg *c) {
     if (!c || c->layers < 1 || c->hidden < 64 || c->heads < 1 || c->kv_heads < 1 || c->heads % c->kv_heads ||
         c->head_dim < Q3_CHUNK || c->head_dim > Q3_MAX_HD || c->head_dim % 64 || c->ffn < 32 || c->vocab < 32 ||
-        c->max_ctx < 1 || c->max_ctx > Q3_MAX_S * Q3_CHUNK || c->max_rows < 1 || c->max_rows > c->max_ctx)
+        c->max_ctx < 1 || c->max_ctx > Q3_MAX_S * Q3_CHUNK || c->max_rows < 1 || c->max_rows > c->max_ctx ||
+        c->ffn_nf4 < 0 || c->ffn_nf4 > 2)
         return 0;
     if (Q3_ATT_LDS(256 / c->head_dim, c->head_dim) > 65536) return 0;
     /* the matmul API's dimension rules: K % 32, N % 32 */
@@ -241,6 +247,8 @@ q3_model *q3_create(ork_npu *ctx, const q3_cfg *cfg) {
     DA(m->x, R * H * 4);
     DA(m->q, R * QD * 4);
     DA(m->part, R * c->heads * m->S * (HD + 2) * 4);
+    DA(m->att, QD * 4);
+    DA(m->yffn, F * 4);
     DA(m->rcos, (size_t)c->max_ctx * (HD / 2) * 4);
     DA(m->rsin, (size_t)c->max_ctx * (HD / 2) * 4);
     DA(m->a8x, R * H);
@@ -282,6 +290,7 @@ q3_model *q3_create(ork_npu *ctx, const q3_cfg *cfg) {
         const unsigned long long b0 = 0;
         if (upload(m, m->st, st0, sizeof st0) || upload(m, m->best, &b0, 8)) goto fail;
     }
+    m->fused = 1;
     ork_npu_set_async(ctx, 1);
     return m;
 fail:
@@ -298,12 +307,13 @@ int q3_set_linear(q3_model *m, int layer, int which, const float *w) {
     struct q3_lin *L = layer == -1 ? &m->lm : &m->L[layer].l[which];
     float *bs = malloc((size_t)N * 4);
     if (!bs) return -1;
-    const int nf4 = layer >= 0 && m->c.ffn_nf4 && (which == Q3_WG || which == Q3_WU || which == Q3_WD);
+    const int w4 = layer >= 0 && m->c.ffn_nf4 && (which == Q3_WG || which == Q3_WU || which == Q3_WD);
     ork_w *pw;
-    if (nf4) { /* ork_i4a8_mm_pack selects the NF4 codebook when ORK_NF4 is present */
+    if (w4) { /* ork_i4a8_mm_pack selects the NF4 codebook when ORK_NF4 is present, uniform int4 otherwise */
         const char *prev = getenv("ORK_NF4");
         char *saved = prev ? strdup(prev) : NULL;
-        setenv("ORK_NF4", "1", 1);
+        if (m->c.ffn_nf4 == 2) unsetenv("ORK_NF4");
+        else setenv("ORK_NF4", "1", 1);
         pw = ork_i4a8_mm_pack(m->ctx, K, N, w, bs);
         if (saved) {
             setenv("ORK_NF4", saved, 1);
@@ -332,6 +342,14 @@ int q3_set_linear(q3_model *m, int layer, int which, const float *w) {
     }
     if (L->w) ork_mm_free(m->ctx, L->w);
     L->w = pw;
+    L->pan = NULL;
+    if (ork_w_device_panels(pw, &L->pan, &L->KB, &L->kind, L->lut)) L->pan = NULL;
+    /* a captured decode step holds the old weight's addresses */
+    if (m->graph) {
+        (void)ork_npu_sync(m->ctx);
+        q3g_destroy(m->graph);
+        m->graph = NULL;
+    }
     return 0;
 }
 
@@ -478,6 +496,161 @@ static int pass(q3_model *m, int M, int decode) {
     return 0;
 }
 
+/* ---- the fused decode step (M = 1) --------------------------------------------------------------------------- *
+ * Per layer: q/k/v as one k_fgemv whose prologue is the attention RMSNorm + int8 row (layer 0: the embedding
+ * kernel and the q/k/v chain, as in pass()); attention partials; the chunk combine into an fp32 row; o with the
+ * row's quant in its prologue and the residual add in its epilogue; gate/up with the FFN RMSNorm prologue and the
+ * silu(g) * u epilogue; down with the quant prologue and the residual add. 6 launches per layer instead of 9, with
+ * the same float operations in the same order, so logits and tokens equal those of pass(). */
+static int fused_ok(const q3_model *m) {
+    const q3_cfg *c = &m->c;
+    if (!m->fused) return 0;
+    for (int l = 0; l < c->layers; l++) {
+        const struct q3_lin *L = m->L[l].l;
+        for (int i = 0; i < Q3_NLIN; i++) {
+            const int kpb = L[i].kind == 0 ? 64 : 128;
+            if (!L[i].pan || L[i].kind < 0 || L[i].kind > 2 || L[i].N % 16 || L[i].KB * kpb > Q3_FG_KMAX) return 0;
+        }
+        if (L[Q3_WQ].kind || L[Q3_WK].kind || L[Q3_WV].kind || L[Q3_WQ].KB != L[Q3_WK].KB ||
+            L[Q3_WQ].KB != L[Q3_WV].KB || L[Q3_WG].kind != L[Q3_WU].kind || L[Q3_WG].KB != L[Q3_WU].KB)
+            return 0;
+    }
+    return 1;
+}
+
+static int pass_fused(q3_model *m) {
+    const q3_cfg *c = &m->c;
+    void *s = m->stream;
+    const int H = c->hidden, NH = c->heads, NKV = c->kv_heads, HD = c->head_dim, F = c->ffn;
+    for (int l = 0; l < c->layers; l++) {
+        struct q3_layer *Ly = &m->L[l];
+        const struct q3_lin *Lq = &Ly->l[Q3_WQ], *Lk = &Ly->l[Q3_WK], *Lv = &Ly->l[Q3_WV], *Lo = &Ly->l[Q3_WO],
+                            *Lg = &Ly->l[Q3_WG], *Lu = &Ly->l[Q3_WU], *Ld = &Ly->l[Q3_WD];
+        if (l == 0) {
+            q3_nq nq = {0};
+            nq.M = 1;
+            nq.H = H;
+            nq.V = c->vocab;
+            nq.x = m->x;
+            nq.st = m->st;
+            nq.toks = m->toks;
+            nq.nw = Ly->n1;
+            nq.eps = c->eps;
+            nq.a8 = m->a8x;
+            nq.as = m->asx;
+            nq.emb = m->emb;
+            nq.best = m->best;
+            CK(q3k_norm_quant(&nq, s));
+            ork_mm_task_i8 qkv[3] = {{Lq->w, 1, m->a8x, m->cq, 0}, {Lk->w, 1, m->a8x, m->ck, 0},
+                                     {Lv->w, 1, m->a8x, m->cv, 0}};
+            CK(ork_i8_mm_run_chain(m->ctx, 3, qkv));
+        } else {
+            q3_fg f = {0};
+            f.K = H;
+            f.KB = Lq->KB;
+            f.kind = 0;
+            f.epi = Q3_EPI_STORE;
+            f.nt = 3;
+            f.B[0] = Lq->pan;
+            f.B[1] = Lk->pan;
+            f.B[2] = Lv->pan;
+            f.nb[0] = Lq->N / 16;
+            f.nb[1] = Lk->N / 16;
+            f.nb[2] = Lv->N / 16;
+            f.C[0] = m->cq;
+            f.C[1] = m->ck;
+            f.C[2] = m->cv;
+            f.row = m->x;
+            f.nw = Ly->n1;
+            f.eps = c->eps;
+            f.as_out = m->asx;
+            CK(q3k_fgemv(&f, s));
+        }
+        q3_att at = {.M = 1, .NH = NH, .NKV = NKV, .HD = HD, .S = m->S, .max_ctx = c->max_ctx, .q = m->q,
+                     .kc = Ly->kc, .vc = Ly->vc, .st = m->st, .scale = 1.0f / sqrtf((float)HD), .part = m->part,
+                     .cq = m->cq, .ck = m->ck, .cv = m->cv, .as = m->asx, .wsq = Lq->ws, .wsk = Lk->ws,
+                     .wsv = Lv->ws, .qn = Ly->qn, .kn = Ly->kn, .eps = c->eps, .rcos = m->rcos, .rsin = m->rsin};
+        CK(q3k_attn_part(&at, s));
+        const q3_comb cb = {NH, HD, m->S, m->part, m->att};
+        CK(q3k_attn_combine(&cb, s));
+        q3_fg fo = {0};
+        fo.K = NH * HD;
+        fo.KB = Lo->KB;
+        fo.kind = Lo->kind;
+        fo.epi = Q3_EPI_RESID;
+        fo.nt = 1;
+        fo.B[0] = Lo->pan;
+        fo.nb[0] = H / 16;
+        fo.row = m->att;
+        fo.ws0 = Lo->ws;
+        fo.x = m->x;
+        CK(q3k_fgemv(&fo, s));
+        q3_fg fg = {0};
+        fg.K = H;
+        fg.KB = Lg->KB;
+        fg.kind = Lg->kind;
+        memcpy(fg.lut, Lg->lut, sizeof fg.lut);
+        fg.epi = Q3_EPI_SWIGLU;
+        fg.nt = 2;
+        fg.B[0] = Lg->pan;
+        fg.B[1] = Lu->pan;
+        fg.nb[0] = F / 16;
+        fg.nb[1] = F / 16;
+        fg.row = m->x;
+        fg.nw = Ly->n2;
+        fg.eps = c->eps;
+        fg.ws0 = Lg->ws;
+        fg.ws1 = Lu->ws;
+        fg.y = m->yffn;
+        CK(q3k_fgemv(&fg, s));
+        q3_fg fd = {0};
+        fd.K = F;
+        fd.KB = Ld->KB;
+        fd.kind = Ld->kind;
+        memcpy(fd.lut, Ld->lut, sizeof fd.lut);
+        fd.epi = Q3_EPI_RESID;
+        fd.nt = 1;
+        fd.B[0] = Ld->pan;
+        fd.nb[0] = H / 16;
+        fd.row = m->yffn;
+        fd.ws0 = Ld->ws;
+        fd.x = m->x;
+        CK(q3k_fgemv(&fd, s));
+    }
+    q3_nq fn = {0}; /* the residual add is done: plain final norm */
+    fn.M = 1;
+    fn.H = H;
+    fn.V = c->vocab;
+    fn.x = m->x;
+    fn.st = m->st;
+    fn.toks = m->toks;
+    fn.nw = m->nf;
+    fn.eps = c->eps;
+    fn.a8 = m->a8x;
+    fn.as = m->asx;
+    CK(q3k_norm_quant(&fn, s));
+    CK(ork_i8_mm_run(m->ctx, m->lm.w, 1, m->a8x, m->clog));
+    const q3_amax am = {c->vocab, m->clog, m->asx, m->lm.ws, m->best};
+    CK(q3k_argmax(&am, s));
+    m->last_row = 0;
+    return 0;
+}
+
+static int decode_pass(q3_model *m) { return fused_ok(m) ? pass_fused(m) : pass(m, 1, 1); }
+
+int q3_set_fused(q3_model *m, int on) {
+    if (!m) return -2;
+    if ((on != 0) != m->fused) {
+        if (ork_npu_sync(m->ctx)) return -1;
+        q3g_destroy(m->graph);
+        m->graph = NULL;
+    }
+    m->fused = on != 0;
+    return 0;
+}
+
+int q3_decode_fused(const q3_model *m) { return m ? fused_ok(m) : 0; }
+
 static int weights_ready(const q3_model *m) {
     if (!m->lm.w) return 0;
     for (int l = 0; l < m->c.layers; l++)
@@ -516,7 +689,7 @@ int q3_decode(q3_model *m, int steps, int graph) {
     for (int i = 0; i < steps; i++) {
         if (graph && !m->graph) {
             if (q3g_begin(m->stream)) return -1;
-            const int rc = pass(m, 1, 1);
+            const int rc = decode_pass(m);
             void *g = NULL;
             const int rc2 = q3g_end(m->stream, &g);
             if (rc || rc2) {
@@ -529,7 +702,7 @@ int q3_decode(q3_model *m, int steps, int graph) {
         if (graph) {
             if (q3g_launch(m->graph, m->stream)) return -1;
         } else {
-            CK(pass(m, 1, 1));
+            CK(decode_pass(m));
         }
         m->pos++;
     }

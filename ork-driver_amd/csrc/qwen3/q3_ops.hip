@@ -521,6 +521,221 @@ __global__ void k_argmax(q3_amax p) {
     }
 }
 
+// ---- fused M = 1 matmul of the decode step ------------------------------------------------------------------
+// k_fgemv: one 16-column panel per workgroup (pair mode: the same columns of two weights), 8 waves splitting the
+// panel's K-blocks, on the library's resident layout (lane l of a 1 KiB block holds 16 bytes of column l % 16,
+// k-group l / 16). Around that GEMV:
+//   prologue: the int8 row, built in LDS by every workgroup: PRO_NORM = RMSNorm of the residual row then the
+//     per-row quant (norm_quant_body's operations with its 512-thread element mapping, so the sum of squares is
+//     rounded identically); PRO_QUANT = the per-row quant of a float row (quant_regs' operations; the absmax is
+//     order-independent). The weight blocks of each wave are loaded before the prologue, which hides their
+//     memory latency behind it.
+//   epilogue on each column's int32 sum: STORE; RESID x[n] += (c * a_scale) * ws[n] (the residual add that
+//     k_norm_quant_acc would do next); SWIGLU y[n] = silu(g) * u from the gate and up sums (k_swiglu_quant's
+//     operations).
+// So the rows, scales and results equal those of the unfused kernels bit for bit.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+struct FgLut { uint32_t l0, l1, l2, l3; };
+// One dword of NF4 codes -> the int8 codebook values of its low nibbles (lo) and of its high nibbles (hi):
+// v_perm selects within the 8 bytes of two LUT words by the low 3 bits of each code, and a second v_perm takes
+// that from the upper or the lower LUT half by the code's top bit.
+__device__ inline void fg_nf4_map8(uint32_t x, const FgLut &L, uint32_t &lo, uint32_t &hi) {
+    const uint32_t i0 = x & 0x07070707u, i1 = (x >> 4) & 0x07070707u;
+    const uint32_t s0 = ((x >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t s1 = ((x >> 5) & 0x04040404u) | 0x03020100u;
+    lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L.l3, L.l2, i0), __builtin_amdgcn_perm(L.l1, L.l0, i0), s0);
+    hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L.l3, L.l2, i1), __builtin_amdgcn_perm(L.l1, L.l0, i1), s1);
+}
+
+// One lane's 16 bytes of a block against the row: int8 = 16 k; nibble kinds = 32 k, dword d holding
+// k = 8 d .. 8 d + 3 in its low nibbles and 8 d + 4 .. 8 d + 7 in its high nibbles. Uniform int4 codes are
+// widened as 16 v (the sum is shifted back once, exactly); NF4 codes map through the codebook.
+template <int KIND>
+__device__ inline int fg_dot(v4i_t raw, const int *__restrict__ a, int acc, const FgLut &L) {
+    const uint32_t xs[4] = {(uint32_t)raw.x, (uint32_t)raw.y, (uint32_t)raw.z, (uint32_t)raw.w};
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        if constexpr (KIND == 0) {
+            acc = __builtin_amdgcn_sdot4(a[d], (int)xs[d], acc, false);
+        } else {
+            uint32_t lo, hi;
+            if constexpr (KIND == 1) {
+                lo = (xs[d] << 4) & 0xf0f0f0f0u;
+                hi = xs[d] & 0xf0f0f0f0u;
+            } else {
+                fg_nf4_map8(xs[d], L, lo, hi);
+            }
+            acc = __builtin_amdgcn_sdot4(a[2 * d], (int)lo, acc, false);
+            acc = __builtin_amdgcn_sdot4(a[2 * d + 1], (int)hi, acc, false);
+        }
+    }
+    return acc;
+}
+
+constexpr int FG_WAVES = 8;  // 512 threads: norm_quant_body's element mapping
+constexpr int FG_PRE = 8;    // K-blocks per wave and panel loaded ahead of the prologue
+
+template <int PRO, int EPI, int KIND, int E>
+__global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
+    __shared__ __align__(16) int8_t arow[Q3_FG_KMAX];
+    __shared__ __align__(16) float red[16];
+    __shared__ __align__(16) float redq[16];
+    __shared__ int racc[FG_WAVES][2][16];
+    constexpr bool PAIR = EPI == Q3_EPI_SWIGLU;
+    constexpr int KPB = KIND == 0 ? 64 : 128;
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int K = p.K, KB = p.KB;
+
+    // ---- this workgroup's panel(s) and this wave's K-blocks (loads clamped, branch-free)
+    int t = 0, pnl = blockIdx.x;
+    if constexpr (!PAIR) {
+        while (t < p.nt - 1 && pnl >= p.nb[t]) {
+            pnl -= p.nb[t];
+            t++;
+        }
+    }
+    const int kbw = (KB + FG_WAVES - 1) / FG_WAVES, kb0 = min(wv * kbw, KB), kb1 = min(kb0 + kbw, KB);
+    const v4i_t *b0 = (const v4i_t *)p.B[t] + (size_t)pnl * KB * 64 + lane;
+    const v4i_t *b1 = PAIR ? (const v4i_t *)p.B[1] + (size_t)pnl * KB * 64 + lane : b0;
+    // the row's loads are issued first: the wait for them then leaves the weight loads in flight
+    float y[E], nw[E];
+    load_row(y, p.row, K);
+    if constexpr (PRO == Q3_PRO_NORM) load_row(nw, p.nw, K);
+    v4i_t r0[FG_PRE], r1[FG_PRE];
+#pragma unroll
+    for (int u = 0; u < FG_PRE; u++) {
+        const size_t o = (size_t)min(kb0 + u, KB - 1) * 64;
+        r0[u] = __builtin_nontemporal_load(b0 + o);
+        if constexpr (PAIR) r1[u] = __builtin_nontemporal_load(b1 + o);
+    }
+
+    // ---- prologue: the int8 row in LDS
+    float mx = 0.f;
+    if constexpr (PRO == Q3_PRO_NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < E; k++) ss += y[k] * y[k];
+        ss = block_sum(ss, red);
+        const float r = 1.0f / sqrtf(ss / (float)K + p.eps);
+#pragma unroll
+        for (int k = 0; k < E; k++) y[k] = (y[k] * r) * nw[k];
+    }
+#pragma unroll
+    for (int k = 0; k < E; k++)
+        if (threadIdx.x + k * blockDim.x < (unsigned)K) mx = fmaxf(mx, fabsf(y[k]));
+    mx = block_max(mx, redq);
+    const float as = mx > 0.f ? mx / 127.0f : 1.0f;
+    {
+        const float inv = 1.0f / as;
+#pragma unroll
+        for (int k = 0; k < E; k++) {
+            const int i = threadIdx.x + k * blockDim.x;
+            if (i < K) {
+                float r = y[k] * inv;
+                if (fabsf(r - floorf(r) - 0.5f) < 1e-4f) r = y[k] / as;
+                r = fminf(fmaxf(rintf(r), -127.f), 127.f);
+                arow[i] = (int8_t)(int)r;
+            }
+        }
+        for (int i = K + (int)threadIdx.x; i < KB * KPB; i += (int)blockDim.x) arow[i] = 0;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0 && p.as_out) *p.as_out = as;
+    __syncthreads();
+
+    // ---- the GEMV: the preloaded blocks, then any further ones of this wave
+    const FgLut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
+    const int aoff = (lane >> 4) * (KPB / 4);
+    int acc0 = 0, acc1 = 0;
+#pragma unroll
+    for (int u = 0; u < FG_PRE; u++) {
+        if (kb0 + u < kb1) {
+            const int *a = (const int *)(arow + (kb0 + u) * KPB + aoff);
+            acc0 = fg_dot<KIND>(r0[u], a, acc0, L);
+            if constexpr (PAIR) acc1 = fg_dot<KIND>(r1[u], a, acc1, L);
+        }
+    }
+    for (int kb = kb0 + FG_PRE; kb < kb1; kb++) {
+        const v4i_t s0 = __builtin_nontemporal_load(b0 + (size_t)kb * 64);
+        v4i_t s1 = s0;
+        if constexpr (PAIR) s1 = __builtin_nontemporal_load(b1 + (size_t)kb * 64);
+        const int *a = (const int *)(arow + kb * KPB + aoff);
+        acc0 = fg_dot<KIND>(s0, a, acc0, L);
+        if constexpr (PAIR) acc1 = fg_dot<KIND>(s1, a, acc1, L);
+    }
+    // the four k-groups of a column are lanes l, l ^ 16, l ^ 32, l ^ 48; then the waves through LDS, in order
+    {
+        auto s32 = __builtin_amdgcn_permlane32_swap(acc0, acc0, false, false);
+        acc0 += (int)((lane & 32) == 0 ? s32[1] : s32[0]);
+        auto s16 = __builtin_amdgcn_permlane16_swap(acc0, acc0, false, false);
+        acc0 += (int)((lane & 16) == 0 ? s16[1] : s16[0]);
+        if constexpr (PAIR) {
+            auto t32 = __builtin_amdgcn_permlane32_swap(acc1, acc1, false, false);
+            acc1 += (int)((lane & 32) == 0 ? t32[1] : t32[0]);
+            auto t16 = __builtin_amdgcn_permlane16_swap(acc1, acc1, false, false);
+            acc1 += (int)((lane & 16) == 0 ? t16[1] : t16[0]);
+        }
+    }
+    if (lane < 16) {
+        racc[wv][0][lane] = acc0;
+        racc[wv][1][lane] = acc1;
+    }
+    __syncthreads();
+    if (threadIdx.x >= 16) return;
+    const int j = threadIdx.x;
+    int c0 = 0, c1 = 0;
+#pragma unroll
+    for (int w = 0; w < FG_WAVES; w++) {
+        c0 += racc[w][0][j];
+        if constexpr (PAIR) c1 += racc[w][1][j];
+    }
+    if constexpr (KIND == 1) { // every block's partial is 16 x an integer
+        c0 >>= 4;
+        c1 >>= 4;
+    }
+    const int n = pnl * 16 + j;
+    if constexpr (EPI == Q3_EPI_STORE) {
+        p.C[t][n] = c0;
+    } else if constexpr (EPI == Q3_EPI_RESID) {
+        p.x[n] = p.x[n] + ((float)c0 * as) * p.ws0[n];
+    } else {
+        const float gv = ((float)c0 * as) * p.ws0[n];
+        const float uv = ((float)c1 * as) * p.ws1[n];
+        p.y[n] = (gv / (1.0f + expf(-gv))) * uv;
+    }
+}
+
+// k_attn_combine: one workgroup per query head, thread d = dimension d: the log-sum-exp combine of the head's
+// chunks with attn_quant_body's operations in its order, so the row equals the one that kernel quantises.
+__global__ __launch_bounds__(Q3_MAX_HD) void k_attn_combine(q3_comb p) {
+    __shared__ float w[Q3_MAX_S];
+    __shared__ float inv;
+    const int h = blockIdx.x, HD = p.HD, S = p.S, d = threadIdx.x;
+    const float *__restrict__ ph = p.part + (size_t)h * S * (HD + 2);
+    float acc[Q3_MAX_S];
+#pragma unroll
+    for (int s = 0; s < Q3_MAX_S; s++) {
+        const float x = ph[(size_t)min(s, S - 1) * (HD + 2) + d];
+        acc[s] = s < S ? x : 0.f;
+    }
+    if (threadIdx.x < 64) {
+        const int ln = threadIdx.x, sc = min(ln, S - 1);
+        const float m0 = ph[(size_t)sc * (HD + 2) + HD], l0 = ph[(size_t)sc * (HD + 2) + HD + 1];
+        const float m = ln < S ? m0 : -INFINITY;
+        const float mxm = wave_max(m);
+        const float e = m == -INFINITY ? 0.f : expf(m - mxm);
+        const float den = wave_sum(ln < S ? l0 * e : 0.f);
+        if (ln < S) w[ln] = e;
+        if (ln == 0) inv = den > 0.f ? 1.0f / den : 0.f;
+    }
+    __syncthreads();
+    float num = 0.f;
+#pragma unroll
+    for (int s = 0; s < Q3_MAX_S; s++)
+        if (s < S) num += acc[s] * w[s];
+    p.out[(size_t)h * HD + d] = num * inv;
+}
+
 inline int launch_ok() { return hipGetLastError() == hipSuccess ? 0 : -1; }
 
 } // namespace
@@ -605,6 +820,71 @@ int q3k_argmax(const q3_amax *p, void *stream) {
     int grid = (p->V + 1023) / 1024;
     if (grid > 512) grid = 512;
     hipLaunchKernelGGL(k_argmax, dim3(grid), dim3(256), 0, (hipStream_t)stream, *p);
+    return launch_ok();
+}
+
+// Fused M = 1 matmul (k_fgemv), the instantiations the decoder uses: PRO_NORM + STORE (q/k/v, int8), PRO_QUANT +
+// RESID (o, int8; down, int8 / uniform int4 / NF4), PRO_NORM + SWIGLU (gate/up pairs, int8 / uniform int4 / NF4).
+// E (row elements per thread) is norm_quant_body's for the same K.
+#define Q3_FG_E(PRO, EPI, KIND)                                                                               \
+    do {                                                                                                      \
+        const int e_ = (p->K + FG_WAVES * 64 - 1) / (FG_WAVES * 64);                                          \
+        const dim3 gr_(grid), bl_(FG_WAVES * 64);                                                             \
+        if (e_ <= 1) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 1>), gr_, bl_, 0, s_, *p);                    \
+        else if (e_ <= 2) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 2>), gr_, bl_, 0, s_, *p);               \
+        else if (e_ <= 3) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 3>), gr_, bl_, 0, s_, *p);               \
+        else if (e_ <= 4) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 4>), gr_, bl_, 0, s_, *p);               \
+        else if (e_ <= 6) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 6>), gr_, bl_, 0, s_, *p);               \
+        else if (e_ <= 8) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 8>), gr_, bl_, 0, s_, *p);               \
+        else if (e_ <= 12) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 12>), gr_, bl_, 0, s_, *p);             \
+        else if (e_ <= 16) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 16>), gr_, bl_, 0, s_, *p);             \
+        else return -2;                                                                                       \
+    } while (0)
+
+int q3k_fgemv(const q3_fg *p, void *stream) {
+    const hipStream_t s_ = (hipStream_t)stream;
+    if (p->kind < 0 || p->kind > 2 || p->epi < Q3_EPI_STORE || p->epi > Q3_EPI_SWIGLU) return -2;
+    const int kpb = p->kind == 0 ? 64 : 128;
+    const int pro = p->nw ? Q3_PRO_NORM : Q3_PRO_QUANT;
+    const int nt = p->epi == Q3_EPI_SWIGLU ? 2 : p->epi == Q3_EPI_RESID ? 1 : p->nt;
+    if (p->K < 32 || p->KB < 1 || (long)p->KB * kpb < p->K || (long)p->KB * kpb > Q3_FG_KMAX || nt < 1 || nt > 3 ||
+        !p->row)
+        return -2;
+    int grid = 0;
+    for (int i = 0; i < nt; i++) {
+        if (!p->B[i] || p->nb[i] < 1) return -2;
+        grid += p->nb[i];
+    }
+    switch (p->epi) {
+    case Q3_EPI_STORE:
+        for (int i = 0; i < nt; i++)
+            if (!p->C[i]) return -2;
+        if (pro != Q3_PRO_NORM || p->kind != 0) return -2;
+        Q3_FG_E(Q3_PRO_NORM, Q3_EPI_STORE, 0);
+        break;
+    case Q3_EPI_RESID:
+        if (pro != Q3_PRO_QUANT || !p->x || !p->ws0) return -2;
+        if (p->kind == 0) Q3_FG_E(Q3_PRO_QUANT, Q3_EPI_RESID, 0);
+        else if (p->kind == 1) Q3_FG_E(Q3_PRO_QUANT, Q3_EPI_RESID, 1);
+        else Q3_FG_E(Q3_PRO_QUANT, Q3_EPI_RESID, 2);
+        break;
+    default:
+        if (pro != Q3_PRO_NORM || !p->y || !p->ws0 || !p->ws1 || p->nb[1] != p->nb[0]) return -2;
+        grid = p->nb[0];
+        if (p->kind == 0) Q3_FG_E(Q3_PRO_NORM, Q3_EPI_SWIGLU, 0);
+        else if (p->kind == 1) Q3_FG_E(Q3_PRO_NORM, Q3_EPI_SWIGLU, 1);
+        else Q3_FG_E(Q3_PRO_NORM, Q3_EPI_SWIGLU, 2);
+        break;
+    }
+    return launch_ok();
+}
+#undef Q3_FG_E
+
+int q3k_attn_combine(const q3_comb *p, void *stream) {
+    if (p->NH < 1 || p->HD < 64 || p->HD > Q3_MAX_HD || p->HD % 64 || p->S < 1 || p->S > Q3_MAX_S || !p->part ||
+        !p->out)
+        return -2;
+    hipLaunchKernelGGL(k_attn_combine, dim3(p->NH), dim3(p->HD), 0, (hipStream_t)stream, *p);
     return launch_ok();
 }
 

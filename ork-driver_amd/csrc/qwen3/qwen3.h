@@ -25,7 +25,7 @@ typedef struct q3_cfg {
     int layers, hidden, heads, kv_heads, head_dim, ffn, vocab;
     int max_ctx;       /* KV-cache positions (prefill + decode) */
     int max_rows;      /* largest prefill batch */
-    int ffn_nf4;       /* 1: gate/up/down packed as NF4 w4a8 (ork_i4a8_mm_pack with ORK_NF4) */
+    int ffn_nf4;       /* 1: gate/up/down packed as NF4 w4a8 (ork_i4a8_mm_pack with ORK_NF4); 2: uniform int4 w4a8 */
     float rope_theta;  /* Qwen3: 1e6 */
     float eps;         /* Qwen3: 1e-6 */
 } q3_cfg;
@@ -53,6 +53,11 @@ int       q3_prefill(q3_model *m, const int *tokens, int n);
 /* Greedy decode: feed the last sampled token, sample the next; `steps` times. graph = 1 replays one
  * captured HIP graph per step. Returns after the last step has finished. */
 int       q3_decode(q3_model *m, int steps, int graph);
+/* Decode through the fused M = 1 kernels (on = 1, the default) or the unfused operator sequence (0); both give
+ * identical logits and tokens. The fused form needs every weight resident on the device with K-blocks that fit
+ * its LDS row (8 KiB); q3_decode_fused says whether the current weights take it. */
+int       q3_set_fused(q3_model *m, int on);
+int       q3_decode_fused(const q3_model *m);
 /* Tokens at positions 0..n-1 and the one sampled last (out[n] when n == the position count). */
 int       q3_tokens(q3_model *m, int *out, int n);
 /* Number of positions filled (prefill + decode inputs). */

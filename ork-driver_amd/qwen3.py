@@ -45,6 +45,8 @@ API = {
     "q3_positions": (C.c_int, [_P]),
     "q3_last_logits": (C.c_int, [_P, _P]),
     "q3_weight_bytes": (C.c_double, [_P]),
+    "q3_set_fused": (C.c_int, [_P, C.c_int]),
+    "q3_decode_fused": (C.c_int, [_P]),
 }
 
 _lib = None
@@ -121,6 +123,14 @@ class Model:
 
     def decode(self, steps, graph=True):
         return lib().q3_decode(self.h, steps, int(graph))
+
+    def set_fused(self, on):
+        """Decode through the fused M = 1 kernels (default) or the unfused operator sequence."""
+        return lib().q3_set_fused(self.h, int(on))
+
+    def decode_fused(self):
+        """Whether decode steps take the fused kernels with the current weights."""
+        return bool(lib().q3_decode_fused(self.h))
 
     def positions(self):
         return lib().q3_positions(self.h)

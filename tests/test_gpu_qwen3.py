@@ -7,7 +7,9 @@ the GPU's tokens. Checked at every step:
     output; int8 activation codes may flip at rounding boundaries between two float32 evaluation orders);
   - the GPU's sampled token is the first maximum of its own logits and a near-maximum of the reference's;
   - the token log holds the prompt and every sampled token.
-Graph-replayed and eagerly launched decode steps must give identical tokens and bit-identical logits.
+Graph-replayed and eagerly launched decode steps must give identical tokens and bit-identical logits, and so
+must the fused decode kernels (k_fgemv, k_attn_combine: 6 launches per layer) and the unfused operator sequence
+(9), which do the same float operations in the same order.
 """
 import numpy as np
 import pytest
@@ -79,6 +81,7 @@ def test_decoder_parity(npu, case):
     ref = R.Qwen3Ref(cfg, W, Nm, ffn_nf4=case["nf4"])
     m = _model(npu, cfg, W, Nm)
     try:
+        assert m.decode_fused()  # the decode steps below take the fused kernels
         n = case["n"]
         prompt = np.random.default_rng(23).integers(0, cfg.vocab, n).astype(np.int32)
         assert m.prefill(prompt) == 0
@@ -111,6 +114,35 @@ def test_graph_replay_equals_eager(npu):
             assert m.prefill(prompt) == 0
             assert m.decode(90, graph=graph) == 0  # crosses two 64-key chunk boundaries
             out.append((m.tokens(), m.last_logits()))
+        finally:
+            m.close()
+    assert np.array_equal(out[0][0], out[1][0])
+    assert np.array_equal(out[0][1], out[1][1])
+
+
+@pytest.mark.parametrize("case", [
+    dict(name="int8", over={}, nf4=0, n=20, steps=40),
+    dict(name="nf4-gqa4-hd64", over=dict(heads=8, kv_heads=2, head_dim=64), nf4=1, n=9, steps=30),
+    dict(name="uniform-int4-mha", over=dict(heads=2, kv_heads=2), nf4=2, n=1, steps=36),
+    dict(name="qwen3-widths-2-layers", over=dict(Q.QWEN3_1P7B, layers=2, vocab=4096), nf4=1, n=12, steps=20),
+])
+def test_fused_decode_equals_unfused(npu, case):
+    _say("fused vs unfused", case["name"])
+    cfg = _cfg(nf4=case["nf4"], **case["over"])
+    W, Nm = _weights(cfg, 53, std=0.05 if cfg.hidden < 1024 else 0.02)
+    prompt = np.random.default_rng(59).integers(0, cfg.vocab, case["n"]).astype(np.int32)
+    out = []
+    for fused in (False, True):
+        m = _model(npu, cfg, W, Nm)
+        try:
+            assert m.set_fused(fused) == 0
+            assert m.decode_fused() == fused
+            assert m.prefill(prompt) == 0
+            lg = []
+            for s in range(case["steps"]):
+                assert m.decode(1, graph=(s % 2 == 1)) == 0
+                lg.append(m.last_logits())
+            out.append((m.tokens(), np.stack(lg)))
         finally:
             m.close()
     assert np.array_equal(out[0][0], out[1][0])
