@@ -527,9 +527,12 @@ __global__ void k_argmax(q3_amax p) {
 // k-group l / 16). Around that GEMV:
 //   prologue: the int8 row, built in LDS by every workgroup: PRO_NORM = RMSNorm of the residual row then the
 //     per-row quant (norm_quant_body's operations with its 512-thread element mapping, so the sum of squares is
-//     rounded identically); PRO_QUANT = the per-row quant of a float row (quant_regs' operations; the absmax is
-//     order-independent). The weight blocks of each wave are loaded before the prologue, which hides their
-//     memory latency behind it.
+//     rounded identically: elements past K add exact zeros, so any E >= K / 512 gives the same sums);
+//     PRO_QUANT = the per-row quant of a float row (quant_regs' operations; the absmax is order-independent).
+//     Each wave's weight blocks (PRE >= its share, no more: a load past the share would fetch another wave's
+//     bytes again) are loaded once the row has arrived: their latency hides behind the reductions and the
+//     quant, and the row's own loads do not queue behind them in the CU's memory pipeline (measured: issuing
+//     them first delayed the row by 1-2 us).
 //   epilogue on each column's int32 sum: STORE; RESID x[n] += (c * a_scale) * ws[n] (the residual add that
 //     k_norm_quant_acc would do next); SWIGLU y[n] = silu(g) * u from the gate and up sums (k_swiglu_quant's
 //     operations).
@@ -573,10 +576,9 @@ __device__ inline int fg_dot(v4i_t raw, const int *__restrict__ a, int acc, cons
     return acc;
 }
 
-constexpr int FG_WAVES = 8;  // 512 threads: norm_quant_body's element mapping
-constexpr int FG_PRE = 8;    // K-blocks per wave and panel loaded ahead of the prologue
+constexpr int FG_WAVES = 8; // 512 threads: norm_quant_body's element mapping
 
-template <int PRO, int EPI, int KIND, int E>
+template <int PRO, int EPI, int KIND, int E, int PRE>
 __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
     __shared__ __align__(16) int8_t arow[Q3_FG_KMAX];
     __shared__ __align__(16) float red[16];
@@ -587,7 +589,7 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = p.K, KB = p.KB;
 
-    // ---- this workgroup's panel(s) and this wave's K-blocks (loads clamped, branch-free)
+    // ---- this workgroup's panel(s) and this wave's K-blocks
     int t = 0, pnl = blockIdx.x;
     if constexpr (!PAIR) {
         while (t < p.nt - 1 && pnl >= p.nb[t]) {
@@ -598,32 +600,39 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
     const int kbw = (KB + FG_WAVES - 1) / FG_WAVES, kb0 = min(wv * kbw, KB), kb1 = min(kb0 + kbw, KB);
     const v4i_t *b0 = (const v4i_t *)p.B[t] + (size_t)pnl * KB * 64 + lane;
     const v4i_t *b1 = PAIR ? (const v4i_t *)p.B[1] + (size_t)pnl * KB * 64 + lane : b0;
-    // the row's loads are issued first: the wait for them then leaves the weight loads in flight
+    // ---- prologue: the int8 row in LDS
     float y[E], nw[E];
     load_row(y, p.row, K);
     if constexpr (PRO == Q3_PRO_NORM) load_row(nw, p.nw, K);
-    v4i_t r0[FG_PRE], r1[FG_PRE];
+    float mx = 0.f, ss = 0.f;
+    if constexpr (PRO == Q3_PRO_NORM) {
 #pragma unroll
-    for (int u = 0; u < FG_PRE; u++) {
-        const size_t o = (size_t)min(kb0 + u, KB - 1) * 64;
+        for (int k = 0; k < E; k++) ss += y[k] * y[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < E; k++)
+            if (threadIdx.x + k * blockDim.x < (unsigned)K) mx = fmaxf(mx, fabsf(y[k]));
+    }
+    // the weight blocks, issued after the first use of the row (which waits for it); clamped to the wave's own
+    // last block, branch-free (a wave without blocks re-reads the panel's last one and discards it)
+    v4i_t r0[PRE], r1[PRE];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < PRE; u++) {
+        const size_t o = (size_t)min(kb0 + u, kb1 - 1) * 64;
         r0[u] = __builtin_nontemporal_load(b0 + o);
         if constexpr (PAIR) r1[u] = __builtin_nontemporal_load(b1 + o);
     }
-
-    // ---- prologue: the int8 row in LDS
-    float mx = 0.f;
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (PRO == Q3_PRO_NORM) {
-        float ss = 0.f;
-#pragma unroll
-        for (int k = 0; k < E; k++) ss += y[k] * y[k];
         ss = block_sum(ss, red);
         const float r = 1.0f / sqrtf(ss / (float)K + p.eps);
 #pragma unroll
         for (int k = 0; k < E; k++) y[k] = (y[k] * r) * nw[k];
-    }
 #pragma unroll
-    for (int k = 0; k < E; k++)
-        if (threadIdx.x + k * blockDim.x < (unsigned)K) mx = fmaxf(mx, fabsf(y[k]));
+        for (int k = 0; k < E; k++)
+            if (threadIdx.x + k * blockDim.x < (unsigned)K) mx = fmaxf(mx, fabsf(y[k]));
+    }
     mx = block_max(mx, redq);
     const float as = mx > 0.f ? mx / 127.0f : 1.0f;
     {
@@ -648,14 +657,14 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
     const int aoff = (lane >> 4) * (KPB / 4);
     int acc0 = 0, acc1 = 0;
 #pragma unroll
-    for (int u = 0; u < FG_PRE; u++) {
+    for (int u = 0; u < PRE; u++) {
         if (kb0 + u < kb1) {
             const int *a = (const int *)(arow + (kb0 + u) * KPB + aoff);
             acc0 = fg_dot<KIND>(r0[u], a, acc0, L);
             if constexpr (PAIR) acc1 = fg_dot<KIND>(r1[u], a, acc1, L);
         }
     }
-    for (int kb = kb0 + FG_PRE; kb < kb1; kb++) {
+    for (int kb = kb0 + PRE; kb < kb1; kb++) {
         const v4i_t s0 = __builtin_nontemporal_load(b0 + (size_t)kb * 64);
         v4i_t s1 = s0;
         if constexpr (PAIR) s1 = __builtin_nontemporal_load(b1 + (size_t)kb * 64);
@@ -737,6 +746,25 @@ __global__ __launch_bounds__(Q3_MAX_HD) void k_attn_combine(q3_comb p) {
 }
 
 inline int launch_ok() { return hipGetLastError() == hipSuccess ? 0 : -1; }
+
+// Fused M = 1 matmul (k_fgemv), the instantiations the decoder uses: PRO_NORM + STORE (q/k/v, int8), PRO_QUANT +
+// RESID (o, int8; down, int8 / uniform int4 / NF4), PRO_NORM + SWIGLU (gate/up pairs, int8 / uniform int4 / NF4).
+// E: row elements per thread, a bound of K / 512; PRE: the weight blocks per wave, a bound of its share.
+template <int PRO, int EPI, int KIND, int E>
+void fg_launch_pre(const q3_fg *p, int grid, int pre, hipStream_t s) {
+    if (pre <= 4) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 4>), dim3(grid), dim3(FG_WAVES * 64), 0, s, *p);
+    else if (pre <= 8) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 8>), dim3(grid), dim3(FG_WAVES * 64), 0, s, *p);
+    else hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 16>), dim3(grid), dim3(FG_WAVES * 64), 0, s, *p);
+}
+template <int PRO, int EPI, int KIND> int fg_launch(const q3_fg *p, int grid, hipStream_t s) {
+    const int e = (p->K + FG_WAVES * 64 - 1) / (FG_WAVES * 64), pre = (p->KB + FG_WAVES - 1) / FG_WAVES;
+    if (e <= 4) fg_launch_pre<PRO, EPI, KIND, 4>(p, grid, pre, s);
+    else if (e <= 8) fg_launch_pre<PRO, EPI, KIND, 8>(p, grid, pre, s);
+    else if (e <= 12) fg_launch_pre<PRO, EPI, KIND, 12>(p, grid, pre, s);
+    else if (e <= 16) fg_launch_pre<PRO, EPI, KIND, 16>(p, grid, pre, s);
+    else return -2;
+    return 0;
+}
 
 } // namespace
 
@@ -823,24 +851,6 @@ int q3k_argmax(const q3_amax *p, void *stream) {
     return launch_ok();
 }
 
-// Fused M = 1 matmul (k_fgemv), the instantiations the decoder uses: PRO_NORM + STORE (q/k/v, int8), PRO_QUANT +
-// RESID (o, int8; down, int8 / uniform int4 / NF4), PRO_NORM + SWIGLU (gate/up pairs, int8 / uniform int4 / NF4).
-// E (row elements per thread) is norm_quant_body's for the same K.
-#define Q3_FG_E(PRO, EPI, KIND)                                                                               \
-    do {                                                                                                      \
-        const int e_ = (p->K + FG_WAVES * 64 - 1) / (FG_WAVES * 64);                                          \
-        const dim3 gr_(grid), bl_(FG_WAVES * 64);                                                             \
-        if (e_ <= 1) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 1>), gr_, bl_, 0, s_, *p);                    \
-        else if (e_ <= 2) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 2>), gr_, bl_, 0, s_, *p);               \
-        else if (e_ <= 3) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 3>), gr_, bl_, 0, s_, *p);               \
-        else if (e_ <= 4) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 4>), gr_, bl_, 0, s_, *p);               \
-        else if (e_ <= 6) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 6>), gr_, bl_, 0, s_, *p);               \
-        else if (e_ <= 8) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 8>), gr_, bl_, 0, s_, *p);               \
-        else if (e_ <= 12) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 12>), gr_, bl_, 0, s_, *p);             \
-        else if (e_ <= 16) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, 16>), gr_, bl_, 0, s_, *p);             \
-        else return -2;                                                                                       \
-    } while (0)
-
 int q3k_fgemv(const q3_fg *p, void *stream) {
     const hipStream_t s_ = (hipStream_t)stream;
     if (p->kind < 0 || p->kind > 2 || p->epi < Q3_EPI_STORE || p->epi > Q3_EPI_SWIGLU) return -2;
@@ -855,30 +865,30 @@ int q3k_fgemv(const q3_fg *p, void *stream) {
         if (!p->B[i] || p->nb[i] < 1) return -2;
         grid += p->nb[i];
     }
+    int rc = -2;
     switch (p->epi) {
     case Q3_EPI_STORE:
         for (int i = 0; i < nt; i++)
             if (!p->C[i]) return -2;
         if (pro != Q3_PRO_NORM || p->kind != 0) return -2;
-        Q3_FG_E(Q3_PRO_NORM, Q3_EPI_STORE, 0);
+        rc = fg_launch<Q3_PRO_NORM, Q3_EPI_STORE, 0>(p, grid, s_);
         break;
     case Q3_EPI_RESID:
         if (pro != Q3_PRO_QUANT || !p->x || !p->ws0) return -2;
-        if (p->kind == 0) Q3_FG_E(Q3_PRO_QUANT, Q3_EPI_RESID, 0);
-        else if (p->kind == 1) Q3_FG_E(Q3_PRO_QUANT, Q3_EPI_RESID, 1);
-        else Q3_FG_E(Q3_PRO_QUANT, Q3_EPI_RESID, 2);
+        if (p->kind == 0) rc = fg_launch<Q3_PRO_QUANT, Q3_EPI_RESID, 0>(p, grid, s_);
+        else if (p->kind == 1) rc = fg_launch<Q3_PRO_QUANT, Q3_EPI_RESID, 1>(p, grid, s_);
+        else rc = fg_launch<Q3_PRO_QUANT, Q3_EPI_RESID, 2>(p, grid, s_);
         break;
     default:
         if (pro != Q3_PRO_NORM || !p->y || !p->ws0 || !p->ws1 || p->nb[1] != p->nb[0]) return -2;
         grid = p->nb[0];
-        if (p->kind == 0) Q3_FG_E(Q3_PRO_NORM, Q3_EPI_SWIGLU, 0);
-        else if (p->kind == 1) Q3_FG_E(Q3_PRO_NORM, Q3_EPI_SWIGLU, 1);
-        else Q3_FG_E(Q3_PRO_NORM, Q3_EPI_SWIGLU, 2);
+        if (p->kind == 0) rc = fg_launch<Q3_PRO_NORM, Q3_EPI_SWIGLU, 0>(p, grid, s_);
+        else if (p->kind == 1) rc = fg_launch<Q3_PRO_NORM, Q3_EPI_SWIGLU, 1>(p, grid, s_);
+        else rc = fg_launch<Q3_PRO_NORM, Q3_EPI_SWIGLU, 2>(p, grid, s_);
         break;
     }
-    return launch_ok();
+    return rc ? rc : launch_ok();
 }
-#undef Q3_FG_E
 
 int q3k_attn_combine(const q3_comb *p, void *stream) {
     if (p->NH < 1 || p->HD < 64 || p->HD > Q3_MAX_HD || p->HD % 64 || p->S < 1 || p->S > Q3_MAX_S || !p->part ||
