@@ -480,13 +480,16 @@ template <int VM> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Waves across a tile's block columns: all of them up to 4, else 4 when they divide evenly, else 2.
+constexpr int t2_wn(int nb) { return nb < 4 ? nb : (nb % 4 == 0 ? 4 : 2); }
+
 template <int KIND, int BM, int BN, int KS, bool XGW = false> struct T2 {
     using T = KT<KIND>;
     static constexpr int MB = BM / 16, NB = BN / 16, NW = 16;
-    // 16 waves: WM x WN over the tile's 16 x 16 blocks and, on tiles of fewer than 16 blocks (32- and 16-row tiles),
-    // WK groups that split each stage's K-blocks; their partial tiles are summed through LDS after the loop, in
-    // group order (deterministic for fp16)
-    static constexpr int WM = XGW ? 2 : (MB < 4 ? MB : 4), WN = NB < 4 ? NB : 4, WK = NW / (WM * WN);
+    // 16 waves: WM x WN over the tile's 16 x 16 blocks and, on tiles of fewer than 16 blocks (32- and 16-row tiles)
+    // or whose 6 block columns take 2 waves (128 x 96: 32 x 48 of C per wave), WK groups that split each stage's
+    // K-blocks; their partial tiles are summed through LDS after the loop, in group order (deterministic for fp16)
+    static constexpr int WM = XGW ? 2 : (MB < 4 ? MB : 4), WN = t2_wn(NB), WK = NW / (WM * WN);
     static constexpr int MTW = MB / WM, NTW = NB / WN, KPW = KS / WK; // blocks and K-blocks per wave
     static constexpr int NIA = MB * KS * T::STEPS, NIB = NB * KS, NI = NIA + NIB;  // loads per stage
     static constexpr int IPW = (NI + NW - 1) / NW;                               // per wave
@@ -1138,7 +1141,7 @@ int launch_tiled_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
 // K-blocks per stage of k_tiled2: ~128 bytes of each activation row per stage for small tiles, ~64 for the
 // 256 x 256 tile (whose ring would not fit otherwise); at least one per K group of waves.
 template <int KIND, int BM, int BN, bool XGW = false> constexpr int t2_ks() {
-    constexpr int mb = XGW ? 2 : (BM / 16 < 4 ? BM / 16 : 4), nb = BN / 16 < 4 ? BN / 16 : 4, wk = 16 / (mb * nb);
+    constexpr int mb = XGW ? 2 : (BM / 16 < 4 ? BM / 16 : 4), nb = t2_wn(BN / 16), wk = 16 / (mb * nb);
     constexpr int base = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 1 : (BM * BN >= 65536 ? 1 : 2);
     return base > wk ? base : wk;
 }
@@ -1175,6 +1178,7 @@ int launch_tiled(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     if (q->algo == ORKH_ALGO_TILED2) {
         if (q->bm == 256 && q->bn == 256) return launch_tiled2_v<KIND, 256, 256>(p, q, s);
         if (q->bm == 128 && q->bn == 128) return launch_tiled2_v<KIND, 128, 128>(p, q, s);
+        if (q->bm == 128 && q->bn == 96) return launch_tiled2_v<KIND, 128, 96>(p, q, s);
         if (q->bm == 64 && q->bn == 192) return launch_tiled2_v<KIND, 64, 192>(p, q, s);
         if (q->bm == 64 && q->bn == 64) return launch_tiled2_v<KIND, 64, 64>(p, q, s);
         if (q->bm == 32 && q->bn == 64) return launch_tiled2_v<KIND, 32, 64>(p, q, s);
@@ -1335,6 +1339,7 @@ extern "C" int orkh_tiled2_ring_lds(int kind, int bm, int bn) {
     if (bm == 64 && bn == 64) return (int)T2<KIND, 64, 64, t2_ks<KIND, 64, 64>()>::LDS;                       \
     if (bm == 64 && bn == 192) return (int)T2<KIND, 64, 192, t2_ks<KIND, 64, 192>()>::LDS;                    \
     if (bm == 128 && bn == 128) return (int)T2<KIND, 128, 128, t2_ks<KIND, 128, 128>()>::LDS;                 \
+    if (bm == 128 && bn == 96) return (int)T2<KIND, 128, 96, t2_ks<KIND, 128, 96>()>::LDS;                    \
     if (bm == 256 && bn == 256) return (int)T2<KIND, 256, 256, t2_ks<KIND, 256, 256>()>::LDS;                 \
     return -1;
     switch (kind) {

@@ -484,12 +484,13 @@ def test_run_errors(npu):
     assert L.ork_io_failures() == 0
 
 
-@pytest.mark.parametrize("tile", ["256x256", "128x128", "64x192", "64x64", "32x64", "32x32", "16x64", "16x32"])
+@pytest.mark.parametrize("tile", ["256x256", "128x128", "128x96", "64x192", "64x64", "32x64", "32x32", "16x64", "16x32"])
 @pytest.mark.parametrize("ks", [1, 3])
 @pytest.mark.parametrize("aline", [0, 1])
 def test_lds_ring_tiles_all_kinds(npu, tile, ks, aline):
-    """The LDS-ring tiled kernel at every tile shape the planner can choose (32- and 16-row tiles split each stage's K-blocks
-    over groups of waves and sum their partial tiles in LDS), unsplit and K-split, with A stages
+    """The LDS-ring tiled kernel at every tile shape the planner can choose (32- and 16-row tiles, and 128x96 whose six
+    block columns take two waves, split each stage's K-blocks over groups of waves and sum their partial tiles in
+    LDS), unsplit and K-split, with A stages
     in fragment order and as whole row lines (ORK_ALINE; 256x256 has 64-byte stage rows and always uses
     fragment order): exact for int8, uniform-int4 and NF4 i4a8 and W4A4, within the fp16 bar (and run-to-run
     identical) for fp16. M, N and K tails: M = 300 and 70 are no tile multiple, N = 224 (14 panels) leaves a
@@ -551,7 +552,7 @@ def _lds_ring_tiles_all_kinds(npu, tile, ks):
     ork.free(w)
 
 
-@pytest.mark.parametrize("tile", ["64x192", "64x64", "32x64", "32x32", "16x64", "16x32"])
+@pytest.mark.parametrize("tile", ["128x96", "64x192", "64x64", "32x64", "32x32", "16x64", "16x32"])
 @pytest.mark.parametrize("M", [1, 5, 17, 48, 64])
 def test_lds_ring_small_m(npu, tile, M):
     """The LDS-ring kernel below one tile height (the planner takes it from M = 24 on wide or long-K
