@@ -483,13 +483,13 @@ template <int VM> __device__ __forceinline__ void wait_vmcnt() {
 // Waves across a tile's block columns: all of them up to 4, else 4 when they divide evenly, else 2.
 constexpr int t2_wn(int nb) { return nb < 4 ? nb : (nb % 4 == 0 ? 4 : 2); }
 
-template <int KIND, int BM, int BN, int KS, bool XGW = false> struct T2 {
+template <int KIND, int BM, int BN, int KS, int XG = 0> struct T2 {
     using T = KT<KIND>;
     static constexpr int MB = BM / 16, NB = BN / 16, NW = 16;
     // 16 waves: WM x WN over the tile's 16 x 16 blocks and, on tiles of fewer than 16 blocks (32- and 16-row tiles)
     // or whose 6 block columns take 2 waves (128 x 96: 32 x 48 of C per wave), WK groups that split each stage's
     // K-blocks; their partial tiles are summed through LDS after the loop, in group order (deterministic for fp16)
-    static constexpr int WM = XGW ? 2 : (MB < 4 ? MB : 4), WN = t2_wn(NB), WK = NW / (WM * WN);
+    static constexpr int WM = XG ? 2 : (MB < 4 ? MB : 4), WN = XG == 2 ? 2 : t2_wn(NB), WK = NW / (WM * WN);
     static constexpr int MTW = MB / WM, NTW = NB / WN, KPW = KS / WK; // blocks and K-blocks per wave
     static constexpr int NIA = MB * KS * T::STEPS, NIB = NB * KS, NI = NIA + NIB;  // loads per stage
     static constexpr int IPW = (NI + NW - 1) / NW;                               // per wave
@@ -513,12 +513,19 @@ template <int KIND, int BM, int BN, int KS, bool XGW = false> struct T2 {
     static_assert(!LINE_OK || NIA * 8 == BM, "line-loaded A: one instruction per 8 rows");
 };
 
-// Wave grid 2 x 4 with 2 K groups instead of 4 x 4 (each B block decoded by two waves instead of four), for the
-// uniform-int4 64 x 192 tile. Measured against 4 x 4 (us): W4A8 K=2048 N=6144 M=512 14.7 -> 13.4, M=256 13.3 ->
-// 12.5; W4A4 M=512 K=N=4096 22.0 -> 19.9. Not kept elsewhere: int8 M=512 64 x 192 13.9 -> 14.7, fp16 M=1024
-// 20.5 -> 21.1, uniform int4 128 x 128 21.9 -> 22.4 (W4A4 M=256), 64 x 64 unchanged.
-template <int KIND, int BM, int BN, int GR> constexpr bool t2_xg() {
-    return GR == 0 && KIND == ORKH_I4U && BM == 64 && BN == 192;
+// Wave grids other than 4 x 4 (grouped runs always keep it):
+// 1: 2 x 4 with 2 K groups (each B block decoded by two waves instead of four), for the uniform-int4 64 x 192
+//    tile. Measured against 4 x 4 (us): W4A8 K=2048 N=6144 M=512 14.7 -> 13.4, M=256 13.3 -> 12.5; W4A4 M=512
+//    K=N=4096 22.0 -> 19.9. Not kept elsewhere: int8 M=512 64 x 192 13.9 -> 14.7, fp16 M=1024 20.5 -> 21.1,
+//    uniform int4 128 x 128 21.9 -> 22.4 (W4A4 M=256), 64 x 64 unchanged.
+// 2: 2 x 2 with 4 K groups (each wave 32 x 32 of C: half the LDS reads per MFMA of a 16 x 16 wave block, each B
+//    block decoded by two waves), for the uniform-int4 64 x 64 tile: W4A4 M=256 K=N=4096 14.76 -> 14.00. Not
+//    kept for fp16 (M=512 K=N=2048 13.98 -> 15.35).
+template <int KIND, int BM, int BN, int GR> constexpr int t2_xg() {
+    if (GR != 0) return 0;
+    if (KIND == ORKH_I4U && BM == 64 && BN == 192) return 1;
+    if (KIND == ORKH_I4U && BM == 64 && BN == 64) return 2;
+    return 0;
 }
 
 // Index (in 16-byte units) within a stage's A image of lane `lane`'s operand of fragment (mb, kbl, st).
@@ -1140,17 +1147,17 @@ int launch_tiled_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
 
 // K-blocks per stage of k_tiled2: ~128 bytes of each activation row per stage for small tiles, ~64 for the
 // 256 x 256 tile (whose ring would not fit otherwise); at least one per K group of waves.
-template <int KIND, int BM, int BN, bool XGW = false> constexpr int t2_ks() {
-    constexpr int mb = XGW ? 2 : (BM / 16 < 4 ? BM / 16 : 4), nb = t2_wn(BN / 16), wk = 16 / (mb * nb);
+template <int KIND, int BM, int BN, int XG = 0> constexpr int t2_ks() {
+    constexpr int mb = XG ? 2 : (BM / 16 < 4 ? BM / 16 : 4), nb = XG == 2 ? 2 : t2_wn(BN / 16), wk = 16 / (mb * nb);
     constexpr int base = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 1 : (BM * BN >= 65536 ? 1 : 2);
     return base > wk ? base : wk;
 }
 
 template <int KIND, int BM, int BN>
 int launch_tiled2_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
-    constexpr bool XGW = t2_xg<KIND, BM, BN, 0>();
-    constexpr int KS = t2_ks<KIND, BM, BN, XGW>();
-    using P = T2<KIND, BM, BN, KS, XGW>;
+    constexpr int XG = t2_xg<KIND, BM, BN, 0>();
+    constexpr int KS = t2_ks<KIND, BM, BN, XG>();
+    using P = T2<KIND, BM, BN, KS, XG>;
     const bool al = q->aline && P::LINE_OK;
     auto kern = al ? k_tiled2<KIND, BM, BN, KS, true> : k_tiled2<KIND, BM, BN, KS, false>;
     static lds_flags attr[2]; // per instantiation: allow more than the default 64 KiB of dynamic LDS

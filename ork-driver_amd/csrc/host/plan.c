@@ -176,8 +176,10 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
 static int aline_rule(const ork_npu *c, int rkind, const orkh_plan *q) {
     /* the kernel has the line layout only where a stage row is one 128-byte line: K-blocks per stage as
      * k_tiled2's t2_ks (1 for int4 kinds, 1 for 256 x 256, else 2; at least the tile's K groups of waves) */
-    const int nbt = q->bn / 16, mb = q->bm / 16 < 4 ? q->bm / 16 : 4;
-    const int nb = nbt < 4 ? nbt : (nbt % 4 == 0 ? 4 : 2), wk = 16 / (mb * nb); /* k_tiled2's wave grid (t2_wn) */
+    /* k_tiled2's wave grid (t2_xg, t2_wn): 2 x 4 on the uniform-int4 64 x 192 tile, 2 x 2 on its 64 x 64 tile */
+    const int xg = (rkind == ORKH_I4U && q->bm == 64) ? (q->bn == 192 ? 1 : q->bn == 64 ? 2 : 0) : 0;
+    const int nbt = q->bn / 16, mb = xg ? 2 : (q->bm / 16 < 4 ? q->bm / 16 : 4);
+    const int nb = xg == 2 ? 2 : (nbt < 4 ? nbt : (nbt % 4 == 0 ? 4 : 2)), wk = 16 / (mb * nb);
     const int base = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 1 : (q->bm * q->bn >= 65536 ? 1 : 2);
     const int ks = base > wk ? base : wk;
     if (ks * a_bytes_per_kb(rkind) != 128) return 0;
