@@ -77,8 +77,10 @@ class Linear:
     """A packed linear as the library stores it: codes [K][N] and per-channel scales [N]."""
 
     def __init__(self, w_nk, nf4=False):
+        """nf4: False (int8, ork_i8_mm_pack_f32), True or 1 (NF4 w4a8) or 2 (uniform int4 w4a8), as the harness's
+        ffn_nf4 (both w4a8 kinds through ork_i4a8_mm_pack, src/npu/i4/pack.c)."""
         if nf4:
-            bs, _, codes = O.pack_i4a8(w_nk, nf4=True)
+            bs, _, codes = O.pack_i4a8(w_nk, nf4=(nf4 != 2))
         else:
             codes, bs = O.pack_i8_f32(w_nk)
         self.codes, self.ws = codes, bs
@@ -94,7 +96,7 @@ class Qwen3Ref:
 
     def __init__(self, cfg, weights, norms, ffn_nf4=False):
         self.c = cfg
-        self.lin = {k: Linear(w, nf4=ffn_nf4 and k[0] >= 0 and k[1] in (4, 5, 6)) for k, w in weights.items()}
+        self.lin = {k: Linear(w, nf4=ffn_nf4 if (k[0] >= 0 and k[1] in (4, 5, 6)) else False) for k, w in weights.items()}
         self.emb = weights[(-1, 0)].astype(np.float16).astype(F32)
         self.norms = {k: np.asarray(v, F32) for k, v in norms.items()}
         self.cos, self.sin = rope_tables(cfg.max_ctx, cfg.head_dim, cfg.rope_theta)

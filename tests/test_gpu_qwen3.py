@@ -73,6 +73,7 @@ def _check_sample(m, logits, ref_logits, what):
     dict(name="gqa2-hd128", over={}, nf4=False, n=70, steps=12),
     dict(name="gqa4-hd64-nf4", over=dict(heads=8, kv_heads=2, head_dim=64), nf4=True, n=33, steps=10),
     dict(name="mha-hd128", over=dict(heads=2, kv_heads=2), nf4=False, n=1, steps=70),
+    dict(name="gqa2-uniform-int4", over={}, nf4=2, n=24, steps=12),
 ])
 def test_decoder_parity(npu, case):
     _say(case["name"])
