@@ -603,7 +603,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the resident-weight matmul has no collective; "
-              "N-sharding across GPUs is described in DESIGN.md but not run). Use --gpus 1.", file=sys.stderr)
+              "N-sharding across GPUs is designed but not run in this build). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import ork
