@@ -435,7 +435,8 @@ static int pass(q3_model *m, int M, int decode) {
                                  {Ly->l[Q3_WV].w, M, m->a8x, m->cv, 0}};
         CK(ork_i8_mm_run_chain(m->ctx, 3, qkv));
         q3_att at = {.M = M, .NH = NH, .NKV = NKV, .HD = HD, .S = m->S, .max_ctx = c->max_ctx, .q = m->q,
-                     .kc = Ly->kc, .vc = Ly->vc, .st = m->st, .scale = 1.0f / sqrtf((float)HD), .part = m->part};
+                     .kc = Ly->kc, .vc = Ly->vc, .st = m->st, .scale = 1.0f / sqrtf((float)HD), .part = m->part,
+                     .rows = m->fused};
         if (M == 1) { /* one row: attention does the q/k/v post-processing itself */
             at.cq = m->cq;
             at.ck = m->ck;

@@ -60,6 +60,7 @@ typedef struct q3_att { /* grid (NKV * query-head sub-groups, S, M): Q3_CHUNK-ke
     const int *st;
     float scale;
     float *part; /* [M][NH][S][HD + 2]: P.V, then max and sum */
+    int rows;    /* unfused form: 1 = one workgroup per block of rows (k_attn_rows), 0 = per row; same partials */
     /* fused form (M = 1, cq != NULL): the q/k/v matmul results and what k_qkv_post takes */
     const int32_t *cq, *ck, *cv;
     const float *as, *wsq, *wsk, *wsv, *qn, *kn;

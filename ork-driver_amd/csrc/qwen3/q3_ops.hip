@@ -22,6 +22,7 @@
 
 namespace {
 
+
 // Wave-wide sum / max in every lane, on the cross-lane paths of the VALU: DPP quad_perm swaps (lanes
 // l ^ 1, l ^ 2), DPP row_half_mirror and row_mirror (the other quad of an 8-lane half, the other half of a
 // 16-lane row), then v_permlane16_swap / v_permlane32_swap (l ^ 16, l ^ 32). Every step combines the same two
@@ -418,6 +419,116 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
     }
 }
 
+// k_attn_rows: the prefill form of k_attn_part (M > 1 rows, rotated queries in p.q): one workgroup per (kv head's
+// query-head group, key chunk, block of HD / Q3_CHUNK rows). The chunk's keys go to LDS and its values to registers
+// once and serve every row of the block, every thread scoring one (row, head, key), instead of one workgroup
+// reloading the chunk for each row. (Blocks of 16 rows, several such passes per workgroup, measured slower: the
+// scoring is per-thread latency, and 4x fewer workgroups left most CUs idle.) Each row's partials are computed with
+// k_attn_part's operations in its order (the score sums, the 32-lane max and sum, the P.V accumulation), and a row
+// with no key in the chunk gets k_attn_part's empty partial, so the partials are bit-identical to it.
+template <int GW>
+__global__ __launch_bounds__(256) void k_attn_rows(q3_att p) {
+    extern __shared__ float sm[];
+    const int HD = p.HD, G = p.NH / p.NKV, KVD = p.NKV * HD, QD = p.NH * HD;
+    const int nsub = G / GW, sub = blockIdx.x % nsub;
+    const int kvh = blockIdx.x / nsub, h0 = kvh * G + sub * GW; // first query head
+    const int s = blockIdx.y, tid = threadIdx.x;
+    const int g = tid / HD, d = tid - g * HD;
+    const int RR = HD / Q3_CHUNK; // rows per workgroup: GW * Q3_CHUNK * RR threads score them together
+    const int t0 = blockIdx.z * RR, t1 = min(t0 + RR, p.M); // rows t0 .. t1 - 1
+    const int j0 = s * Q3_CHUNK;
+    const int nmax = min(Q3_CHUNK, min(p.st[0] + t1, p.max_ctx) - j0); // keys of the block's last row
+    if (nmax <= 0) { // no row of the block reaches this chunk
+        for (int t = t0; t < t1; t++) {
+            float *out = p.part + (((size_t)t * p.NH + h0 + g) * p.S + s) * (HD + 2);
+            out[d] = 0.f;
+            if (d == 0) {
+                out[HD] = -INFINITY;
+                out[HD + 1] = 0.f;
+            }
+        }
+        return;
+    }
+    const int KS = HD + 4; // LDS row stride: 16-byte rows, 8 consecutive lanes of a float4 read hit distinct banks
+    float *Ks = sm;
+    float *qs = Ks + Q3_CHUNK * KS; // [RR][GW][HD]
+    float *P = qs + RR * GW * HD;   // [RR][GW][Q3_CHUNK]
+    float *ml = P + RR * GW * Q3_CHUNK; // [RR][GW][2]
+    const float *__restrict__ kb = p.kc + (size_t)j0 * KVD + kvh * HD;
+    const float *__restrict__ vb = p.vc + (size_t)j0 * KVD + kvh * HD + d;
+    float vv[Q3_CHUNK];
+#pragma unroll
+    for (int j = 0; j < Q3_CHUNK; j++) vv[j] = vb[(size_t)min(j, nmax - 1) * KVD];
+    const int HD4 = HD >> 2;
+    constexpr int KR = Q3_CHUNK / 4 / GW;
+    float4 kreg[KR];
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int f = tid + k * blockDim.x, j = f / HD4, c4 = f - j * HD4;
+        kreg[k] = *(const float4 *)(kb + (size_t)min(j, nmax - 1) * KVD + 4 * c4);
+    }
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int f = tid + k * blockDim.x, j = f / HD4, c4 = f - j * HD4;
+        *(float4 *)(Ks + j * KS + 4 * c4) = kreg[k];
+    }
+    for (int r0 = t0; r0 < t1; r0 += RR) {
+        for (int rr = 0; rr < RR; rr++) {
+            const int t = min(r0 + rr, t1 - 1);
+            qs[rr * GW * HD + tid] = p.q[(size_t)t * QD + h0 * HD + tid];
+        }
+        __syncthreads(); // keys (first pass) and this pass's queries
+        {   // scores: thread = (row rr, head gg, key j)
+            const int rr = tid / (GW * Q3_CHUNK), gg = (tid / Q3_CHUNK) % GW, j = tid % Q3_CHUNK;
+            const int t = r0 + rr;
+            const int n = min(Q3_CHUNK, min(p.st[0] + t + 1, p.max_ctx) - j0);
+            const float4 *qr = (const float4 *)(qs + (rr * GW + gg) * HD), *kr = (const float4 *)(Ks + j * KS);
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll 8
+            for (int e = 0; e < HD4; e++) {
+                const float4 qv = qr[e], kv = kr[e];
+                a0 += qv.x * kv.x;
+                a1 += qv.y * kv.y;
+                a2 += qv.z * kv.z;
+                a3 += qv.w * kv.w;
+            }
+            const float sc = j < n ? ((a0 + a1) + (a2 + a3)) * p.scale : -INFINITY;
+            const float m = group_max<Q3_CHUNK>(sc);
+            const float pj = j < n ? expf(sc - m) : 0.f;
+            const float l = group_sum<Q3_CHUNK>(pj);
+            P[(rr * GW + gg) * Q3_CHUNK + j] = pj;
+            if (j == 0) {
+                ml[2 * (rr * GW + gg)] = m;
+                ml[2 * (rr * GW + gg) + 1] = l;
+            }
+        }
+        __syncthreads();
+        for (int rr = 0; rr < RR && r0 + rr < t1; rr++) {
+            const int t = r0 + rr;
+            float *out = p.part + (((size_t)t * p.NH + h0 + g) * p.S + s) * (HD + 2);
+            const int n = min(Q3_CHUNK, min(p.st[0] + t + 1, p.max_ctx) - j0);
+            if (n <= 0) { // k_attn_part's empty partial
+                out[d] = 0.f;
+                if (d == 0) {
+                    out[HD] = -INFINITY;
+                    out[HD + 1] = 0.f;
+                }
+                continue;
+            }
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < Q3_CHUNK; j++) acc += P[(rr * GW + g) * Q3_CHUNK + j] * vv[j];
+            out[d] = acc;
+            if (d == 0) {
+                out[HD] = ml[2 * (rr * GW + g)];
+                out[HD + 1] = ml[2 * (rr * GW + g) + 1];
+            }
+        }
+        __syncthreads(); // this pass's P and queries read before the next pass writes them
+    }
+}
+
+
 // Combine the chunks of every head (log-sum-exp weights), then quantise the row. Each thread's partial
 // sums are loaded before the chunk weights are known, so the kernel pays one round trip to memory.
 template <int E, int MS>
@@ -812,6 +923,17 @@ int q3k_attn_part(const q3_att *p, void *stream) {
     const dim3 grid(p->NKV * (G / GW), p->S, p->M), block(GW * p->HD);
     const hipStream_t st = (hipStream_t)stream;
     const bool fused = p->cq != nullptr;
+    if (!fused && p->rows) { // prefill: the chunk once per block of rows
+        const size_t lr = (size_t)(Q3_CHUNK * (p->HD + 4) + (p->HD / Q3_CHUNK) * GW * (p->HD + Q3_CHUNK + 2)) * 4;
+        const int rr = p->HD / Q3_CHUNK;
+        const dim3 gr(p->NKV * (G / GW), p->S, (p->M + rr - 1) / rr);
+        if (lr > 64 * 1024) return -2;
+        if (GW == 1) hipLaunchKernelGGL((k_attn_rows<1>), gr, block, lr, st, *p);
+        else if (GW == 2) hipLaunchKernelGGL((k_attn_rows<2>), gr, block, lr, st, *p);
+        else if (GW == 4) hipLaunchKernelGGL((k_attn_rows<4>), gr, block, lr, st, *p);
+        else return -2;
+        return launch_ok();
+    }
     if (GW == 1) {
         if (fused) hipLaunchKernelGGL((k_attn_part<1, true>), grid, block, lds, st, *p);
         else hipLaunchKernelGGL((k_attn_part<1, false>), grid, block, lds, st, *p);

@@ -53,8 +53,8 @@ int       q3_prefill(q3_model *m, const int *tokens, int n);
 /* Greedy decode: feed the last sampled token, sample the next; `steps` times. graph = 1 replays one
  * captured HIP graph per step. Returns after the last step has finished. */
 int       q3_decode(q3_model *m, int steps, int graph);
-/* Decode through the fused M = 1 kernels (on = 1, the default) or the unfused operator sequence (0); both give
- * identical logits and tokens. The fused form needs every weight resident on the device with K-blocks that fit
+/* Decode through the fused M = 1 kernels and prefill attention by blocks of rows (on = 1, the default), or the
+ * unfused operator sequence and row-by-row prefill attention (0); both give identical logits and tokens. The fused form needs every weight resident on the device with K-blocks that fit
  * its LDS row (8 KiB); q3_decode_fused says whether the current weights take it. */
 int       q3_set_fused(q3_model *m, int on);
 int       q3_decode_fused(const q3_model *m);

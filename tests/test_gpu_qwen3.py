@@ -9,7 +9,8 @@ the GPU's tokens. Checked at every step:
   - the token log holds the prompt and every sampled token.
 Graph-replayed and eagerly launched decode steps must give identical tokens and bit-identical logits, and so
 must the fused decode kernels (k_fgemv, k_attn_combine: 6 launches per layer) and the unfused operator sequence
-(9), which do the same float operations in the same order.
+(9), which do the same float operations in the same order; likewise prefill attention by blocks of rows
+(k_attn_rows) and row by row.
 """
 import numpy as np
 import pytest
@@ -139,7 +140,7 @@ def test_fused_decode_equals_unfused(npu, case):
             assert m.set_fused(fused) == 0
             assert m.decode_fused() == fused
             assert m.prefill(prompt) == 0
-            lg = []
+            lg = [m.last_logits()]  # prefill: attention by blocks of rows (fused) or row by row
             for s in range(case["steps"]):
                 assert m.decode(1, graph=(s % 2 == 1)) == 0
                 lg.append(m.last_logits())
