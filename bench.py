@@ -205,7 +205,7 @@ def cpu_rows_baseline(fn_rows, M, nbytes, ops, bound, kind, what, budget_s):
             "sample": f"{n} calls of {r} row(s): {what}, 1 thread, {dt * 1e3:.2f} ms/call{scaled}; host {cpu_model()}"}
 
 
-def sweep_configs(npu, hip, L, ws_c1, dA, dC, codes1, A512, cpu_s):
+def sweep_configs(npu, hip, L, ws_c1, dA, dC, codes1, A512, cpu_s, only=None):
     """BASELINE configs 1-4 at their stated shapes, measured like the headline (one HIP graph of
     rotating resident weights, >= 2x the 256 MB MALL, A and C in HBM): throughput and roofline fraction
     per config. Each result is spot-checked against the oracle on a few rows. With cpu_s > 0 each config
@@ -217,6 +217,10 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC, codes1, A512, cpu_s):
 
     rng = np.random.default_rng(0x6F726B00 + (9 << 8))
     out = []
+
+    def want(name):
+        """Sections to run (profiling runs select some); the grouped section reuses config 4's operands."""
+        return only is None or name in only or (name == "c4" and "grouped" in only)
     have_ref = O.ref_available()
     gemm = O.ref_gemm_i32 if have_ref else O.gemm_i32
     gkind = "reference" if have_ref else "port"
@@ -244,133 +248,140 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC, codes1, A512, cpu_s):
     def steps_for(ms_guess):
         return max(64, min(2400, int(400.0 / max(ms_guess * 1e3, 1.0))))
 
-    # ---- config 1, M=16 (the headline weights)
-    g, _ = measure(npu, hip, ws_c1, 16, dA, dC, 960, 48)
-    rec("C1 w8a8 K=2048 N=6144", npu.plan_name(ws_c1[0], 16), 16, g, K * N + 16 * K + 4 * 16 * N, 2 * 16 * N * K, "hbm",
-        (lambda r: gemm(A512[:r], codes1), gkind, gwhat))
+    if want("c1"):
+        # ---- config 1, M=16 (the headline weights)
+        g, _ = measure(npu, hip, ws_c1, 16, dA, dC, 960, 48)
+        rec("C1 w8a8 K=2048 N=6144", npu.plan_name(ws_c1[0], 16), 16, g, K * N + 16 * K + 4 * 16 * N, 2 * 16 * N * K, "hbm",
+            (lambda r: gemm(A512[:r], codes1), gkind, gwhat))
 
-    # ---- config 2: fp16, K = N = 2048, M in {1, 16, 128, 512}
-    K2 = N2 = 2048
-    B2 = (rng.standard_normal((K2, N2)) * 0.02).astype(np.float16)
-    A2 = rng.standard_normal((512, K2)).astype(np.float16)
-    ws2 = [npu.pack_f16(B2) for _ in range(64)]   # 64 x 8 MB
-    dA2 = L.ork_dev_alloc(npu.h, A2.nbytes)
-    assert all(ws2) and dA2 and L.ork_dev_upload(npu.h, dA2, ork.ptr(A2), A2.nbytes) == 0
-    for M in (1, 16, 128, 512):
-        n = steps_for(0.006 if M < 512 else 0.012)
-        g, _ = measure(npu, hip, ws2, M, dA2, dC, n, 16, "ork_f16_mm_run")
-        rec("C2 fp16 K=N=2048", npu.plan_name(ws2[0], M), M, g, 2 * M * K2 + 2 * K2 * N2 + 4 * M * N2,
-            2 * M * N2 * K2, "hbm" if M <= 128 else "mfma_fp16",
-            (lambda r: O.gemm_f16_f32acc(A2[:r], B2), "port",
-             "oracle restatement of the reference's fp32-accumulate fp16 loop (examples/test_matmul.c:37)"))
-    L.ork_npu_set_async(npu.h, 0)
-    C2 = np.empty((4, N2), np.float32)
-    assert L.ork_f16_mm_run(npu.h, ws2[0], 4, dA2, dC) == 0
-    assert L.ork_dev_download(npu.h, ork.ptr(C2), dC, C2.nbytes) == 0
-    assert O.fp16_err(C2, O.gemm_f16_f64acc(A2[:4], B2)) <= 2e-3, "fp16 spot check"
-    L.ork_npu_set_async(npu.h, 1)
-    for w in ws2:
-        L.ork_mm_free(npu.h, w)
-    L.ork_dev_free(npu.h, dA2)
-
-    # ---- config 3: w4a8, K=2048, N=6144, importance vector, uniform and NF4, M in {1, 64}
-    W3 = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
-    im3 = rng.uniform(0.5, 2.0, K).astype(np.float32)
-    for nf4 in (0, 1):
-        if nf4:
-            os.environ["ORK_NF4"] = "1"
-        try:
-            w0, _ = npu.pack_i4a8(W3, im3)
-        finally:
-            os.environ.pop("ORK_NF4", None)
-        blob = ork.dump_i4a8(w0)
-        ws3 = [w0] + [npu.load_i4a8(K, N, blob) for _ in range(83)]   # 84 x 6.3 MB
-        assert all(ws3)
-        _, codes3 = O.o4n1_decode(K, N, blob)   # the reference's CPU path: inflate at load, then the int8 GEMM
-        name = "C3 w4a8 %s K=2048 N=6144" % ("nf4" if nf4 else "uniform")
-        for M in (1, 64):
-            g, _ = measure(npu, hip, ws3, M, dA, dC, steps_for(0.003), 32)
-            rec(name, npu.plan_name(ws3[0], M), M, g, K * N // 2 + M * K + 4 * M * N, 2 * M * N * K, "hbm",
-                (lambda r, c3=codes3: gemm(A512[:r], c3), gkind, gwhat + " on the inflated codes"))
+    if want("c2"):
+        # ---- config 2: fp16, K = N = 2048, M in {1, 16, 128, 512}
+        K2 = N2 = 2048
+        B2 = (rng.standard_normal((K2, N2)) * 0.02).astype(np.float16)
+        A2 = rng.standard_normal((512, K2)).astype(np.float16)
+        ws2 = [npu.pack_f16(B2) for _ in range(64)]   # 64 x 8 MB
+        dA2 = L.ork_dev_alloc(npu.h, A2.nbytes)
+        assert all(ws2) and dA2 and L.ork_dev_upload(npu.h, dA2, ork.ptr(A2), A2.nbytes) == 0
+        for M in (1, 16, 128, 512):
+            n = steps_for(0.006 if M < 512 else 0.012)
+            g, _ = measure(npu, hip, ws2, M, dA2, dC, n, 16, "ork_f16_mm_run")
+            rec("C2 fp16 K=N=2048", npu.plan_name(ws2[0], M), M, g, 2 * M * K2 + 2 * K2 * N2 + 4 * M * N2,
+                2 * M * N2 * K2, "hbm" if M <= 128 else "mfma_fp16",
+                (lambda r: O.gemm_f16_f32acc(A2[:r], B2), "port",
+                 "oracle restatement of the reference's fp32-accumulate fp16 loop (examples/test_matmul.c:37)"))
         L.ork_npu_set_async(npu.h, 0)
-        A3 = np.empty((2, K), np.int8)
-        assert L.ork_dev_download(npu.h, ork.ptr(A3), dA, A3.nbytes) == 0
-        C3 = np.empty((2, N), np.int32)
-        assert L.ork_i8_mm_run(npu.h, ws3[-1], 2, dA, dC) == 0
-        assert L.ork_dev_download(npu.h, ork.ptr(C3), dC, C3.nbytes) == 0
-        assert np.array_equal(C3, O.gemm_i32(A3, codes3)), "w4a8 spot check"
+        C2 = np.empty((4, N2), np.float32)
+        assert L.ork_f16_mm_run(npu.h, ws2[0], 4, dA2, dC) == 0
+        assert L.ork_dev_download(npu.h, ork.ptr(C2), dC, C2.nbytes) == 0
+        assert O.fp16_err(C2, O.gemm_f16_f64acc(A2[:4], B2)) <= 2e-3, "fp16 spot check"
         L.ork_npu_set_async(npu.h, 1)
-        for w in ws3:
+        for w in ws2:
             L.ork_mm_free(npu.h, w)
+        L.ork_dev_free(npu.h, dA2)
 
-    # ---- config 4: W4A4, M=256, K=N=4096, values in [-8, 7]
-    K4 = N4 = 4096
-    B4 = rng.integers(-8, 8, size=(K4, N4), dtype=np.int8)
-    A4 = rng.integers(-8, 8, size=(256, K4), dtype=np.int8)
-    ws4 = [npu.pack_i4(B4) for _ in range(64)]   # 64 x 8 MB of nibbles
-    dA4 = L.ork_dev_alloc(npu.h, A4.nbytes)
-    assert all(ws4) and dA4 and L.ork_dev_upload(npu.h, dA4, ork.ptr(A4), A4.nbytes) == 0
-    g, _ = measure(npu, hip, ws4, 256, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run")
-    rec("C4 W4A4 K=N=4096", npu.plan_name(ws4[0], 256), 256, g, 256 * K4 + K4 * N4 // 2 + 4 * 256 * N4,
-        2 * 256 * N4 * K4, "mfma_int8",
-        (lambda r: gemm(A4[:r], B4), gkind, gwhat + " on the int8 containers (ork_i4_mm_run's offline branch)"))
-    L.ork_npu_set_async(npu.h, 0)
-    C4 = np.empty((256, N4), np.int32)
-    assert L.ork_dev_download(npu.h, ork.ptr(C4), dC, C4.nbytes) == 0
-    assert np.array_equal(C4[:2], O.gemm_i32(A4[:2], B4)) and np.array_equal(C4[-2:], O.gemm_i32(A4[-2:], B4)), \
-        "W4A4 spot check"
-    L.ork_npu_set_async(npu.h, 1)
-    for w in ws4:
-        L.ork_mm_free(npu.h, w)
+    if want("c3"):
+        # ---- config 3: w4a8, K=2048, N=6144, importance vector, uniform and NF4, M in {1, 64}
+        W3 = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        im3 = rng.uniform(0.5, 2.0, K).astype(np.float32)
+        for nf4 in (0, 1):
+            if nf4:
+                os.environ["ORK_NF4"] = "1"
+            try:
+                w0, _ = npu.pack_i4a8(W3, im3)
+            finally:
+                os.environ.pop("ORK_NF4", None)
+            blob = ork.dump_i4a8(w0)
+            ws3 = [w0] + [npu.load_i4a8(K, N, blob) for _ in range(83)]   # 84 x 6.3 MB
+            assert all(ws3)
+            _, codes3 = O.o4n1_decode(K, N, blob)   # the reference's CPU path: inflate at load, then the int8 GEMM
+            name = "C3 w4a8 %s K=2048 N=6144" % ("nf4" if nf4 else "uniform")
+            for M in (1, 64):
+                g, _ = measure(npu, hip, ws3, M, dA, dC, steps_for(0.003), 32)
+                rec(name, npu.plan_name(ws3[0], M), M, g, K * N // 2 + M * K + 4 * M * N, 2 * M * N * K, "hbm",
+                    (lambda r, c3=codes3: gemm(A512[:r], c3), gkind, gwhat + " on the inflated codes"))
+            L.ork_npu_set_async(npu.h, 0)
+            A3 = np.empty((2, K), np.int8)
+            assert L.ork_dev_download(npu.h, ork.ptr(A3), dA, A3.nbytes) == 0
+            C3 = np.empty((2, N), np.int32)
+            assert L.ork_i8_mm_run(npu.h, ws3[-1], 2, dA, dC) == 0
+            assert L.ork_dev_download(npu.h, ork.ptr(C3), dC, C3.nbytes) == 0
+            assert np.array_equal(C3, O.gemm_i32(A3, codes3)), "w4a8 spot check"
+            L.ork_npu_set_async(npu.h, 1)
+            for w in ws3:
+                L.ork_mm_free(npu.h, w)
 
-    # ---- grouped scales (not a BASELINE config): W4A4 K=N=4096 with G=128 scales, M in {1, 256}; and the
-    # grouped int8 shape of examples/test_grouped_i8.c (W4A4 pack loaded as int8, K=2048, N=16384, G=512)
-    G4 = 128
-    Sk4 = K4 // G4
-    ggemm = O.ref_gemm_grouped if have_ref else O.gemm_grouped
-    ggwhat = "orki_cpu_gemm_grouped as built (-O2)" if have_ref else "oracle restatement of orki_cpu_gemm_grouped"
-    aS4 = rng.uniform(1e-3, 1e-2, size=(256, Sk4)).astype(np.float32)
-    bS4 = rng.uniform(1e-3, 1e-2, size=(Sk4, N4)).astype(np.float32)
-    dS4 = [L.ork_dev_alloc(npu.h, a.nbytes) for a in (aS4, bS4)]
-    assert all(dS4) and all(L.ork_dev_upload(npu.h, d, ork.ptr(a), a.nbytes) == 0 for d, a in zip(dS4, (aS4, bS4)))
-    wg4 = [L.ork_i4_mm_pack_grouped(npu.h, K4, N4, ork.ptr(B4), G4) for _ in range(64)]
-    assert all(wg4)
-    for M in (1, 256):
-        g, _ = measure(npu, hip, wg4, M, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run_grouped", dS4)
-        nbytes = K4 * N4 // 2 + M * K4 + 4 * (M * Sk4 + Sk4 * N4) + 4 * M * N4
-        rec("grouped W4A4 K=N=4096 G=128", npu.grouped_plan_name(wg4[0], M), M, g, nbytes, 2 * M * N4 * K4,
-            "hbm" if M <= 16 else "mfma_int8",
-            (lambda r: ggemm(A4[:r], B4, aS4[:r], bS4, G4), gkind, ggwhat))
-    L.ork_npu_set_async(npu.h, 0)
-    Cg = np.empty((256, N4), np.float32)  # what the timed M=256 launches wrote (every copy holds B4)
-    assert L.ork_dev_download(npu.h, ork.ptr(Cg), dC, Cg.nbytes) == 0
-    rows = np.r_[0:2, 254:256]
-    assert np.array_equal(Cg[rows], O.gemm_grouped(A4[rows], B4, aS4[rows], bS4, G4)), "grouped W4A4 M=256 spot check"
-    Cg = np.empty((4, N4), np.float32)
-    assert L.ork_i4_mm_run_grouped(npu.h, wg4[0], 4, dA4, dS4[0], dS4[1], dC) == 0
-    assert L.ork_dev_download(npu.h, ork.ptr(Cg), dC, Cg.nbytes) == 0
-    assert np.array_equal(Cg, O.gemm_grouped(A4[:4], B4, aS4[:4], bS4, G4)), "grouped W4A4 spot check"
-    L.ork_npu_set_async(npu.h, 1)
-    for w in wg4:
-        L.ork_mm_free(npu.h, w)
-    L.ork_dev_free(npu.h, dA4)
-    K8, N8, G8, M8 = 2048, 16384, 512, 8
-    B8 = rng.integers(-8, 8, size=(K8, N8), dtype=np.int8)
-    blob8 = ork.dump_cpu(npu.h, B8, w4a4=True)
-    wg8 = [L.ork_i4a8_mm_load_tiled(npu.h, K8, N8, ork.ptr(blob8), blob8.nbytes, G8) for _ in range(40)]
-    aS8 = rng.uniform(1e-3, 1e-2, size=(M8, K8 // G8)).astype(np.float32)
-    bS8 = rng.uniform(1e-3, 1e-2, size=(K8 // G8, N8)).astype(np.float32)
-    dS8 = [L.ork_dev_alloc(npu.h, a.nbytes) for a in (aS8, bS8)]
-    assert all(wg8) and all(dS8)
-    assert all(L.ork_dev_upload(npu.h, d, ork.ptr(a), a.nbytes) == 0 for d, a in zip(dS8, (aS8, bS8)))
-    g, _ = measure(npu, hip, wg8, M8, dA, dC, steps_for(0.01), 16, "ork_i8_mm_run_grouped", dS8)
-    rec("grouped int8 (W4A4 pack) K=2048 N=16384 G=512", npu.grouped_plan_name(wg8[0], M8), M8, g,
-        K8 * N8 // 2 + M8 * K8 + 4 * (M8 * 4 + 4 * N8) + 4 * M8 * N8, 2 * M8 * N8 * K8, "hbm",
-        (lambda r: ggemm(A512[:r], B8, aS8[:r], bS8, G8), gkind, ggwhat))
-    for w in wg8:
-        L.ork_mm_free(npu.h, w)
-    for d in dS4 + dS8:
-        L.ork_dev_free(npu.h, d)
+    if want("c4"):
+        # ---- config 4: W4A4, M=256, K=N=4096, values in [-8, 7]
+        K4 = N4 = 4096
+        B4 = rng.integers(-8, 8, size=(K4, N4), dtype=np.int8)
+        A4 = rng.integers(-8, 8, size=(256, K4), dtype=np.int8)
+        ws4 = [npu.pack_i4(B4) for _ in range(64)]   # 64 x 8 MB of nibbles
+        dA4 = L.ork_dev_alloc(npu.h, A4.nbytes)
+        assert all(ws4) and dA4 and L.ork_dev_upload(npu.h, dA4, ork.ptr(A4), A4.nbytes) == 0
+        g, _ = measure(npu, hip, ws4, 256, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run")
+        rec("C4 W4A4 K=N=4096", npu.plan_name(ws4[0], 256), 256, g, 256 * K4 + K4 * N4 // 2 + 4 * 256 * N4,
+            2 * 256 * N4 * K4, "mfma_int8",
+            (lambda r: gemm(A4[:r], B4), gkind, gwhat + " on the int8 containers (ork_i4_mm_run's offline branch)"))
+        L.ork_npu_set_async(npu.h, 0)
+        C4 = np.empty((256, N4), np.int32)
+        assert L.ork_dev_download(npu.h, ork.ptr(C4), dC, C4.nbytes) == 0
+        assert np.array_equal(C4[:2], O.gemm_i32(A4[:2], B4)) and np.array_equal(C4[-2:], O.gemm_i32(A4[-2:], B4)), \
+            "W4A4 spot check"
+        L.ork_npu_set_async(npu.h, 1)
+        for w in ws4:
+            L.ork_mm_free(npu.h, w)
+        if not want("grouped"):
+            L.ork_dev_free(npu.h, dA4)
+
+    if want("grouped"):
+        # ---- grouped scales (not a BASELINE config): W4A4 K=N=4096 with G=128 scales, M in {1, 256}; and the
+        # grouped int8 shape of examples/test_grouped_i8.c (W4A4 pack loaded as int8, K=2048, N=16384, G=512)
+        G4 = 128
+        Sk4 = K4 // G4
+        ggemm = O.ref_gemm_grouped if have_ref else O.gemm_grouped
+        ggwhat = "orki_cpu_gemm_grouped as built (-O2)" if have_ref else "oracle restatement of orki_cpu_gemm_grouped"
+        aS4 = rng.uniform(1e-3, 1e-2, size=(256, Sk4)).astype(np.float32)
+        bS4 = rng.uniform(1e-3, 1e-2, size=(Sk4, N4)).astype(np.float32)
+        dS4 = [L.ork_dev_alloc(npu.h, a.nbytes) for a in (aS4, bS4)]
+        assert all(dS4) and all(L.ork_dev_upload(npu.h, d, ork.ptr(a), a.nbytes) == 0 for d, a in zip(dS4, (aS4, bS4)))
+        wg4 = [L.ork_i4_mm_pack_grouped(npu.h, K4, N4, ork.ptr(B4), G4) for _ in range(64)]
+        assert all(wg4)
+        for M in (1, 256):
+            g, _ = measure(npu, hip, wg4, M, dA4, dC, steps_for(0.01), 16, "ork_i4_mm_run_grouped", dS4)
+            nbytes = K4 * N4 // 2 + M * K4 + 4 * (M * Sk4 + Sk4 * N4) + 4 * M * N4
+            rec("grouped W4A4 K=N=4096 G=128", npu.grouped_plan_name(wg4[0], M), M, g, nbytes, 2 * M * N4 * K4,
+                "hbm" if M <= 16 else "mfma_int8",
+                (lambda r: ggemm(A4[:r], B4, aS4[:r], bS4, G4), gkind, ggwhat))
+        L.ork_npu_set_async(npu.h, 0)
+        Cg = np.empty((256, N4), np.float32)  # what the timed M=256 launches wrote (every copy holds B4)
+        assert L.ork_dev_download(npu.h, ork.ptr(Cg), dC, Cg.nbytes) == 0
+        rows = np.r_[0:2, 254:256]
+        assert np.array_equal(Cg[rows], O.gemm_grouped(A4[rows], B4, aS4[rows], bS4, G4)), "grouped W4A4 M=256 spot check"
+        Cg = np.empty((4, N4), np.float32)
+        assert L.ork_i4_mm_run_grouped(npu.h, wg4[0], 4, dA4, dS4[0], dS4[1], dC) == 0
+        assert L.ork_dev_download(npu.h, ork.ptr(Cg), dC, Cg.nbytes) == 0
+        assert np.array_equal(Cg, O.gemm_grouped(A4[:4], B4, aS4[:4], bS4, G4)), "grouped W4A4 spot check"
+        L.ork_npu_set_async(npu.h, 1)
+        for w in wg4:
+            L.ork_mm_free(npu.h, w)
+        L.ork_dev_free(npu.h, dA4)
+        K8, N8, G8, M8 = 2048, 16384, 512, 8
+        B8 = rng.integers(-8, 8, size=(K8, N8), dtype=np.int8)
+        blob8 = ork.dump_cpu(npu.h, B8, w4a4=True)
+        wg8 = [L.ork_i4a8_mm_load_tiled(npu.h, K8, N8, ork.ptr(blob8), blob8.nbytes, G8) for _ in range(40)]
+        aS8 = rng.uniform(1e-3, 1e-2, size=(M8, K8 // G8)).astype(np.float32)
+        bS8 = rng.uniform(1e-3, 1e-2, size=(K8 // G8, N8)).astype(np.float32)
+        dS8 = [L.ork_dev_alloc(npu.h, a.nbytes) for a in (aS8, bS8)]
+        assert all(wg8) and all(dS8)
+        assert all(L.ork_dev_upload(npu.h, d, ork.ptr(a), a.nbytes) == 0 for d, a in zip(dS8, (aS8, bS8)))
+        g, _ = measure(npu, hip, wg8, M8, dA, dC, steps_for(0.01), 16, "ork_i8_mm_run_grouped", dS8)
+        rec("grouped int8 (W4A4 pack) K=2048 N=16384 G=512", npu.grouped_plan_name(wg8[0], M8), M8, g,
+            K8 * N8 // 2 + M8 * K8 + 4 * (M8 * 4 + 4 * N8) + 4 * M8 * N8, 2 * M8 * N8 * K8, "hbm",
+            (lambda r: ggemm(A512[:r], B8, aS8[:r], bS8, G8), gkind, ggwhat))
+        for w in wg8:
+            L.ork_mm_free(npu.h, w)
+        for d in dS4 + dS8:
+            L.ork_dev_free(npu.h, d)
     return out
 
 
@@ -595,8 +606,11 @@ def main():
     ap.add_argument("--no-decoder", action="store_true", help="skip BASELINE config 5 (the Qwen3-shaped decoder)")
     ap.add_argument("--eager-decoder", action="store_true",
                     help="profiling: launch the decode steps eagerly instead of replaying the captured graph (same kernels)")
-    ap.add_argument("--only", choices=["gemv", "m512", "chain", "decoder"],
-                    help="profiling: time only one kernel (decoder: only BASELINE config 5, w8a8)")
+    ap.add_argument("--only", choices=["gemv", "m512", "chain", "decoder", "configs"],
+                    help="profiling: time only one kernel (decoder: only BASELINE config 5, w8a8; configs: the "
+                         "config sweep's sections named by --configs)")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,grouped",
+                    help="with --only configs: comma-separated sections of the config sweep (c1 c2 c3 c4 grouped)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling: run device-to-device copies of one weight's bytes (a plain copy kernel of "
                          "known size) instead of the bench, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -637,6 +651,14 @@ def main():
         assert dA and dC
         assert L.ork_dev_upload(npu.h, dA, ork.ptr(A512), A512.nbytes) == 0
         L.ork_npu_set_async(npu.h, 1)
+        if args.only == "configs":
+            sel = set(x.strip() for x in args.configs.split(",") if x.strip())
+            print(json.dumps(sweep_configs(npu, hip, L, ws, dA, dC, codes, A512,
+                                           0.0 if args.no_cpu else min(2.0, args.cpu_seconds / 5), only=sel)),
+                  flush=True)
+            for w in ws:
+                ork.lib().ork_mm_free(npu.h, w)
+            return
         gemv_plan = npu.plan_name(ws[0], 1)
         gemm_plan = npu.plan_name(ws[0], 512)
         print(f"[bench] packed {R} x {K}x{N} int8 weights ({pack_s * 1e3:.1f} ms/pack); plans M=1 {gemv_plan}, "
