@@ -58,6 +58,8 @@ int         orkh_device_count(void);
 int         orkh_init(int ordinal, orkh_dev *out, void **stream_out);
 void        orkh_stream_destroy(void *stream);
 const char *orkh_last_error(void);
+/* Why the last orkh_mm_launch* call on this thread refused its plan ("" when it did not). */
+const char *orkh_launch_error(void);
 void       *orkh_malloc(size_t n);                 /* device memory (HBM); NULL on failure */
 int         orkh_free(void *p);
 void       *orkh_host_alloc(size_t n);             /* pinned, device-mapped host memory */
@@ -111,6 +113,8 @@ typedef struct orkh_plan {
     int aline;
     /* STREAM: np = 2 pairs panels: npg workgroups, the first N/16 - npg owning two adjacent panels each */
     int np, npg;
+    /* GEMV: 1 = half a panel (8 columns) per workgroup, grid (N/8, ksplit) (k_gemv_half), else one panel */
+    int half;
     void *ws;             /* split-K partials, >= ksplit*M*N*4 bytes (device) */
 } orkh_plan;
 

@@ -10,6 +10,8 @@
 //             broadcast of one dword per lane, and the four K-groups of a column fold with
 //             v_permlane32/16_swap. Measured on MI355X at K=2048, N=6144 int8: 3.83 us against
 //             4.08 us for the same flow on MFMA (the MFMA issue itself adds ~0.4 us per launch).
+//             k_gemv_half, the planner's default, gives each workgroup half a panel (8 columns) so
+//             that the bytes spread evenly over the CUs.
 //   k_stream  small M (<= 64): each wave streams a run of 1 KiB panel blocks straight from HBM into
 //             registers (one coalesced 16 B load per lane per block), decodes int4 in registers and
 //             issues v_mfma_i32_16x16x64_i8 / v_mfma_f32_16x16x32_f16 with the activations as the A
@@ -342,6 +344,85 @@ template <int KIND, int WPG, int KU>
 __global__ __launch_bounds__(WPG * 64) void k_gemv(orkh_mm p, int kbw, int kbs, int ksplit, void *ws) {
     __shared__ typename KT<KIND>::c_t red[WPG][16];
     gemv_panel<KIND, WPG, KU>(p, blockIdx.x, blockIdx.y, kbw, kbs, ksplit, ws, red);
+}
+
+// k_gemv_half: M = 1 with half a panel per workgroup. Grid (N/8, ksplit), WPG waves; workgroup (b, ks) owns
+// columns 8h .. 8h+7 (h = b % 2) of panel b / 2 over K-blocks [ks*kbs, ks*kbs+kbs), wave w a run of kbw of them.
+// Whole panels put two panels on some CUs and one on others whenever N/16 is not a multiple of the CU count
+// (N = 6144: 384 panels on 256 CUs); halves spread the bytes three to a CU there, and fill twice the CUs where
+// there are fewer panels than CUs. In a 1 KiB block, column c's k-group g is the 16 bytes at (16 g + c) * 16, so
+// a half is four whole 128-byte lines, and one load instruction fetches the halves of two blocks: lane l takes
+// block kb + l/32, k-group (l/8) % 4, column 8h + l%8. A wave issues all NI instructions of its run at once (the
+// launcher picks NI = ceil(kbw / 2) where it is instantiated, so only an odd run's last half re-reads a block;
+// runs past 16 blocks go in batches of 8 instructions), then each lane
+// loads its k-group's activation bytes (16, or 32 for the nibble kinds: the same few addresses across lanes,
+// served by the L1) and accumulates with v_dot4 / v_dot2. The eight lanes of a column (block l/32, k-group
+// (l/8)%4) fold with permlane32 / permlane16 swaps and a row rotation by 8; the waves reduce through LDS.
+template <int KIND, int WPG, int NI>
+__global__ __launch_bounds__(WPG * 64) void k_gemv_half(orkh_mm p, int kbw, int kbs, int ksplit, void *ws) {
+    using T = KT<KIND>;
+    typedef typename T::c_t c_t;
+    constexpr int W = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 8 : 4;  // activation dwords per k-group per block
+    constexpr int KPBB = T::KPB * T::ESZ;                               // activation bytes per block
+    __shared__ c_t red[WPG][8];
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = blockIdx.x >> 1, h = blockIdx.x & 1, ks = blockIdx.y;
+    const int kb_hi = min(ks * kbs + kbs, p.KB);
+    const int kb0 = ks * kbs + w * kbw, kb1 = min(kb0 + kbw, kb_hi);
+    const int g = (lane >> 3) & 3, sub = lane >> 5;
+    const v4i *bp = (const v4i *)p.B + (size_t)nb * p.KB * 64 + g * 16 + h * 8 + (lane & 7);
+    const char *A = (const char *)p.A;
+    const Lut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
+    c_t acc = 0;
+    for (int kb = kb0; kb < kb1; kb += 2 * NI) {
+        v4i raw[NI], act[NI][W / 4];
+        bool ok[NI];
+#pragma unroll
+        for (int q = 0; q < NI; q++)  // past the run's end: its last block again (no branches), with activations 0
+            raw[q] = __builtin_nontemporal_load(bp + (size_t)min(kb + 2 * q + sub, kb1 - 1) * 64);
+#pragma unroll
+        for (int q = 0; q < NI; q++) {
+            const int blk = kb + 2 * q + sub, byte = blk * KPBB + g * (W * 4);
+            ok[q] = blk < kb1 && byte / T::ESZ < p.K;
+#pragma unroll
+            for (int j = 0; j < W / 4; j++) act[q][j] = *(const v4i *)(A + (ok[q] ? byte + 16 * j : 0));
+        }
+#pragma unroll
+        for (int q = 0; q < NI; q++) {
+            v4i op[T::STEPS];
+            decode<KIND>(raw[q], op, L);
+#pragma unroll
+            for (int d = 0; d < W; d++) {
+                const int a = ok[q] ? act[q][d / 4][d % 4] : 0;
+                const int b = op[d / 4][d % 4];
+                if constexpr (KIND == ORKH_F16)
+                    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, a), __builtin_bit_cast(v2h, b), acc, false);
+                else
+                    acc = __builtin_amdgcn_sdot4(a, b, acc, false);
+            }
+        }
+    }
+    // the column's eight lanes: l ^ 32, l ^ 16, then l ^ 8 (row_ror:8 within each 16-lane row)
+    {
+        int x = __builtin_bit_cast(int, acc);
+        const auto s32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        acc += __builtin_bit_cast(c_t, (int)(lane < 32 ? s32[1] : s32[0]));
+        x = __builtin_bit_cast(int, acc);
+        const auto s16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        acc += __builtin_bit_cast(c_t, (int)((lane & 16) == 0 ? s16[1] : s16[0]));
+        x = __builtin_bit_cast(int, acc);
+        acc += __builtin_bit_cast(c_t, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+    }
+    if (lane < 8) red[w][lane] = acc;
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        c_t s = red[0][threadIdx.x];
+#pragma unroll
+        for (int ww = 1; ww < WPG; ww++) s += red[ww][threadIdx.x];
+        const int n = nb * 16 + h * 8 + threadIdx.x;
+        if (ksplit == 1) ((c_t *)p.C)[n] = finish<KIND>(s);
+        else ((c_t *)ws)[(size_t)ks * p.N + n] = finish<KIND>(s);
+    }
 }
 
 // k_gemv_group: up to ORKH_GROUP_MAX independent M = 1 GEMVs of one kind in a single launch (the
@@ -1060,6 +1141,50 @@ int launch_gemv(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
         snprintf(g_lerr, sizeof g_lerr, "gemv plan: M=%d (needs 1)", p->M);
         return -2;
     }
+    if (q->half && ((uintptr_t)p->A & 15) == 0) {
+        // NI: load instructions per batch (two blocks each), the smallest instantiated count that covers the run
+        // (every count up to 8 on 8 waves, where the planner's runs are 5-16 blocks; 1-4 and 8 on 2 or 4 waves)
+        const int need = (q->kbw + 1) / 2;
+        if ((q->wpg != 2 && q->wpg != 4 && q->wpg != 8) || q->kbw < 1 || (p->N & 15)) {
+            snprintf(g_lerr, sizeof g_lerr, "gemv half plan: wpg=%d kbw=%d N=%d unsupported", q->wpg, q->kbw, p->N);
+            return -2;
+        }
+        dim3 grid(p->N / 8, q->ksplit), block(q->wpg * 64);
+#define ORKH_GH(W_, N_) hipLaunchKernelGGL((k_gemv_half<KIND, W_, N_>), grid, block, 0, s, *p, q->kbw, q->kbs, q->ksplit, q->ws)
+        if (q->wpg == 8) {
+            switch (need < 8 ? need : 8) {
+            case 1: ORKH_GH(8, 1); break;
+            case 2: ORKH_GH(8, 2); break;
+            case 3: ORKH_GH(8, 3); break;
+            case 4: ORKH_GH(8, 4); break;
+            case 5: ORKH_GH(8, 5); break;
+            case 6: ORKH_GH(8, 6); break;
+            case 7: ORKH_GH(8, 7); break;
+            default: ORKH_GH(8, 8); break;
+            }
+        } else if (q->wpg == 4) {
+            if (need <= 1) ORKH_GH(4, 1);
+            else if (need <= 2) ORKH_GH(4, 2);
+            else if (need <= 3) ORKH_GH(4, 3);
+            else if (need <= 4) ORKH_GH(4, 4);
+            else ORKH_GH(4, 8);
+        } else {
+            if (need <= 1) ORKH_GH(2, 1);
+            else if (need <= 2) ORKH_GH(2, 2);
+            else if (need <= 3) ORKH_GH(2, 3);
+            else if (need <= 4) ORKH_GH(2, 4);
+            else ORKH_GH(2, 8);
+        }
+#undef ORKH_GH
+        return 0;
+    }
+    if (q->half) {
+        // A not 16-byte aligned (the half kernel loads activations 16 bytes at a time): whole panels, same K split
+        orkh_plan w = *q;
+        w.wpg = q->wpg == 8 ? 8 : 4;
+        w.kbw = (q->kbs + w.wpg - 1) / w.wpg;
+        return w.wpg == 8 ? launch_gemv_v<KIND, 8>(p, &w, s) : launch_gemv_v<KIND, 4>(p, &w, s);
+    }
     if (q->wpg == 8) return launch_gemv_v<KIND, 8>(p, q, s);
     if (q->wpg == 4) return launch_gemv_v<KIND, 4>(p, q, s);
     snprintf(g_lerr, sizeof g_lerr, "gemv plan: wpg=%d unsupported", q->wpg);
@@ -1204,8 +1329,11 @@ int launch_tiled(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
 
 }  // namespace
 
+extern "C" const char *orkh_launch_error(void) { return g_lerr; }
+
 extern "C" int orkh_mm_launch(const orkh_mm *p, const orkh_plan *q, void *stream) {
     hipStream_t s = (hipStream_t)stream;
+    g_lerr[0] = 0;
     int rc;
     if (q->algo == ORKH_ALGO_GEMV) {
         switch (p->kind) {
@@ -1272,6 +1400,7 @@ extern "C" int orkh_mm_launch(const orkh_mm *p, const orkh_plan *q, void *stream
 
 extern "C" int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream) {
     hipStream_t s = (hipStream_t)stream;
+    g_lerr[0] = 0;
     if (g->n < 1 || g->n > ORKH_GROUP_MAX) {
         snprintf(g_lerr, sizeof g_lerr, "group: n=%d", g->n);
         return -2;
@@ -1361,6 +1490,7 @@ extern "C" int orkh_tiled2_ring_lds(int kind, int bm, int bn) {
 
 extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *q, int G, const float *aS, const float *bS,
                                       float *C, int ldc, void *stream) {
+    g_lerr[0] = 0;
     hipStream_t s = (hipStream_t)stream;
     if (G < 32 || G % 32 || p->K % G || p->N % 16 || p->M < 1 || ldc < p->N ||
         (p->kind != ORKH_I8 && p->kind != ORKH_I4U && p->kind != ORKH_NF4) ||
@@ -1402,7 +1532,7 @@ extern "C" const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *q) {
     static const char *kn[] = {"i8", "i4u", "nf4", "f16"};
     const char *k = (p->kind >= 0 && p->kind <= 3) ? kn[p->kind] : "?";
     if (q->algo == ORKH_ALGO_GEMV)
-        snprintf(b, sizeof b, "gemv_%s_w%d_kbw%d_ks%d", k, q->wpg, q->kbw, q->ksplit);
+        snprintf(b, sizeof b, "%s_%s_w%d_kbw%d_ks%d", q->half ? "gemvh" : "gemv", k, q->wpg, q->kbw, q->ksplit);
     else if (q->algo == ORKH_ALGO_STREAM)
         snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d%s", k, q->mt, q->wpg, q->kbw, q->ksplit, q->np == 2 ? "_p2" : "");
     else if (q->ksplit > 1)

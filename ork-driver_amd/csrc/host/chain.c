@@ -110,7 +110,8 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
         if (done[i] || q[i].algo != ORKH_ALGO_GEMV || q[i].ksplit != 1) continue;
         orkh_group g;
         memset(&g, 0, sizeof g);
-        const int wpg = q[i].wpg;
+        /* the grouped kernel runs whole panels: their wave count, whatever geometry the task's own plan has */
+        const int wpg = orki_gemv_panel_wpg(c, t[i].w->rkind, t[i].w->KB, t[i].w->N / 16);
         int wg = 0;
         for (int j = i; j < S && g.n < ORKH_GROUP_MAX; j++) {
             if (done[j] || q[j].algo != ORKH_ALGO_GEMV || q[j].ksplit != 1 || t[j].w->rkind != t[i].w->rkind) continue;

@@ -28,7 +28,9 @@ void orki_err(const char *fmt, ...) {
 
 void orki_hip_fail(const char *what) {
     atomic_fetch_add(&g_io_fail, 1);
-    orki_err("HIP failure in %s: %s", what, orkh_last_error());
+    const char *le = orkh_launch_error();
+    if (le && le[0]) orki_err("HIP failure in %s: %s", what, le);
+    else orki_err("HIP failure in %s: %s", what, orkh_last_error());
 }
 
 long ork_io_failures(void) { return atomic_load(&g_io_fail); }

@@ -98,6 +98,8 @@ void   orki_tile_nib_kn(const int8_t *B_kn, int K, int N, int KB, uint8_t *out);
 
 /* ---- planner (plan.c) ---- */
 int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes);
+/* Waves per workgroup of the whole-panel GEMV for this weight (the grouped M = 1 launch of the multi-matmul submit). */
+int orki_gemv_panel_wpg(const ork_npu *c, int rkind, int KB, int NB);
 /* Kernel for a grouped-scale run (never K-split). */
 void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB, int G, orkh_plan *q);
 

@@ -6,8 +6,9 @@
  * 8192-wide outputs and M into CBUF-sized row groups, each a separate submit with a host int32
  * accumulate. On MI355X every shape is one launch (plus a reduce pass when K is split across
  * workgroups); the planner only decides how to fill 256 CUs:
- *   M = 1    GEMV: one 16-column panel per workgroup, waves split K in runs of 8 KiB; K is split across
- *            workgroups only for long-K, few-panel shapes that leave the machine underfilled.
+ *   M = 1    GEMV: half a 16-column panel per workgroup (whole panels where those already spread evenly over
+ *            the CUs), waves split K in runs of ~8 KiB; K is split across workgroups only for long-K,
+ *            few-panel shapes that leave the machine underfilled.
  *   M <= 64  the streaming kernel (same grid, runs of 1-4 KiB) or the LDS-ring tiled kernel, whichever a
  *            delivery model of both prices lower, each with its best K split (NF4: streaming, by the
  *            occupancy rule of the GEMV).
@@ -85,6 +86,37 @@ static int stream_rule_ks(const ork_npu *c, int rkind, int M, int KB, int NB, in
         if (ks > runs) ks = runs; /* every wave keeps a full run */
     }
     return ks;
+}
+
+/* The GEMV's half-panel geometry (k_gemv_half: 8 columns per workgroup, so the bytes spread evenly over the CUs
+ * whatever N/16 is): waves whose runs are about four load instructions (eight K-blocks; two instructions for
+ * NF4, whose codebook decode is heavier), 2, 4 or 8 waves. Measured against whole panels (graph-timed, us):
+ *   int8  K=2048 N=6144 3.95 -> 3.82; K=N=2048 2.77 -> 2.50; K=6144 N=2048 4.33 -> 3.77; K=8192 N=512 4.30 -> 3.39;
+ *         K=2048 N=151936 (an LM head) 45.9 -> 44.6
+ *   fp16  K=N=2048 3.52 -> 3.17
+ *   W4A8  uniform K=2048 N=6144 3.14 -> 3.10, K=6144 N=2048 3.94 -> 3.15; NF4 K=2048 N=6144 3.58 -> 3.28,
+ *         K=6144 N=2048 4.44 -> 3.35; W4A4 K=N=4096 3.60 -> 3.33
+ * Where whole panels already spread evenly (N/16 x the K split a multiple of the CU count) they stay: K=2048
+ * N=4096 int8 3.19 whole, 3.22 halves. ORK_GEMV_HALF=0/1 forces either and ORK_WPG=2/4/8 the waves (tests, A/B). */
+static void gemv_half_geom(const ork_npu *c, int rkind, int NB, int cu, orkh_plan *q) {
+    const char *e = knob(c, "ORK_GEMV_HALF");
+    if (e && atoi(e) == 0) return;
+    const long wgs = (long)NB * q->ksplit;
+    if (!e && wgs >= cu && cdiv((int)(2 * wgs), cu) >= 2 * cdiv((int)wgs, cu)) return;
+    const int blocks_per_wave = rkind == ORKH_NF4 ? 4 : 8;
+    const int need = cdiv(q->kbs, blocks_per_wave);
+    q->half = 1;
+    q->wpg = need <= 2 ? 2 : need <= 4 ? 4 : 8;
+    const char *fw = knob(c, "ORK_WPG");
+    if (fw && (atoi(fw) == 2 || atoi(fw) == 4 || atoi(fw) == 8)) q->wpg = atoi(fw);
+    q->kbw = cdiv(q->kbs, q->wpg);
+}
+
+int orki_gemv_panel_wpg(const ork_npu *c, int rkind, int KB, int NB) {
+    orkh_plan g;
+    memset(&g, 0, sizeof g);
+    stream_geom(c, rkind, 1, KB, NB, (c && c->cores > 0) ? c->cores : 256, 1, &g);
+    return g.wpg;
 }
 
 /* Time models (us) of the two MFMA kernels, for int8, fp16 and uniform int4 weights. A workgroup's time is
@@ -257,6 +289,7 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
         /* M = 1 takes the VALU-dot GEMV (same grid and fields); ORK_PLAN=stream keeps the MFMA kernel. */
         q->algo = (M == 1 && !f_stream) ? ORKH_ALGO_GEMV : ORKH_ALGO_STREAM;
         stream_geom(c, rkind, M, KB, NB, cu, ks, q);
+        if (q->algo == ORKH_ALGO_GEMV) gemv_half_geom(c, rkind, NB, cu, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }

@@ -16,6 +16,7 @@ int orkh_init(int ordinal, orkh_dev *out, void **stream_out) {
 }
 void orkh_stream_destroy(void *s) { (void)s; }
 const char *orkh_last_error(void) { return "stub"; }
+const char *orkh_launch_error(void) { return ""; }
 #define MAXP 100000
 static void *devp[MAXP]; static size_t devn[MAXP]; static int ndev;
 void *orkh_malloc(size_t n) { void *p = malloc(n ? n : 1); if (ndev < MAXP) { devp[ndev] = p; devn[ndev++] = n; } return p; }

@@ -660,3 +660,104 @@ def test_planner_mid_m_default(npu, kind, K, N, M):
     assert npu.plan_name(w, M).startswith("tiled2_"), npu.plan_name(w, M)
     assert rc == 0 and np.array_equal(C, O.gemm_i32(A, B)), npu.plan_name(w, M)
     ork.free(w)
+
+
+# ------------------------------------------------------------------------ M = 1: half panels and whole panels
+GEMV_HALF_SHAPES = [  # (K, N): K tails (K % 64 == 32; K % 128 == 32 for the nibble kinds), odd runs per wave, one panel
+    (32, 64), (96, 64), (2080, 64), (1056, 4160), (2048, 6144), (6144, 2048)]
+
+
+def _gemv_weight(npu, kind, K, N, rng):
+    """A packed weight of one kind and the B operand its oracle product takes (the codes for the W4A8 kinds)."""
+    if kind == "f16":
+        Bh = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+        return npu.pack_f16(Bh), Bh
+    if kind == "w4a4":
+        B = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
+        return npu.pack_i4(B), B
+    if kind == "i8":
+        B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+        return npu.pack_i8(B), B
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    if kind == "nf4":
+        os.environ["ORK_NF4"] = "1"
+    try:
+        w, _ = npu.pack_i4a8(W)
+    finally:
+        os.environ.pop("ORK_NF4", None)
+    _, _, codes = O.pack_i4a8(W, nf4=kind == "nf4")
+    return w, codes
+
+
+def _gemv_run(npu, kind, w, B, A):
+    if kind == "f16":
+        rc, C = npu.run_f16(w, A)
+        return rc == 0 and O.fp16_err(C, O.gemm_f16_f64acc(A, B)) <= FP16_TOL
+    rc, C = (npu.run_i4 if kind == "w4a4" else npu.run_i8)(w, A)
+    return rc == 0 and np.array_equal(C, O.gemm_i32(A, B))
+
+
+@pytest.mark.parametrize("kind", ["i8", "f16", "i4a8", "nf4", "w4a4"])
+def test_gemv_half_panels(npu, kind):
+    """M = 1 runs on half panels by default (8 columns per workgroup): exact against the oracle for the integer
+    kinds and within tolerance for fp16, like whole panels (ORK_GEMV_HALF=0), at every wave count (ORK_WPG) and
+    with forced K splits, over K tails and runs with an odd number of blocks."""
+    _say("gemv half", kind)
+    rng = _rng(77)
+    for K, N in GEMV_HALF_SHAPES:
+        w, B = _gemv_weight(npu, kind, K, N, rng)
+        assert w, (kind, K, N)
+        if kind == "f16":
+            A = rng.standard_normal((1, K)).astype(np.float16)
+        elif kind == "w4a4":
+            A = rng.integers(-8, 8, size=(1, K), dtype=np.int8)
+        else:
+            A = rng.integers(-127, 128, size=(1, K), dtype=np.int8)
+        assert _gemv_run(npu, kind, w, B, A), (kind, K, N, npu.plan_name(w, 1))
+        for env in (dict(ORK_GEMV_HALF=0), dict(ORK_GEMV_HALF=1), dict(ORK_GEMV_HALF=1, ORK_WPG=2),
+                    dict(ORK_GEMV_HALF=1, ORK_WPG=4), dict(ORK_GEMV_HALF=1, ORK_WPG=8), dict(ORK_GEMV_HALF=1, ORK_KSPLIT=3),
+                    dict(ORK_GEMV_HALF=1, ORK_KSPLIT=2, ORK_WPG=8), dict(ORK_GEMV_HALF=0, ORK_KSPLIT=2)):
+            with _env(**env):
+                name = npu.plan_name(w, 1)
+                assert name.startswith("gemvh_" if env["ORK_GEMV_HALF"] else "gemv_"), (env, name)
+                assert _gemv_run(npu, kind, w, B, A), (kind, K, N, env, name)
+        ork.free(w)
+
+
+def test_gemv_half_panel_rule(npu):
+    """The planner keeps whole panels where they already spread evenly (N/16 a multiple of the CU count) and takes
+    half panels otherwise: fewer panels than CUs, or a remainder that would put two panels on some CUs only."""
+    cu = ork.lib().ork_npu_cores(npu.h)
+    rng = _rng(79)
+    for N, half in ((16 * cu, False), (32 * cu, False), (24 * cu, True), (8 * cu, True), (16 * cu + 32, True)):
+        B = rng.integers(-128, 128, size=(256, N), dtype=np.int8)
+        w = npu.pack_i8(B)
+        assert npu.plan_name(w, 1).startswith("gemvh_" if half else "gemv_"), (N, cu, npu.plan_name(w, 1))
+        A = rng.integers(-127, 128, size=(1, 256), dtype=np.int8)
+        rc, C = npu.run_i8(w, A)
+        assert rc == 0 and np.array_equal(C, O.gemm_i32(A, B)), N
+        ork.free(w)
+
+
+def test_gemv_half_unaligned_activations(npu):
+    """A device activation row that is not 16-byte aligned runs on whole panels (the half-panel kernel loads
+    16 bytes at a time): same exact result."""
+    _say("gemv half unaligned A")
+    L = ork.lib()
+    rng = _rng(78)
+    K, N = 2080, 1056
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-127, 128, size=(1, K), dtype=np.int8)
+    w = npu.pack_i8(B)
+    dA = L.ork_dev_alloc(npu.h, K + 64)
+    dC = L.ork_dev_alloc(npu.h, N * 4)
+    assert w and dA and dC
+    for off in (0, 4, 8, 20):
+        assert L.ork_dev_upload(npu.h, dA + off, ork.ptr(A), K) == 0
+        assert L.ork_i8_mm_run(npu.h, w, 1, dA + off, dC) == 0
+        C = np.zeros((1, N), np.int32)
+        assert L.ork_dev_download(npu.h, ork.ptr(C), dC, N * 4) == 0
+        assert np.array_equal(C, O.gemm_i32(A, B)), off
+    L.ork_dev_free(npu.h, dA)
+    L.ork_dev_free(npu.h, dC)
+    ork.free(w)
