@@ -519,6 +519,14 @@ static int fused_ok(const q3_model *m) {
     return 1;
 }
 
+/* A fused matmul over P panels runs half a panel per workgroup unless whole panels already spread evenly over the
+ * CUs (P a multiple of the CU count), the rule of the library's M = 1 planner: o and down (128 panels) and the
+ * gate/up pair (384) take halves, q/k/v (256) whole panels. */
+static int fg_half(const q3_model *m, int P) {
+    const int cu = ork_npu_cores(m->ctx) > 0 ? ork_npu_cores(m->ctx) : 256;
+    return !(P >= cu && (2 * P + cu - 1) / cu >= 2 * ((P + cu - 1) / cu));
+}
+
 static int pass_fused(q3_model *m) {
     const q3_cfg *c = &m->c;
     void *s = m->stream;
@@ -565,6 +573,7 @@ static int pass_fused(q3_model *m) {
             f.nw = Ly->n1;
             f.eps = c->eps;
             f.as_out = m->asx;
+            f.half = fg_half(m, f.nb[0] + f.nb[1] + f.nb[2]);
             CK(q3k_fgemv(&f, s));
         }
         q3_att at = {.M = 1, .NH = NH, .NKV = NKV, .HD = HD, .S = m->S, .max_ctx = c->max_ctx, .q = m->q,
@@ -585,6 +594,7 @@ static int pass_fused(q3_model *m) {
         fo.row = m->att;
         fo.ws0 = Lo->ws;
         fo.x = m->x;
+        fo.half = fg_half(m, fo.nb[0]);
         CK(q3k_fgemv(&fo, s));
         q3_fg fg = {0};
         fg.K = H;
@@ -603,6 +613,7 @@ static int pass_fused(q3_model *m) {
         fg.ws0 = Lg->ws;
         fg.ws1 = Lu->ws;
         fg.y = m->yffn;
+        fg.half = fg_half(m, fg.nb[0]);
         CK(q3k_fgemv(&fg, s));
         q3_fg fd = {0};
         fd.K = F;
@@ -616,6 +627,7 @@ static int pass_fused(q3_model *m) {
         fd.row = m->yffn;
         fd.ws0 = Ld->ws;
         fd.x = m->x;
+        fd.half = fg_half(m, fd.nb[0]);
         CK(q3k_fgemv(&fd, s));
     }
     q3_nq fn = {0}; /* the residual add is done: plain final norm */

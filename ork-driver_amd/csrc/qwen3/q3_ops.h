@@ -116,6 +116,7 @@ typedef struct q3_fg {
     const float *ws0, *ws1; /* column scales (RESID: ws0; SWIGLU: gate ws0, up ws1) */
     float *x;       /* RESID: residual row, x[n] += (c * a_scale) * ws0[n], in place (not the row read) */
     float *y;       /* SWIGLU: output row, silu(g) * u (not the row read) */
+    int half;       /* 1: half a panel (8 columns) per workgroup, 2 x the panels' workgroups; 0: one panel each */
 } q3_fg;
 
 typedef struct q3_comb { /* grid NH: one head's chunks combined into an fp32 row */

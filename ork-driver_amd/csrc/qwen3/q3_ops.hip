@@ -635,7 +635,8 @@ __global__ void k_argmax(q3_amax p) {
 // ---- fused M = 1 matmul of the decode step ------------------------------------------------------------------
 // k_fgemv: one 16-column panel per workgroup (pair mode: the same columns of two weights), 8 waves splitting the
 // panel's K-blocks, on the library's resident layout (lane l of a 1 KiB block holds 16 bytes of column l % 16,
-// k-group l / 16). Around that GEMV:
+// k-group l / 16); with H, half a panel per workgroup (8 columns, twice the workgroups: the bytes spread evenly
+// over the CUs where whole panels would leave some CUs one panel and others two, or none). Around that GEMV:
 //   prologue: the int8 row, built in LDS by every workgroup: PRO_NORM = RMSNorm of the residual row then the
 //     per-row quant (norm_quant_body's operations with its 512-thread element mapping, so the sum of squares is
 //     rounded identically: elements past K add exact zeros, so any E >= K / 512 gives the same sums);
@@ -689,7 +690,7 @@ __device__ inline int fg_dot(v4i_t raw, const int *__restrict__ a, int acc, cons
 
 constexpr int FG_WAVES = 8; // 512 threads: norm_quant_body's element mapping
 
-template <int PRO, int EPI, int KIND, int E, int PRE>
+template <int PRO, int EPI, int KIND, int E, int PRE, int H>
 __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
     __shared__ __align__(16) int8_t arow[Q3_FG_KMAX];
     __shared__ __align__(16) float red[16];
@@ -700,8 +701,11 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = p.K, KB = p.KB;
 
-    // ---- this workgroup's panel(s) and this wave's K-blocks
-    int t = 0, pnl = blockIdx.x;
+    // ---- this workgroup's panel(s) and this wave's K-blocks; H: columns 8 hh .. 8 hh + 7 of the panel(s), lane l
+    // taking block kb + l / 32, k-group (l / 8) % 4, column 8 hh + l % 8 (a half block is four whole 128-byte lines)
+    int t = 0, pnl = H ? (int)(blockIdx.x >> 1) : (int)blockIdx.x;
+    const int hh = H ? (int)(blockIdx.x & 1) : 0, sub = H ? lane >> 5 : 0, grp = H ? (lane >> 3) & 3 : lane >> 4;
+    const int loff = H ? grp * 16 + hh * 8 + (lane & 7) : lane;
     if constexpr (!PAIR) {
         while (t < p.nt - 1 && pnl >= p.nb[t]) {
             pnl -= p.nb[t];
@@ -709,8 +713,8 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
         }
     }
     const int kbw = (KB + FG_WAVES - 1) / FG_WAVES, kb0 = min(wv * kbw, KB), kb1 = min(kb0 + kbw, KB);
-    const v4i_t *b0 = (const v4i_t *)p.B[t] + (size_t)pnl * KB * 64 + lane;
-    const v4i_t *b1 = PAIR ? (const v4i_t *)p.B[1] + (size_t)pnl * KB * 64 + lane : b0;
+    const v4i_t *b0 = (const v4i_t *)p.B[t] + (size_t)pnl * KB * 64 + loff;
+    const v4i_t *b1 = PAIR ? (const v4i_t *)p.B[1] + (size_t)pnl * KB * 64 + loff : b0;
     // ---- prologue: the int8 row in LDS
     float y[E], nw[E];
     load_row(y, p.row, K);
@@ -725,12 +729,13 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
             if (threadIdx.x + k * blockDim.x < (unsigned)K) mx = fmaxf(mx, fabsf(y[k]));
     }
     // the weight blocks, issued after the first use of the row (which waits for it); clamped to the wave's own
-    // last block, branch-free (a wave without blocks re-reads the panel's last one and discards it)
+    // last block, branch-free (a wave without blocks re-reads the panel's last one and discards it). H: PRE load
+    // instructions of two half blocks each
     v4i_t r0[PRE], r1[PRE];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < PRE; u++) {
-        const size_t o = (size_t)min(kb0 + u, kb1 - 1) * 64;
+        const size_t o = (size_t)min(kb0 + (H ? 2 * u + sub : u), kb1 - 1) * 64;
         r0[u] = __builtin_nontemporal_load(b0 + o);
         if constexpr (PAIR) r1[u] = __builtin_nontemporal_load(b1 + o);
     }
@@ -765,25 +770,57 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
 
     // ---- the GEMV: the preloaded blocks, then any further ones of this wave
     const FgLut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
-    const int aoff = (lane >> 4) * (KPB / 4);
+    const int aoff = grp * (KPB / 4);
     int acc0 = 0, acc1 = 0;
+    if constexpr (H) {
+        // a lane whose block lies past the run (the second half of an odd run's last instruction) adds nothing
 #pragma unroll
-    for (int u = 0; u < PRE; u++) {
-        if (kb0 + u < kb1) {
-            const int *a = (const int *)(arow + (kb0 + u) * KPB + aoff);
-            acc0 = fg_dot<KIND>(r0[u], a, acc0, L);
-            if constexpr (PAIR) acc1 = fg_dot<KIND>(r1[u], a, acc1, L);
+        for (int u = 0; u < PRE; u++) {
+            const int blk = kb0 + 2 * u + sub;
+            const bool ok = blk < kb1;
+            const int *a = (const int *)(arow + min(blk, kb1 - 1) * KPB + aoff);
+            const int d0 = fg_dot<KIND>(r0[u], a, 0, L);
+            acc0 += ok ? d0 : 0;
+            if constexpr (PAIR) {
+                const int d1 = fg_dot<KIND>(r1[u], a, 0, L);
+                acc1 += ok ? d1 : 0;
+            }
+        }
+        for (int kb = kb0 + 2 * PRE; kb < kb1; kb += 2) {
+            const int blk = kb + sub;
+            const bool ok = blk < kb1;
+            const size_t o = (size_t)min(blk, kb1 - 1) * 64;
+            const v4i_t s0 = __builtin_nontemporal_load(b0 + o);
+            v4i_t s1 = s0;
+            if constexpr (PAIR) s1 = __builtin_nontemporal_load(b1 + o);
+            const int *a = (const int *)(arow + min(blk, kb1 - 1) * KPB + aoff);
+            const int d0 = fg_dot<KIND>(s0, a, 0, L);
+            acc0 += ok ? d0 : 0;
+            if constexpr (PAIR) {
+                const int d1 = fg_dot<KIND>(s1, a, 0, L);
+                acc1 += ok ? d1 : 0;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < PRE; u++) {
+            if (kb0 + u < kb1) {
+                const int *a = (const int *)(arow + (kb0 + u) * KPB + aoff);
+                acc0 = fg_dot<KIND>(r0[u], a, acc0, L);
+                if constexpr (PAIR) acc1 = fg_dot<KIND>(r1[u], a, acc1, L);
+            }
+        }
+        for (int kb = kb0 + PRE; kb < kb1; kb++) {
+            const v4i_t s0 = __builtin_nontemporal_load(b0 + (size_t)kb * 64);
+            v4i_t s1 = s0;
+            if constexpr (PAIR) s1 = __builtin_nontemporal_load(b1 + (size_t)kb * 64);
+            const int *a = (const int *)(arow + kb * KPB + aoff);
+            acc0 = fg_dot<KIND>(s0, a, acc0, L);
+            if constexpr (PAIR) acc1 = fg_dot<KIND>(s1, a, acc1, L);
         }
     }
-    for (int kb = kb0 + PRE; kb < kb1; kb++) {
-        const v4i_t s0 = __builtin_nontemporal_load(b0 + (size_t)kb * 64);
-        v4i_t s1 = s0;
-        if constexpr (PAIR) s1 = __builtin_nontemporal_load(b1 + (size_t)kb * 64);
-        const int *a = (const int *)(arow + kb * KPB + aoff);
-        acc0 = fg_dot<KIND>(s0, a, acc0, L);
-        if constexpr (PAIR) acc1 = fg_dot<KIND>(s1, a, acc1, L);
-    }
-    // the four k-groups of a column are lanes l, l ^ 16, l ^ 32, l ^ 48; then the waves through LDS, in order
+    // the k-groups of a column are lanes l, l ^ 16, l ^ 32, l ^ 48 (H: l ^ 8, l ^ 16, ..., l ^ 56: blocks and
+    // k-groups); then the waves through LDS, in order
     {
         auto s32 = __builtin_amdgcn_permlane32_swap(acc0, acc0, false, false);
         acc0 += (int)((lane & 32) == 0 ? s32[1] : s32[0]);
@@ -795,13 +832,17 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
             auto t16 = __builtin_amdgcn_permlane16_swap(acc1, acc1, false, false);
             acc1 += (int)((lane & 16) == 0 ? t16[1] : t16[0]);
         }
+        if constexpr (H) {  // row_ror:8 -> lane l ^ 8 within its 16-lane row
+            acc0 += __builtin_amdgcn_update_dpp(0, acc0, 0x128, 0xF, 0xF, false);
+            if constexpr (PAIR) acc1 += __builtin_amdgcn_update_dpp(0, acc1, 0x128, 0xF, 0xF, false);
+        }
     }
-    if (lane < 16) {
+    if (lane < (H ? 8 : 16)) {
         racc[wv][0][lane] = acc0;
         racc[wv][1][lane] = acc1;
     }
     __syncthreads();
-    if (threadIdx.x >= 16) return;
+    if (threadIdx.x >= (H ? 8 : 16)) return;
     const int j = threadIdx.x;
     int c0 = 0, c1 = 0;
 #pragma unroll
@@ -813,7 +854,7 @@ __global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
         c0 >>= 4;
         c1 >>= 4;
     }
-    const int n = pnl * 16 + j;
+    const int n = pnl * 16 + hh * 8 + j;
     if constexpr (EPI == Q3_EPI_STORE) {
         p.C[t][n] = c0;
     } else if constexpr (EPI == Q3_EPI_RESID) {
@@ -860,12 +901,25 @@ inline int launch_ok() { return hipGetLastError() == hipSuccess ? 0 : -1; }
 
 // Fused M = 1 matmul (k_fgemv), the instantiations the decoder uses: PRO_NORM + STORE (q/k/v, int8), PRO_QUANT +
 // RESID (o, int8; down, int8 / uniform int4 / NF4), PRO_NORM + SWIGLU (gate/up pairs, int8 / uniform int4 / NF4).
-// E: row elements per thread, a bound of K / 512; PRE: the weight blocks per wave, a bound of its share.
+// E: row elements per thread, a bound of K / 512; PRE: the weight blocks per wave, a bound of its share (half
+// panels, q3_fg.half: the load instructions of two half blocks each that cover it).
 template <int PRO, int EPI, int KIND, int E>
 void fg_launch_pre(const q3_fg *p, int grid, int pre, hipStream_t s) {
-    if (pre <= 4) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 4>), dim3(grid), dim3(FG_WAVES * 64), 0, s, *p);
-    else if (pre <= 8) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 8>), dim3(grid), dim3(FG_WAVES * 64), 0, s, *p);
-    else hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 16>), dim3(grid), dim3(FG_WAVES * 64), 0, s, *p);
+    const dim3 b(FG_WAVES * 64);
+    if (p->half) {
+        // load instructions (two half blocks each) covering the wave's share: every count the decoder's shapes take
+        const int ni = (pre + 1) / 2, g2 = 2 * grid;
+        if (ni <= 1) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 1, 1>), dim3(g2), b, 0, s, *p);
+        else if (ni <= 2) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 2, 1>), dim3(g2), b, 0, s, *p);
+        else if (ni <= 3) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 3, 1>), dim3(g2), b, 0, s, *p);
+        else if (ni <= 4) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 4, 1>), dim3(g2), b, 0, s, *p);
+        else if (ni <= 6) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 6, 1>), dim3(g2), b, 0, s, *p);
+        else hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 8, 1>), dim3(g2), b, 0, s, *p);
+        return;
+    }
+    if (pre <= 4) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 4, 0>), dim3(grid), b, 0, s, *p);
+    else if (pre <= 8) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 8, 0>), dim3(grid), b, 0, s, *p);
+    else hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 16, 0>), dim3(grid), b, 0, s, *p);
 }
 template <int PRO, int EPI, int KIND> int fg_launch(const q3_fg *p, int grid, hipStream_t s) {
     const int e = (p->K + FG_WAVES * 64 - 1) / (FG_WAVES * 64), pre = (p->KB + FG_WAVES - 1) / FG_WAVES;
