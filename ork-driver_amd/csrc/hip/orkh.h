@@ -120,6 +120,12 @@ typedef struct orkh_plan {
 
 int orkh_mm_launch(const orkh_mm *p, const orkh_plan *plan, void *stream);
 
+/* Grouped tiled launch (multi-matmul submit, M > 1): n (2..ORKH_TGROUP_MAX) matmuls of one kind, one M and one K in
+ * a single k_tiled2 launch under one plan (algo ORKH_ALGO_TILED2, ksplit 1: the tile the planner picks for their
+ * columns together); each matmul keeps its own A, B, C, N and ldc. 0 / -2 inconsistent tasks or plan / -1 HIP. */
+#define ORKH_TGROUP_MAX 8
+int orkh_mm_launch_tgroup(const orkh_mm *p, int n, const orkh_plan *plan, void *stream);
+
 /* Grouped M = 1 launch (multi-matmul submit): n independent GEMVs of one kind (p.kind equal, p.M == 1)
  * in one launch. Task i covers workgroups [t[i].wg0, t[i].wg0 + p.N/16), wg0 ascending from 0 with no
  * gaps; each workgroup runs wpg waves over the whole K of one panel, kbw K-blocks per wave

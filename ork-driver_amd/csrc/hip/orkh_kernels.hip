@@ -26,6 +26,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <string.h>
 
 #include <atomic>
 #include <type_traits>
@@ -648,9 +649,11 @@ struct T2Group {
     const float *bS;  // [K/G][N]
 };
 
+// bid, nT: this workgroup's index among the launch's nT workgroups of this matmul (blockIdx.x and gridDim.x, or a
+// task's share of a grouped launch, which starts at a multiple of 8 so that bid % 8 is still the XCD)
 template <int KIND, int BM, int BN, int KS, int GR, bool AL>
 __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int ntiles_all, int kbs, void *ws,
-                                            const T2Group &gp) {
+                                            const T2Group &gp, int bid, int nT) {
 #pragma clang fp contract(off)
     using T = KT<KIND>;
     using P = T2<KIND, BM, BN, KS, t2_xg<KIND, BM, BN, GR>()>;
@@ -666,7 +669,6 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     const int wm = wr % P::WM, wn = wr / P::WM;
     // XCD-aware order: WG b runs on XCD b%8; each XCD gets a contiguous run of tiles, M fastest, so every
     // M-tile that reads a given B column panel shares one L2.
-    const int nT = gridDim.x, bid = blockIdx.x;
     const int per = nT / 8, rem = nT % 8, x = bid % 8, j = bid / 8;
     const int tl = (x < rem) ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
     int ks, tile, tn, tm;
@@ -916,7 +918,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
 
     // epilogue: one 64-bit base per lane (its first row and column), 32-bit offsets from it
     const int mr0 = m0 + wm * P::MTW * 16 + (lane >> 4) * 4, nc0 = (nb0 + wn * P::NTW) * 16 + (lane & 15);
-    const bool split = !GR && gridDim.x > ntiles_all;
+    const bool split = !GR && nT > ntiles_all;
     const size_t ldc = split ? (size_t)p.N : (size_t)p.ldc;
     using o_t = typename std::conditional<GR != 0, float, c_t>::type;
     o_t *Cl = (split ? (o_t *)ws + (size_t)ks * p.M * p.N : (o_t *)p.C) + (size_t)mr0 * ldc + nc0;
@@ -937,7 +939,27 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
 
 template <int KIND, int BM, int BN, int KS, bool AL>
 __global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntiles_all, int kbs, void *ws) {
-    tiled2_body<KIND, BM, BN, KS, 0, AL>(p, mtiles, ntiles_all, kbs, ws, T2Group{0, nullptr, nullptr});
+    tiled2_body<KIND, BM, BN, KS, 0, AL>(p, mtiles, ntiles_all, kbs, ws, T2Group{0, nullptr, nullptr}, (int)blockIdx.x,
+                                         (int)gridDim.x);
+}
+
+// k_tiled2m: up to ORKH_TGROUP_MAX matmuls of one kind, M and K in one launch (the multi-matmul submit): task t's
+// tiles are workgroups [wg0[t], wg0[t] + tiles), each start a multiple of 8; the padding workgroups before the next
+// start exit at once.
+struct T2Multi {
+    int n;
+    int wg0[ORKH_TGROUP_MAX];
+    int mtiles[ORKH_TGROUP_MAX], tiles[ORKH_TGROUP_MAX];
+    orkh_mm p[ORKH_TGROUP_MAX];
+};
+template <int KIND, int BM, int BN, int KS, bool AL>
+__global__ __launch_bounds__(1024) void k_tiled2m(T2Multi g) {
+    int t = 0;
+    while (t + 1 < g.n && (int)blockIdx.x >= g.wg0[t + 1]) t++;
+    const int local = (int)blockIdx.x - g.wg0[t];
+    if (local >= g.tiles[t]) return;
+    tiled2_body<KIND, BM, BN, KS, 0, AL>(g.p[t], g.mtiles[t], g.tiles[t], g.p[t].KB, nullptr, T2Group{0, nullptr, nullptr},
+                                         local, g.tiles[t]);
 }
 
 // Grouped runs (never K-split: the groups close in order inside one workgroup). GR 2: every group is whole
@@ -945,7 +967,7 @@ __global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntil
 // GR 1: any G % 32 == 0, walked K-block by K-block.
 template <int KIND, int BM, int BN, int KS, int GR, bool AL>
 __global__ __launch_bounds__(1024) void k_tiled2g(orkh_mm p, int mtiles, int ntiles_all, T2Group gp) {
-    tiled2_body<KIND, BM, BN, KS, GR, AL>(p, mtiles, ntiles_all, p.KB, nullptr, gp);
+    tiled2_body<KIND, BM, BN, KS, GR, AL>(p, mtiles, ntiles_all, p.KB, nullptr, gp, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // Dynamic LDS of k_tiled: KG groups x 2 stage buffers of A fragments, or (KG > 1) the 4-wave partial
@@ -1300,6 +1322,46 @@ int launch_tiled2_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     return 0;
 }
 
+template <int KIND, int BM, int BN>
+int launch_tiled2m_v(T2Multi &g, const orkh_plan *q, hipStream_t s) {
+    constexpr int XG = t2_xg<KIND, BM, BN, 0>();
+    constexpr int KS = t2_ks<KIND, BM, BN, XG>();
+    using P = T2<KIND, BM, BN, KS, XG>;
+    const bool al = q->aline && P::LINE_OK;
+    auto kern = al ? k_tiled2m<KIND, BM, BN, KS, true> : k_tiled2m<KIND, BM, BN, KS, false>;
+    static lds_flags attr[2];
+    if (lds_limit((const void *)kern, (int)P::LDS, attr[al])) return -1;
+    long wg = 0;
+    for (int t = 0; t < g.n; t++) {
+        const orkh_mm &p = g.p[t];
+        g.mtiles[t] = (p.M + BM - 1) / BM;
+        g.tiles[t] = g.mtiles[t] * ((p.N / 16 + P::NB - 1) / P::NB);
+        g.wg0[t] = (int)wg;
+        wg += ((long)g.tiles[t] + 7) / 8 * 8;
+    }
+    if (wg >= (1L << 24)) {
+        snprintf(g_lerr, sizeof g_lerr, "tiled2 group: %ld workgroups", wg);
+        return -2;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)wg), dim3(1024), P::LDS, s, g);
+    return 0;
+}
+
+template <int KIND>
+int launch_tiled2m(T2Multi &g, const orkh_plan *q, hipStream_t s) {
+    if (q->bm == 256 && q->bn == 256) return launch_tiled2m_v<KIND, 256, 256>(g, q, s);
+    if (q->bm == 128 && q->bn == 128) return launch_tiled2m_v<KIND, 128, 128>(g, q, s);
+    if (q->bm == 128 && q->bn == 96) return launch_tiled2m_v<KIND, 128, 96>(g, q, s);
+    if (q->bm == 64 && q->bn == 192) return launch_tiled2m_v<KIND, 64, 192>(g, q, s);
+    if (q->bm == 64 && q->bn == 64) return launch_tiled2m_v<KIND, 64, 64>(g, q, s);
+    if (q->bm == 32 && q->bn == 64) return launch_tiled2m_v<KIND, 32, 64>(g, q, s);
+    if (q->bm == 32 && q->bn == 32) return launch_tiled2m_v<KIND, 32, 32>(g, q, s);
+    if (q->bm == 16 && q->bn == 64) return launch_tiled2m_v<KIND, 16, 64>(g, q, s);
+    if (q->bm == 16 && q->bn == 32) return launch_tiled2m_v<KIND, 16, 32>(g, q, s);
+    snprintf(g_lerr, sizeof g_lerr, "tiled2 group plan: %dx%d unsupported", q->bm, q->bn);
+    return -2;
+}
+
 template <int KIND>
 int launch_tiled(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     if (q->ksplit > 1 && (!q->ws || (long)q->ksplit * q->kbs < p->KB)) {
@@ -1391,6 +1453,42 @@ extern "C" int orkh_mm_launch(const orkh_mm *p, const orkh_plan *q, void *stream
     }
     if (rc) return rc;
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_lerr, sizeof g_lerr, "launch: %s", hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" int orkh_mm_launch_tgroup(const orkh_mm *p, int n, const orkh_plan *q, void *stream) {
+    g_lerr[0] = 0;
+    if (n < 2 || n > ORKH_TGROUP_MAX || !p || !q || q->algo != ORKH_ALGO_TILED2 || q->ksplit > 1) {
+        snprintf(g_lerr, sizeof g_lerr, "tiled2 group: n=%d or plan (algo %d, ksplit %d) unsupported", n, q ? q->algo : -1,
+                 q ? q->ksplit : 0);
+        return -2;
+    }
+    T2Multi g;
+    memset(&g, 0, sizeof g);
+    g.n = n;
+    for (int t = 0; t < n; t++) {
+        if (p[t].kind != p[0].kind || p[t].M != p[0].M || p[t].K != p[0].K || p[t].KB != p[0].KB || p[t].M < 1 ||
+            (p[t].N & 15) || p[t].N < 16) {
+            snprintf(g_lerr, sizeof g_lerr, "tiled2 group: task %d differs in kind, M or K, or has N=%d", t, p[t].N);
+            return -2;
+        }
+        g.p[t] = p[t];
+    }
+    hipStream_t s = (hipStream_t)stream;
+    int rc;
+    switch (p[0].kind) {
+    case ORKH_I8: rc = launch_tiled2m<ORKH_I8>(g, q, s); break;
+    case ORKH_I4U: rc = launch_tiled2m<ORKH_I4U>(g, q, s); break;
+    case ORKH_NF4: rc = launch_tiled2m<ORKH_NF4>(g, q, s); break;
+    case ORKH_F16: rc = launch_tiled2m<ORKH_F16>(g, q, s); break;
+    default: snprintf(g_lerr, sizeof g_lerr, "tiled2 group: kind %d", p[0].kind); return -2;
+    }
+    if (rc) return rc;
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_lerr, sizeof g_lerr, "launch: %s", hipGetErrorString(e));
         return -1;

@@ -6,7 +6,9 @@
  * independent matmuls, each result equal to its single run; -2 for bad arguments (S outside 1..1024,
  * NULL weight, M < 1, wrong dtype), -1 for A/C overlap; C row stride override (cstride) for int8.
  * What changes: no PC-chained NPU programs, cores or doorbells. Every M = 1 task of one resident kind
- * goes into a grouped GEMV launch (ORKH_GROUP_MAX tasks each), the remaining tasks launch back to back
+ * goes into a grouped GEMV launch (ORKH_GROUP_MAX tasks each); tasks of one integer kind, M > 1 and K whose summed
+ * columns plan to the LDS-ring kernel unsplit go into one grouped tiled launch (ORKH_TGROUP_MAX each: a
+ * prefill's q/k/v or gate/up); the remaining tasks launch back to back
  * on the context's stream with their normal plans, and host operands move in one pinned staging pass. An
  * offline context runs each task's host codes on the CPU (cpu_chain below), as the reference's int8 chain
  * and int4 chain / stream do; its int8 stream and fp16 stream have no offline branch and return -1 here too. */
@@ -133,6 +135,43 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
             done[j] = 1;
         }
         if (orkh_mm_launch_group(&g, wpg, c->stream)) { orki_hip_fail(who); rc = -1; }
+    }
+    /* grouped tiled launches: tasks of one integer resident kind, M > 1 and K whose columns together plan to the
+     * LDS-ring kernel unsplit, ORKH_TGROUP_MAX at a time, under the tile planned for their summed N (integer results
+     * are exact under any tile; fp16 tasks keep their own tiles, so each result still equals its single run) */
+    for (int i = 0; i < S && !rc; i++) {
+        if (done[i] || t[i].M == 1 || t[i].w->rkind == ORKH_F16) continue;
+        int mem[ORKH_TGROUP_MAX], n = 0, nsum = 0;
+        for (int j = i; j < S && n < ORKH_TGROUP_MAX; j++) {
+            if (done[j] || t[j].M != t[i].M || t[j].w->rkind != t[i].w->rkind || t[j].w->K != t[i].w->K ||
+                t[j].w->KB != t[i].w->KB)
+                continue;
+            mem[n++] = j;
+            nsum += t[j].w->N;
+        }
+        if (n < 2) continue;
+        orkh_plan gq;
+        size_t gws = 0;
+        orki_plan(c, t[i].w->rkind, t[i].M, t[i].w->K, nsum, t[i].w->KB, &gq, &gws);
+        if (gq.algo != ORKH_ALGO_TILED2 || gq.ksplit > 1) continue;
+        orkh_mm ps[ORKH_TGROUP_MAX];
+        memset(ps, 0, sizeof ps);
+        for (int k = 0; k < n; k++) {
+            const ctask *tk = &t[mem[k]];
+            ps[k].kind = tk->w->rkind;
+            ps[k].M = tk->M;
+            ps[k].K = tk->w->K;
+            ps[k].N = tk->w->N;
+            ps[k].KB = tk->w->KB;
+            ps[k].A = tk->dA;
+            ps[k].lda = tk->w->K;
+            ps[k].B = tk->w->dB;
+            ps[k].C = tk->dC;
+            ps[k].ldc = tk->c_dev ? tk->ldc : tk->w->N;
+            memcpy(ps[k].lut, tk->w->lut, sizeof ps[k].lut);
+        }
+        if (orkh_mm_launch_tgroup(ps, n, &gq, c->stream)) { orki_hip_fail(who); rc = -1; }
+        for (int k = 0; k < n; k++) done[mem[k]] = 1;
     }
     for (int i = 0; i < S && !rc; i++) {
         if (done[i]) continue;

@@ -122,11 +122,48 @@ def test_i8_chain_host_c_staging(npu, rows_big):
         ork.free(w)
 
 
+@pytest.mark.parametrize("entry", ["ork_i8_mm_run_chain", "ork_i8_mm_run_stream"])
+def test_i8_chain_grouped_tiled(npu, entry):
+    """Tasks of one kind, M > 1 and K run as one grouped tiled launch (up to 8 per launch, under the tile planned for
+    their summed columns): every result exact against the oracle, as its single run. A prefill's q/k/v shapes, N tails,
+    more tasks of one shape than a launch holds, uniform-int4 and NF4 pairs, a C row stride, and tasks of other
+    shapes between them."""
+    _say(entry, "grouped tiled")
+    rng = np.random.default_rng(74)
+    specs = []  # (w, codes[K][N], M, cstride)
+    for M, K, N in [(128, 2048, 2048), (128, 2048, 1024), (40, 512, 96), (128, 2048, 1024), (96, 512, 416),
+                    (96, 512, 32), (96, 512, 96), (130, 1056, 64)] + [(70, 256, 160)] * 9:
+        B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+        specs.append((npu.pack_i8(B), B, M, N + (16 if M == 96 else 0)))
+    for nf4 in (0, 1):
+        for N in (256, 512):
+            w, codes = _i4a8(npu, rng, 1024, N, nf4)
+            specs.append((w, codes, 200, N))
+    rows, refs, outs = [], [], []
+    for w, codes, M, ldc in specs:
+        assert w
+        K, N = codes.shape
+        A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+        Cb = np.full((M, ldc), -7, np.int32)
+        rows.append((w, M, A, Cb, ldc))
+        refs.append(O.gemm_i32(A, codes))
+        outs.append(Cb)
+    t = ork.tasks(ork.TaskI8, rows)
+    assert getattr(ork.lib(), entry)(npu.h, len(rows), t) == 0
+    for i, (Cb, R) in enumerate(zip(outs, refs)):
+        N = R.shape[1]
+        assert np.array_equal(Cb[:, :N], R), (i, specs[i][2], R.shape)
+        assert np.all(Cb[:, N:] == -7), i
+    for w, *_ in specs:
+        ork.free(w)
+
+
 @pytest.mark.parametrize("entry", ["ork_i4_mm_run_chain", "ork_i4_mm_run_stream"])
 def test_i4_chain(npu, entry):
     _say(entry)
     rows, refs, ws = [], [], []
-    for M, K, N in [(1, 2048, 256), (1, 64, 64), (3, 512, 128), (1, 12288, 64), (128, 512, 256)]:
+    for M, K, N in [(1, 2048, 256), (1, 64, 64), (3, 512, 128), (1, 12288, 64), (128, 512, 256), (128, 512, 512),
+                    (128, 512, 64)]:
         A, B = O.gen_i4_test(M, K, N)
         w = npu.pack_i4(B)
         assert w
