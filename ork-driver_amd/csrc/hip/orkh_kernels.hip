@@ -458,6 +458,102 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const c_t *ws, c_t *C, in
 // scaled terms are summed in ascending group order -- the float sequence of the reference's grouped
 // accumulate (src/npu/core/buf.c:501-520): c = 0; c = c + ((float)P_g * aS[m][g]) * bS[g][n], no fused
 // multiply-adds.
+// k_grouped_gemv: grouped scales at M = 1 on half panels (k_gemv_half's data flow): grid N/8, WPG waves, wave w a
+// run of kbw K-blocks loaded NI instructions (two half blocks each) at a time. A lane's 16 (int8) or 32 (nibble
+// kinds) k lie in one K-group (G % 32 == 0), so each dot product is added exactly, as int32, into that group's and
+// column's partial in LDS (order-free). Then every thread forms some of the scaled terms ((float)P_g * aS[g]) *
+// bS[g][n], their scales loaded at the start, and 8 threads add them in ascending g: k_grouped's operations in its
+// order (src/npu/core/buf.c:501-520), so the results are bit-identical.
+#define ORKH_GGEMV_SK_MAX 512
+template <int KIND, int WPG, int NI>
+__global__ __launch_bounds__(WPG * 64) void k_grouped_gemv(orkh_mm p, int G, const float *aS, const float *bS, float *C,
+                                                          int kbw) {
+#pragma clang fp contract(off)
+    using T = KT<KIND>;
+    constexpr int W = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 8 : 4; // activation dwords per k-group per block
+    constexpr int NT = WPG * 64, SPT = ORKH_GGEMV_SK_MAX * 8 / NT;    // scaled terms per thread, at most
+    __shared__ int P[ORKH_GGEMV_SK_MAX * 8];                           // [group][column]: int32 partials, then terms
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = blockIdx.x >> 1, h = blockIdx.x & 1, n0 = nb * 16 + h * 8;
+    const int Sk = p.K / G, nterm = Sk * 8;
+    // this thread's terms' scales, requested first (term e = group e / 8, column e % 8)
+    float sa[SPT], sb[SPT];
+#pragma unroll
+    for (int q = 0; q < SPT; q++) {
+        if (q * NT >= nterm) break; // workgroup-uniform: only the rounds that hold terms
+        const int e = min((int)threadIdx.x + q * NT, nterm - 1);
+        sa[q] = aS[e >> 3];
+        sb[q] = bS[(size_t)(e >> 3) * p.N + n0 + (e & 7)];
+    }
+    for (int e = threadIdx.x; e < nterm; e += NT) P[e] = 0;
+    __syncthreads();
+    const int kb0 = w * kbw, kb1 = min(kb0 + kbw, p.KB);
+    const int g4 = (lane >> 3) & 3, sub = lane >> 5, col = lane & 7;
+    const v4i *bp = (const v4i *)p.B + (size_t)nb * p.KB * 64 + g4 * 16 + h * 8 + col;
+    const char *A = (const char *)p.A;
+    const Lut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
+    // a lane's dot products run on while its group stays the same; where every block lies in one group (G a multiple
+    // of the block's k, so K has no tail inside a block and a 32-lane half's lanes always share their group) the four
+    // k-group lanes of a column are summed first (l ^ 8, l ^ 16), and one of them adds the sum
+    const bool whole = G % T::KPB == 0;
+    int run = 0, rg = -1;
+    auto flush = [&]() {
+        int v = run;
+        if (whole) {
+            v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false); // row_ror:8 -> lane l ^ 8
+            const auto sw = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+            v += (int)((lane & 16) == 0 ? sw[1] : sw[0]);
+        }
+        if (rg >= 0 && (!whole || g4 == 0)) atomicAdd(&P[rg * 8 + col], v);
+    };
+    for (int kb = kb0; kb < kb1; kb += 2 * NI) {
+        v4i raw[NI], act[NI][W / 4];
+        bool ok[NI];
+#pragma unroll
+        for (int q = 0; q < NI; q++)
+            raw[q] = __builtin_nontemporal_load(bp + (size_t)min(kb + 2 * q + sub, kb1 - 1) * 64);
+#pragma unroll
+        for (int q = 0; q < NI; q++) {
+            const int blk = kb + 2 * q + sub, k0 = blk * T::KPB + g4 * (W * 4);
+            ok[q] = blk < kb1 && k0 < p.K;
+#pragma unroll
+            for (int j = 0; j < W / 4; j++) act[q][j] = *(const v4i *)(A + (ok[q] ? k0 + 16 * j : 0));
+        }
+#pragma unroll
+        for (int q = 0; q < NI; q++) {
+            v4i op[T::STEPS];
+            decode<KIND>(raw[q], op, L);
+            int dot = 0;
+#pragma unroll
+            for (int d = 0; d < W; d++) dot = __builtin_amdgcn_sdot4(act[q][d / 4][d % 4], op[d / 4][d % 4], dot, false);
+            const int g = ok[q] ? ((kb + 2 * q + sub) * T::KPB + g4 * (W * 4)) / G : rg; // past the run: adds 0 to rg
+            if (g != rg) { // uniform across a 32-lane half when whole, since its lanes share the block
+                flush();
+                run = 0;
+                rg = g;
+            }
+            run += ok[q] ? dot : 0;
+        }
+    }
+    flush();
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < SPT; q++) {
+        if (q * NT >= nterm) break;
+        const int e = (int)threadIdx.x + q * NT;
+        if (e < nterm) {
+            const float t = ((float)finish<KIND>(P[e]) * sa[q]) * sb[q];
+            P[e] = __builtin_bit_cast(int, t);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        float c = 0.0f;
+        for (int g = 0; g < Sk; g++) c = c + __builtin_bit_cast(float, P[g * 8 + threadIdx.x]);
+        C[n0 + threadIdx.x] = c;
+    }
+}
+
 // k_grouped: grid (N/16, row tiles of 16*MT), 4 waves. Workgroup (nb, mtile) owns panel nb and walks its
 // K-groups QG at a time: wave w computes groups w, w+4, ... of the chunk over the blocks holding
 // k in [g*G, g*G + G) (every A chunk is 16 k wide and 16-k aligned and G % 32 == 0, so a chunk lies wholly
@@ -1597,7 +1693,28 @@ extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *q, int 
                  p->N, G, ldc, q->algo);
         return -2;
     }
-    if (q->algo == ORKH_ALGO_TILED2) {
+    if (q->algo == ORKH_ALGO_GEMV) {
+        const int need = (q->kbw + 1) / 2, ni = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+        if (p->M != 1 || p->K / G > ORKH_GGEMV_SK_MAX || q->kbw < 1 || (q->wpg != 2 && q->wpg != 4 && q->wpg != 8) ||
+            (q->kbw * q->wpg < p->KB)) {
+            snprintf(g_lerr, sizeof g_lerr, "grouped gemv: M %d K/G %d wpg %d kbw %d", p->M, p->K / G, q->wpg, q->kbw);
+            return -2;
+        }
+        const dim3 grid((unsigned)(p->N / 8)), block(q->wpg * 64);
+#define ORKH_GG(KIND, W_, N_) hipLaunchKernelGGL((k_grouped_gemv<KIND, W_, N_>), grid, block, 0, s, *p, G, aS, bS, C, q->kbw)
+#define ORKH_GGW(KIND, W_) do { if (ni == 1) ORKH_GG(KIND, W_, 1); else if (ni == 2) ORKH_GG(KIND, W_, 2); \
+                                else if (ni == 4) ORKH_GG(KIND, W_, 4); else ORKH_GG(KIND, W_, 8); } while (0)
+#define ORKH_GGK(KIND) do { if (q->wpg == 2) ORKH_GGW(KIND, 2); else if (q->wpg == 4) ORKH_GGW(KIND, 4); \
+                            else ORKH_GGW(KIND, 8); } while (0)
+        switch (p->kind) {
+        case ORKH_I8: ORKH_GGK(ORKH_I8); break;
+        case ORKH_I4U: ORKH_GGK(ORKH_I4U); break;
+        default: ORKH_GGK(ORKH_NF4); break;
+        }
+#undef ORKH_GGK
+#undef ORKH_GGW
+#undef ORKH_GG
+    } else if (q->algo == ORKH_ALGO_TILED2) {
         orkh_mm pc = *p;
         pc.C = C;
         pc.ldc = ldc;

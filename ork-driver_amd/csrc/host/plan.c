@@ -381,6 +381,20 @@ void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB,
         }
         memset(q, 0, sizeof *q);
     }
+    /* one row: the half-panel VALU kernel (k_grouped_gemv) where the groups' partials fit its LDS (K/G <= 512), runs
+     * as the GEMV's (ORK_PLAN=stream keeps k_grouped). Graph-timed against k_grouped (us): W4A4 K=N=4096 G=128
+     * 9.6 -> 4.4; int8 K=2048 N=6144 G=128 7.9 -> 4.7; int8 K=2048 N=16384 G=512 8.1 -> 7.5 */
+    if (M == 1 && K / G <= 512 && !(force && !strcmp(force, "stream"))) {
+        q->algo = ORKH_ALGO_GEMV;
+        q->mt = 1;
+        q->ksplit = 1;
+        q->kbs = KB;
+        q->half = 1;
+        const int need = cdiv(KB, rkind == ORKH_NF4 ? 4 : 8);
+        q->wpg = need <= 2 ? 2 : need <= 4 ? 4 : 8;
+        q->kbw = cdiv(KB, q->wpg);
+        return;
+    }
     q->algo = ORKH_ALGO_STREAM;
     q->mt = M > 16 ? 4 : 1;
     q->ksplit = 1;

@@ -270,6 +270,7 @@ const char *ork_w_grouped_plan_name(ork_npu *c, const ork_w *w, int M) {
     orki_plan_grouped(c, w->rkind, M, w->K, w->N, w->KB, w->gsize, &q);
     const char *k = w->rkind == ORKH_I8 ? "i8" : w->rkind == ORKH_I4U ? "i4u" : "nf4";
     if (q.algo == ORKH_ALGO_TILED2) snprintf(b, sizeof b, "tiled2g_%s_%dx%d", k, q.bm, q.bn);
+    else if (q.algo == ORKH_ALGO_GEMV) snprintf(b, sizeof b, "grouped_%s_gemvh_w%d", k, q.wpg);
     else snprintf(b, sizeof b, "grouped_%s_mt%d", k, q.mt);
     return b;
 }

@@ -246,14 +246,16 @@ def test_grouped_tiled_exact(npu, tile, kind, M, K, N, G):
 
 
 def test_grouped_plan_names(npu):
-    """Default plans: few rows stream panels (k_grouped); int8 / uniform int4 take the LDS-ring kernel from 32
-    rows when G % 128 == 0 and from 128 rows otherwise; NF4 always streams."""
+    """Default plans: one row runs the half-panel VALU kernel (k_grouped_gemv), a few rows stream panels
+    (k_grouped); int8 / uniform int4 take the LDS-ring kernel from 32 rows when G % 128 == 0 and from 128 rows
+    otherwise; NF4 always streams."""
     L = ork.lib()
     B = np.zeros((1024, 256), np.int8)
     w = npu.pack_i8(B)
     assert npu.grouped_plan_name(w, 8) == "none"  # no group size yet
     assert L.ork_w_set_group(w, 128) == 0
-    assert npu.grouped_plan_name(w, 8).startswith("grouped_i8_")
+    assert npu.grouped_plan_name(w, 1).startswith("grouped_i8_gemvh_")  # one row: the half-panel VALU kernel
+    assert npu.grouped_plan_name(w, 8).startswith("grouped_i8_mt")
     assert npu.grouped_plan_name(w, 31).startswith("grouped_i8_")
     assert npu.grouped_plan_name(w, 32).startswith("tiled2g_i8_")
     assert L.ork_w_set_group(w, 64) == 0
@@ -282,3 +284,46 @@ def test_grouped_default_plan_exact(npu):
     rc, C = _run(L.ork_i4_mm_run_grouped, npu, w, A, aS, bS)
     assert rc == 0 and np.array_equal(C, O.gemm_grouped(A, B, aS, bS, G))
     L.ork_mm_free(npu.h, w)
+
+
+@pytest.mark.parametrize("kind", ["w4a4", "i8", "i4a8", "nf4"])
+def test_grouped_one_row_exact(npu, kind):
+    """One row (k_grouped_gemv: half panels, int32 group partials summed in LDS, scaled terms added in ascending
+    group order) bit for bit against the oracle and against the panel-streaming kernel (ORK_PLAN=stream), over
+    group sizes below, equal to and above a K-block, K tails inside a group and up to 512 groups."""
+    _say("grouped one row", kind)
+    L = ork.lib()
+    rng = np.random.default_rng(77 + len(kind))
+    for K, N, G in [(2048, 256, 32), (4096, 512, 128), (1024, 1024, 64), (1056, 256, 96), (2048, 384, 512),
+                    (16384, 128, 32)]:
+        if kind == "w4a4":
+            A, B, aS, bS = _gtest_inputs(1, K, N, G)
+            w = L.ork_i4_mm_pack_grouped(npu.h, K, N, ork.ptr(B), G)
+            fn = L.ork_i4_mm_run_grouped
+            codes = B
+        else:
+            A = rng.integers(-127, 128, size=(1, K), dtype=np.int8)
+            aS = rng.uniform(1e-3, 1e-2, size=(1, K // G)).astype(np.float32)
+            bS = rng.uniform(1e-3, 1e-2, size=(K // G, N)).astype(np.float32)
+            if kind == "i8":
+                codes = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+                w = npu.pack_i8(codes)
+            else:
+                W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+                if kind == "nf4":
+                    os.environ["ORK_NF4"] = "1"
+                try:
+                    w, _ = npu.pack_i4a8(W)
+                finally:
+                    os.environ.pop("ORK_NF4", None)
+                _, _, codes = O.pack_i4a8(W, nf4=kind == "nf4")
+            assert L.ork_w_set_group(w, G) == 0
+            fn = L.ork_i8_mm_run_grouped
+        assert w, (kind, K, N, G)
+        name = npu.grouped_plan_name(w, 1)
+        assert name.startswith("grouped_") and "_gemvh_" in name, name
+        rc, C = _run(fn, npu, w, A, aS, bS)
+        assert rc == 0 and np.array_equal(C, O.gemm_grouped(A, codes, aS, bS, G)), (kind, K, N, G, name)
+        rc2, C2 = _env_run({"ORK_PLAN": "stream"}, fn, npu, w, A, aS, bS)
+        assert rc2 == 0 and np.array_equal(C2, C), (kind, K, N, G)
+        L.ork_mm_free(npu.h, w)
