@@ -434,9 +434,13 @@ static int pass(q3_model *m, int M, int decode) {
                                  {Ly->l[Q3_WK].w, M, m->a8x, m->ck, 0},
                                  {Ly->l[Q3_WV].w, M, m->a8x, m->cv, 0}};
         CK(ork_i8_mm_run_chain(m->ctx, 3, qkv));
-        q3_att at = {.M = M, .NH = NH, .NKV = NKV, .HD = HD, .S = m->S, .max_ctx = c->max_ctx, .q = m->q,
-                     .kc = Ly->kc, .vc = Ly->vc, .st = m->st, .scale = 1.0f / sqrtf((float)HD), .part = m->part,
-                     .rows = m->fused};
+        /* A prefill starts at position 0, so its rows see at most M keys: its attention covers the first
+         * ceil(M / Q3_CHUNK) chunks only. The chunks past them would hold empty partials (max -inf, sum 0,
+         * P.V 0), which add exact zeros to the combine's sums, so the rows are the same bit for bit. */
+        const int Sa = decode ? m->S : (M + Q3_CHUNK - 1) / Q3_CHUNK;
+        q3_att at = {.M = M, .NH = NH, .NKV = NKV, .HD = HD, .S = Sa, .max_ctx = decode ? c->max_ctx : M,
+                     .q = m->q, .kc = Ly->kc, .vc = Ly->vc, .st = m->st, .scale = 1.0f / sqrtf((float)HD),
+                     .part = m->part, .rows = m->fused};
         if (M == 1) { /* one row: attention does the q/k/v post-processing itself */
             at.cq = m->cq;
             at.ck = m->ck;
@@ -457,7 +461,7 @@ static int pass(q3_model *m, int M, int decode) {
             CK(q3k_qkv_post(&qp, s));
         }
         CK(q3k_attn_part(&at, s));
-        const q3_aq aq = {M, NH, HD, m->S, m->part, m->a8att, m->asatt};
+        const q3_aq aq = {M, NH, HD, Sa, m->part, m->a8att, m->asatt};
         CK(q3k_attn_quant(&aq, s));
         CK(ork_i8_mm_run(m->ctx, Ly->l[Q3_WO].w, M, m->a8att, m->co));
         q3_nq n2 = nq;
