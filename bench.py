@@ -90,8 +90,9 @@ class Hip:
         return ms.value
 
 
-def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scales=None, outer=None):
-    """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % len(ws)] through `entry`; the
+def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scales=None, outer=None, call=None):
+    """Returns (graph ms/step, eager ms/step). Step i runs weight ws[i % len(ws)] through `entry` (or, given
+    `call`, runs call(ws[i % len(ws)])); the
     grouped entry points also take the device scale buffers `scales` = (aScale, bScale). With fewer timed
     steps than weights, a second graph streams the weights outside the timed set (ws[steps:]) right before
     the timed replay, so the timed weights are as cold as in a full rotation.
@@ -107,7 +108,7 @@ def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scale
     mid = tuple(scales) if scales else ()
 
     def run(i):
-        rc = fn(npu.h, ws[i % len(ws)], M, dA, *mid, dC)
+        rc = call(ws[i % len(ws)]) if call else fn(npu.h, ws[i % len(ws)], M, dA, *mid, dC)
         if rc:
             raise RuntimeError(f"{entry} rc={rc}")
 
@@ -186,6 +187,35 @@ def measure_copy(hip, L, npu, nbytes, steps, warmup=8):
     hip.L.hipGraphDestroy(g)
     for b in bufs + [dst]:
         L.ork_dev_free(npu.h, b)
+    return ms
+
+
+def measure_read(npu, hip, L, ws, dA, dC, steps, warmup):
+    """ms per plain streaming read of a weight's panel bytes (ork_npu_read_probe: the M = 1 GEMV's loads without its
+    arithmetic), in measure()'s graph harness over the same rotation: what reading the bytes alone costs per launch.
+    The probe's XOR words of the first weight are checked against the host's XOR of its panel bytes."""
+    import ork
+
+    sink = L.ork_dev_alloc(npu.h, 1 << 20)
+    assert sink
+    pan = []
+    for w in ws:
+        p, kb, kind, lut = C.c_void_p(), C.c_int(), C.c_int(), (C.c_uint32 * 4)()
+        kk, nn = C.c_int(), C.c_int()
+        L.ork_w_dims(w, C.byref(kk), C.byref(nn))
+        assert L.ork_w_device_panels(w, C.byref(p), C.byref(kb), C.byref(kind), lut) == 0
+        pan.append((p.value, (nn.value // 16) * kb.value * 1024))
+    nb = pan[0][1]
+    host = np.empty(nb, np.uint8)
+    assert L.ork_dev_download(npu.h, ork.ptr(host), pan[0][0], nb) == 0
+    n = L.ork_npu_read_probe(npu.h, pan[0][0], nb, sink)
+    assert n > 0 and L.ork_npu_sync(npu.h) == 0
+    words = np.empty(n, np.uint32)
+    assert L.ork_dev_download(npu.h, ork.ptr(words), sink, 4 * n) == 0
+    assert np.bitwise_xor.reduce(words) == np.bitwise_xor.reduce(host.view(np.uint32)), "read probe missed bytes"
+    ms, _ = measure(npu, hip, pan, 1, dA, dC, steps, warmup, call=lambda pb: 0 if L.ork_npu_read_probe(
+        npu.h, pb[0], pb[1], sink) > 0 else 1)
+    L.ork_dev_free(npu.h, sink)
     return ms
 
 
@@ -668,7 +698,7 @@ def main():
         print(f"[bench] packed {R} x {K}x{N} int8 weights ({pack_s * 1e3:.1f} ms/pack); plans M=1 {gemv_plan}, "
               f"M=512 {gemm_plan}", file=sys.stderr, flush=True)
 
-        g1 = e1 = g512 = e512 = floor_ms = copy_ms = float("nan")
+        g1 = e1 = g512 = e512 = floor_ms = copy_ms = read_ms = float("nan")
         if args.only == "chain":
             ms = measure_chain(npu, hip, L, ws, dA, dC, 8, 300)
             print(f"[bench] chain of 8: {ms * 1e3:.2f} us/call", file=sys.stderr, flush=True)
@@ -686,8 +716,10 @@ def main():
             floor_ms, _ = measure(npu, hip, [tiny], 1, dA, dC, args.steps, args.warmup)
             ork.lib().ork_mm_free(npu.h, tiny)
             copy_ms = measure_copy(hip, L, npu, K * N, args.steps)
+            read_ms = measure_read(npu, hip, L, ws, dA, dC, args.steps, args.warmup)
             print(f"[bench] launch floor (K=32 N=32 GEMV): {floor_ms * 1e3:.2f} us/step; D2D copy of {K * N} B: "
-                  f"{copy_ms * 1e3:.2f} us ({2 * K * N / (copy_ms * 1e-3) / 1e9:.0f} GB/s read+write)",
+                  f"{copy_ms * 1e3:.2f} us ({2 * K * N / (copy_ms * 1e-3) / 1e9:.0f} GB/s read+write); plain read of "
+                  f"the weight's panels: {read_ms * 1e3:.2f} us ({K * N / (read_ms * 1e-3) / 1e9:.0f} GB/s)",
                   file=sys.stderr, flush=True)
         if args.only != "gemv":
             g512, e512 = measure(npu, hip, ws, 512, dA, dC, args.m512_steps, max(args.warmup // 8, 8), outer=o512)
@@ -787,9 +819,13 @@ def main():
         "launch_floor": {"gemv_k32_n32_us": round(floor_ms * 1e3, 3),
                          "d2d_copy_us": round(copy_ms * 1e3, 3),
                          "d2d_copy_gbs": round(2 * K * N / (copy_ms * 1e-3) / 1e9, 1),
+                         "read_us": round(read_ms * 1e3, 3),
+                         "read_gbs": round(K * N / (read_ms * 1e-3) / 1e9, 1),
                          "note": "same HIP-graph harness and step count as `value`: ork_i8_mm_run on a K=32, N=32 weight "
-                                 "(a launch that moves almost nothing), and hipMemcpyAsync device-to-device of the "
-                                 "weight's 12,582,912 bytes from the same rotation (read + write counted)"},
+                                 "(a launch that moves almost nothing), hipMemcpyAsync device-to-device of the "
+                                 "weight's 12,582,912 bytes from the same rotation (read + write counted), and "
+                                 "ork_npu_read_probe reading those panel bytes alone (the GEMV's loads without its "
+                                 "arithmetic: 1,536 workgroups of 4 waves, 2 loads of 16 bytes per lane, the fastest of 1-4 KiB per wave)"},
         "chain8": {"value": round(chain_gbs, 1), "unit": "GB/s", "us_per_call": round(chain_ms * 1e3, 3),
                    "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("chain8_i8_m1"),
                    "note": "ork_i8_mm_run_chain: 8 M=1 GEMVs of the same shape (distinct resident weights) per call, "

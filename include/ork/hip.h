@@ -30,6 +30,12 @@ int          ork_i8_mm_run_noalloc(ork_npu *ctx, ork_w *w, int M, const int8_t *
  * where event timestamps are not available). ork_npu_wallclock_khz gives the clock's constant rate. 0 / -1. */
 int          ork_npu_mark(ork_npu *ctx, void *dev_u64);
 int          ork_npu_wallclock_khz(const ork_npu *ctx);
+/* Profiling: enqueue on the context's stream a plain streaming read of `bytes` (a multiple of 16) of 16-byte
+ * aligned device memory -- the M = 1 GEMV's loads without its arithmetic, which prices a weight's bytes in the
+ * same launch harness. Workgroup i stores the XOR of the 32-bit words it read into dev_sink[i]; the XOR of all
+ * of them is the XOR of every word of the bytes. Returns the workgroup count (ceil(bytes / 8192) words of
+ * dev_sink), or -1. Synchronises unless async mode is on. */
+long long    ork_npu_read_probe(ork_npu *ctx, const void *dev, size_t bytes, uint32_t *dev_sink);
 /* The resident form of a device weight, for callers that run their own kernels on it (the decoder harness fuses
  * its per-row operators into M = 1 matmul launches): the device address of its panels, the K-blocks per panel and
  * the panel kind (0 int8, 1 uniform int4, 2 NF4, 3 fp16), laid out as ork-driver_amd/csrc/hip/orkh.h documents,

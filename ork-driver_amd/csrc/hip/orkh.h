@@ -74,6 +74,8 @@ int         orkh_sync(void *stream);
 /* Enqueue on the stream one 1-thread kernel that writes the device wall clock (a 64-bit counter at
  * orkh_dev.wall_khz) to dev_u64: a timestamp taken where the stream reaches it, also inside a captured graph. */
 int         orkh_mark(void *dev_u64, void *stream);
+/* streaming read of `bytes` device bytes, one XOR word per workgroup into sink; the workgroup count, or -1 */
+long long   orkh_read_probe(const void *dev, size_t bytes, unsigned *sink, void *stream);
 int         orkh_device_sync(void);
 /* 1 if p is device (or device-mapped) memory known to the HIP runtime, 0 if plain host memory. */
 int         orkh_ptr_is_device(const void *p);

@@ -30,6 +30,31 @@ static int fail(hipError_t e, const char *what) {
 // One thread stores the device wall clock (constant rate, orkh_dev.wall_khz): a timestamp in stream order.
 __global__ void k_mark(unsigned long long *p) { *p = wall_clock64(); }
 
+// Profiling: a plain streaming read of n16 16-byte chunks -- the M = 1 GEMV's loads without its arithmetic. Each
+// workgroup of 4 waves reads RP_U contiguous KiB-runs per wave (RP_U loads per lane, all issued before any is
+// used), XOR-folds them and stores one word, so a caller can check that every byte was read.
+constexpr int RP_U = 2;
+typedef int rp_v4i __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_read_probe(const rp_v4i *__restrict__ p, long long n16, unsigned *sink) {
+    __shared__ unsigned red[4];
+    const long long i0 = (long long)blockIdx.x * (256 * RP_U) + threadIdx.x;
+    rp_v4i r[RP_U];
+#pragma unroll
+    for (int u = 0; u < RP_U; u++) {
+        const long long i = i0 + (long long)u * 256;
+        r[u] = __builtin_nontemporal_load(p + (i < n16 ? i : n16 - 1));
+    }
+    unsigned x = 0;
+#pragma unroll
+    for (int u = 0; u < RP_U; u++)
+        if (i0 + (long long)u * 256 < n16) x ^= (unsigned)(r[u].x ^ r[u].y ^ r[u].z ^ r[u].w);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= (unsigned)__shfl_xor((int)x, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 extern "C" {
 
 const char *orkh_last_error(void) { return g_err; }
@@ -42,6 +67,23 @@ int orkh_mark(void *dev_u64, void *stream) {
     hipLaunchKernelGGL(k_mark, dim3(1), dim3(1), 0, (hipStream_t)stream, (unsigned long long *)dev_u64);
     CK(hipGetLastError(), "k_mark launch");
     return 0;
+}
+
+long long orkh_read_probe(const void *dev, size_t bytes, unsigned *sink, void *stream) {
+    if (!dev || !sink || !bytes || bytes % 16 || (uintptr_t)dev % 16 || (uintptr_t)sink % 4) {
+        snprintf(g_err, sizeof g_err, "orkh_read_probe: 16-byte aligned device bytes (a multiple of 16) and a "
+                                      "4-byte aligned sink are required");
+        return -1;
+    }
+    const long long n16 = (long long)(bytes / 16), grid = (n16 + 256 * RP_U - 1) / (256 * RP_U);
+    if (grid >= (1LL << 31)) {
+        snprintf(g_err, sizeof g_err, "orkh_read_probe: %zu bytes is too many", bytes);
+        return -1;
+    }
+    hipLaunchKernelGGL(k_read_probe, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, (const rp_v4i *)dev, n16,
+                       sink);
+    CK(hipGetLastError(), "k_read_probe launch");
+    return grid;
 }
 
 int orkh_device_count(void) {

@@ -337,6 +337,18 @@ int ork_npu_mark(ork_npu *c, void *dev_u64) {
 
 int ork_npu_wallclock_khz(const ork_npu *c) { return (c && !c->offline) ? c->dev.wall_khz : 0; }
 
+long long ork_npu_read_probe(ork_npu *c, const void *dev, size_t bytes, uint32_t *dev_sink) {
+    if (orki_need_device(c, "ork_npu_read_probe")) return -1;
+    if (!orkh_ptr_is_device(dev) || !orkh_ptr_is_device(dev_sink)) {
+        orki_err("ork_npu_read_probe: the bytes and the sink must be device memory");
+        return -1;
+    }
+    const long long n = orkh_read_probe(dev, bytes, dev_sink, c->stream);
+    if (n < 0) { orki_err("ork_npu_read_probe: %s", orkh_last_error()); return -1; }
+    if (!c->async && orkh_sync(c->stream)) { orki_hip_fail("ork_npu_read_probe"); return -1; }
+    return n;
+}
+
 int ork_dev_download(ork_npu *c, void *dst, const void *src, size_t n) {
     if (orki_need_device(c, "ork_dev_download")) return -1;
     if (orkh_d2h(dst, src, n, c->stream) || orkh_sync(c->stream)) { orki_hip_fail("ork_dev_download"); return -1; }

@@ -82,6 +82,7 @@ API = {
     "ork_npu_stream": (_P, [_P]),
     "ork_npu_mark": (C.c_int, [_P, _P]),
     "ork_npu_wallclock_khz": (C.c_int, [_P]),
+    "ork_npu_read_probe": (C.c_longlong, [_P, _P, C.c_size_t, _P]),
     "ork_w_device_panels": (C.c_int, [_P, _P, _P, _P, _P]),
     "ork_w_plan_name": (C.c_char_p, [_P, _P, C.c_int]),
     "ork_w_grouped_plan_name": (C.c_char_p, [_P, _P, C.c_int]),

@@ -31,6 +31,16 @@ int orkh_d2h_2d(void *d, size_t dp, const void *s, size_t sp, size_t w, size_t r
     (void)st; for (size_t i = 0; i < r; i++) memcpy((char *)d + i * dp, (const char *)s + i * sp, w); return 0; }
 int orkh_sync(void *s) { (void)s; return 0; }
 int orkh_mark(void *p, void *s) { (void)s; memset(p, 0, 8); return 0; }
+long long orkh_read_probe(const void *dev, size_t bytes, unsigned *sink, void *s) {
+    (void)s;
+    const long long grid = (long long)((bytes / 16 + 511) / 512);
+    for (long long g = 0; g < grid; g++) {
+        unsigned x = 0;
+        for (size_t i = (size_t)g * 2048; i < bytes / 4 && i < (size_t)(g + 1) * 2048; i++) x ^= ((const unsigned *)dev)[i];
+        sink[g] = x;
+    }
+    return grid;
+}
 int orkh_device_sync(void) { return 0; }
 int orkh_ptr_is_device(const void *p) { for (int i = 0; i < ndev; i++) if ((const char *)p >= (char *)devp[i] && (const char *)p < (char *)devp[i] + (devn[i] ? devn[i] : 1)) return 1; return 0; }
 int orkh_mm_launch(const orkh_mm *p, const orkh_plan *q, void *s) { (void)p; (void)q; (void)s; return 0; }

@@ -404,6 +404,30 @@ def test_device_resident_operands_async(npu):
     ork.free(w)
 
 
+@pytest.mark.parametrize("nbytes", [16, 8192, 1_000_016, 12_582_912])
+def test_read_probe_reads_every_byte(npu, nbytes):
+    """ork_npu_read_probe (the benchmark's plain read of a weight's bytes): the XOR of its per-workgroup words
+    equals the XOR of every 32-bit word of the buffer, at sizes with and without a partial last workgroup."""
+    L = ork.lib()
+    rng = _rng(nbytes % 997)
+    host = rng.integers(0, 256, size=nbytes, dtype=np.uint8)
+    dev = L.ork_dev_alloc(npu.h, nbytes)
+    sink = L.ork_dev_alloc(npu.h, 4 * ((nbytes + 8191) // 8192))
+    assert dev and sink
+    assert L.ork_dev_upload(npu.h, dev, ork.ptr(host), nbytes) == 0
+    n = L.ork_npu_read_probe(npu.h, dev, nbytes, sink)
+    assert n == (nbytes + 8191) // 8192
+    words = np.empty(n, np.uint32)
+    assert L.ork_dev_download(npu.h, ork.ptr(words), sink, 4 * n) == 0
+    assert np.bitwise_xor.reduce(words) == np.bitwise_xor.reduce(host.view(np.uint32))
+    # refusals: a size that is not a multiple of 16, a misaligned start, host memory
+    assert L.ork_npu_read_probe(npu.h, dev, 24, sink) == -1
+    assert L.ork_npu_read_probe(npu.h, dev + 8, 16, sink) == -1
+    assert L.ork_npu_read_probe(npu.h, ork.ptr(host), 16, sink) == -1
+    L.ork_dev_free(npu.h, dev)
+    L.ork_dev_free(npu.h, sink)
+
+
 def test_dma_buffers(npu):
     import ctypes as Ct
 
