@@ -422,8 +422,9 @@ __global__ __launch_bounds__(256) void k_attn_part(q3_att p) {
 // k_attn_rows: the prefill form of k_attn_part (M > 1 rows, rotated queries in p.q): one workgroup per (kv head's
 // query-head group, key chunk, block of HD / Q3_CHUNK rows). The chunk's keys go to LDS and its values to registers
 // once and serve every row of the block, every thread scoring one (row, head, key), instead of one workgroup
-// reloading the chunk for each row. (Blocks of 16 rows, several such passes per workgroup, measured slower: the
-// scoring is per-thread latency, and 4x fewer workgroups left most CUs idle.) Each row's partials are computed with
+// reloading the chunk for each row. (Blocks of 16 rows measured slower, both as four such passes per workgroup and
+// with register-blocked scores -- each wave scoring four rows per K row read from LDS: the scoring is per-thread
+// latency, and 4x fewer workgroups left most CUs idle.) Each row's partials are computed with
 // k_attn_part's operations in its order (the score sums, the 32-lane max and sum, the P.V accumulation), and a row
 // with no key in the chunk gets k_attn_part's empty partial, so the partials are bit-identical to it.
 template <int GW>
