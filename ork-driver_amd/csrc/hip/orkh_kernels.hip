@@ -676,7 +676,9 @@ template <int KIND, int BM, int BN, int KS, int XG = 0> struct T2 {
     // NF4: a stage's B blocks are decoded once, into int8 MFMA operands in LDS, instead of by each of the
     // WM waves that read a block (the codebook decode is ~8x the VALU work of the uniform-int4 one)
     static constexpr int DEC = KIND == ORKH_NF4 ? NIB * T::STEPS * 1024 : 0;
-    // ring within 160 KiB: 4 slots, 8 for the small stages of the K-group tiles (more bytes in flight per CU)
+    // ring within 160 KiB: 4 slots, 8 for the small stages of the K-group tiles (more bytes in flight per CU);
+    // 8 slots for the 12-16 KiB stages of the other tiles measured slower (int8 M=128 64 x 64 8.5 -> 9.4 us,
+    // fp16 M=512 13.0 -> 14.0, grouped W4A4 M=256 21.9 -> 22.7)
     static constexpr int RMAX = WK > 1 ? 8 : 4;
     static constexpr int R = ((163840 - DEC) / SLOT) < RMAX ? ((163840 - DEC) / SLOT) : RMAX;
     static constexpr size_t LDS = (size_t)R * SLOT + DEC;
