@@ -5,6 +5,7 @@
   pack / load keep the oracle's codes, and runs on an offline context compute the exact result on the CPU
   as the reference's offline branches do (int8 / int4 / grouped runs, int8 chain, int4 chain and stream)
 - dims gates, O4N1 validation cases, ork_i8_mm_run_cpu vs the oracle
+- bench.py refuses more than one GPU
 """
 import ctypes as C
 import os
@@ -290,3 +291,15 @@ def test_reference_offline_load_example_runs_unmodified():
     assert r.returncode == 0, r.stdout + r.stderr
     assert "test_offline_load: PASS" in r.stdout
     assert "FAIL" not in r.stdout
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py's contract: this build runs on one GPU, so --gpus N > 1 exits with status 2 and says why, before
+    touching a device."""
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
