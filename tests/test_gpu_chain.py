@@ -217,3 +217,45 @@ def test_chain_errors(npu):
     assert L.ork_i8_mm_run_chain(npu.h, 1, ork.tasks(ork.TaskI8, [(w, 1, buf[:64], buf.ctypes.data)])) == -1
     ork.free(w)
     ork.free(wf)
+
+
+def _random_chains(n=24, seed=0x63686E):
+    rng = np.random.default_rng(seed)
+    out = []
+    for c in range(n):
+        S = int(rng.integers(1, 9))
+        M = int(rng.choice([1, 3, 16, 33, 64, 65, 100, 128, 200, 256]))
+        K = 32 * int(rng.integers(1, 65))
+        kind = ["i8", "u4", "nf4"][c % 3]
+        tasks = [(int(rng.choice([1, 5, 70])) if rng.random() < 0.2 else M, 32 * int(rng.integers(1, 97)))
+                 for _ in range(S)]
+        out.append((c, kind, K, tasks))
+    return out
+
+
+@pytest.mark.parametrize("c,kind,K,tasks", _random_chains())
+def test_i8_chain_random(npu, c, kind, K, tasks):
+    """Seeded random chains at default plans: runs of tasks sharing M and K (one grouped tiled launch when their
+    summed columns plan to the LDS-ring kernel), M = 1 tasks (one grouped GEMV launch), odd ones out; every task
+    bit-exact against the oracle."""
+    _say("random chain", c, kind, K, tasks)
+    rng = np.random.default_rng(500 + c)
+    rows, refs, outs, ws = [], [], [], []
+    for M, N in tasks:
+        if kind == "i8":
+            codes = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+            w = npu.pack_i8(codes)
+        else:
+            w, codes = _i4a8(npu, rng, K, N, kind == "nf4")
+        assert w
+        A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+        Cb = np.full((M, N), -7, np.int32)
+        rows.append((w, M, A, Cb, 0))
+        refs.append(O.gemm_i32(A, codes))
+        outs.append(Cb)
+        ws.append((w, M))
+    assert ork.lib().ork_i8_mm_run_chain(npu.h, len(rows), ork.tasks(ork.TaskI8, rows)) == 0
+    for i, (Cb, R) in enumerate(zip(outs, refs)):
+        assert np.array_equal(Cb, R), (i, npu.plan_name(*ws[i]))
+    for w, _ in ws:
+        ork.free(w)

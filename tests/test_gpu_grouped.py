@@ -327,3 +327,55 @@ def test_grouped_one_row_exact(npu, kind):
         rc2, C2 = _env_run({"ORK_PLAN": "stream"}, fn, npu, w, A, aS, bS)
         assert rc2 == 0 and np.array_equal(C2, C), (kind, K, N, G)
         L.ork_mm_free(npu.h, w)
+
+
+def _random_grouped(n=40, seed=0x67727073):
+    rng = np.random.default_rng(seed)
+    out = []
+    for c in range(n):
+        kind = ["i8", "w4a4", "u4", "nf4"][c % 4]
+        G = int(rng.choice([32, 64, 96, 128, 256, 512]))
+        K = G * int(rng.integers(1, max(2, 4096 // G) + 1))
+        step = 64 if kind == "w4a4" else 32
+        N = step * int(rng.integers(1, 2048 // step + 1))
+        M = int(rng.choice([1, 2, 8, 17, 31, 32, 64, 100, 128, 129, 256]))
+        while N > step and M * K * N > 300_000_000:
+            N = max(step, (N // 2) // step * step)
+        out.append((c, kind, M, K, N, G))
+    return out
+
+
+@pytest.mark.parametrize("c,kind,M,K,N,G", _random_grouped())
+def test_grouped_random(npu, c, kind, M, K, N, G):
+    """Seeded random grouped-scale runs at default plans (one-row kernel, panel streaming, grouped LDS-ring tiles;
+    group sizes below, at and above a K-block), bit for bit against the oracle's ascending-group accumulate."""
+    _say("random grouped", c, kind, M, K, N, G)
+    L = ork.lib()
+    rng = np.random.default_rng(700 + c)
+    aS = rng.uniform(1e-3, 1e-2, size=(M, K // G)).astype(np.float32)
+    bS = rng.uniform(1e-3, 1e-2, size=(K // G, N)).astype(np.float32)
+    if kind == "w4a4":
+        A = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+        codes = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
+        w = L.ork_i4_mm_pack_grouped(npu.h, K, N, ork.ptr(codes), G)
+        fn = L.ork_i4_mm_run_grouped
+    else:
+        A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+        if kind == "i8":
+            codes = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+            w = npu.pack_i8(codes)
+        else:
+            W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+            if kind == "nf4":
+                os.environ["ORK_NF4"] = "1"
+            try:
+                w, _ = npu.pack_i4a8(W)
+            finally:
+                os.environ.pop("ORK_NF4", None)
+            _, _, codes = O.pack_i4a8(W, nf4=kind == "nf4")
+        assert L.ork_w_set_group(w, G) == 0
+        fn = L.ork_i8_mm_run_grouped
+    assert w
+    rc, C = _run(fn, npu, w, A, aS, bS)
+    assert rc == 0 and np.array_equal(C, O.gemm_grouped(A, codes, aS, bS, G)), npu.grouped_plan_name(w, M)
+    L.ork_mm_free(npu.h, w)
