@@ -1695,7 +1695,9 @@ extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *q, int 
                  p->N, G, ldc, q->algo);
         return -2;
     }
-    if (q->algo == ORKH_ALGO_GEMV) {
+    // the one-row kernel loads the activations 16 bytes at a time: a row that is not 16-byte aligned (a caller's
+    // device pointer) takes the panel-streaming kernel, as the plain GEMV falls back to whole panels
+    if (q->algo == ORKH_ALGO_GEMV && ((uintptr_t)p->A & 15) == 0) {
         const int need = (q->kbw + 1) / 2, ni = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
         if (p->M != 1 || p->K / G > ORKH_GGEMV_SK_MAX || q->kbw < 1 || (q->wpg != 2 && q->wpg != 4 && q->wpg != 8) ||
             (q->kbw * q->wpg < p->KB)) {
