@@ -787,6 +787,33 @@ def main():
         print(f"[bench] M=1 GEMV K={K} N={NL}: {lm_ms * 1e3:.2f} us/step ({lm_gbs:.0f} GB/s, "
               f"{lm_gbs / HBM_PEAK_GBS:.1%} of HBM) {lm_plan}", file=sys.stderr, flush=True)
 
+        # the LDS-ring kernel on a large square GEMM, where each CU's operand bytes per MAC are small enough for the
+        # MFMA work to dominate: what the kernel reaches when operand delivery to the CUs is not the bound
+        L.ork_npu_set_async(npu.h, 1)
+        SQ = 4096
+        rq = np.random.default_rng(0x6F726B51)
+        Bq = np.frombuffer(rq.bytes(SQ * SQ), np.int8).reshape(SQ, SQ)
+        Aq = np.frombuffer(rq.bytes(SQ * SQ), np.int8).reshape(SQ, SQ)
+        wq = [npu.pack_i8(Bq) for _ in range(40)]
+        dAq, dCq = L.ork_dev_alloc(npu.h, SQ * SQ), L.ork_dev_alloc(npu.h, SQ * SQ * 4)
+        assert all(wq) and dAq and dCq
+        assert L.ork_dev_upload(npu.h, dAq, ork.ptr(Aq), Aq.nbytes) == 0
+        sq_ms, _ = measure(npu, hip, wq, SQ, dAq, dCq, 40, 4)
+        L.ork_npu_set_async(npu.h, 0)
+        Cq = np.empty((SQ, SQ), np.int32)
+        assert L.ork_dev_download(npu.h, ork.ptr(Cq), dCq, Cq.nbytes) == 0
+        rows = np.r_[0:4, 2045:2051, SQ - 4:SQ]
+        assert np.array_equal(Cq[rows], O.gemm_i32(Aq[rows], Bq)), "large GEMM result differs"
+        sq_plan = npu.plan_name(wq[0], SQ)
+        sq_tops = 2.0 * SQ ** 3 / (sq_ms * 1e-3) / 1e12
+        for w in wq:
+            ork.lib().ork_mm_free(npu.h, w)
+        L.ork_dev_free(npu.h, dAq)
+        L.ork_dev_free(npu.h, dCq)
+        del Aq, Bq, Cq
+        print(f"[bench] int8 GEMM M=K=N={SQ}: {sq_ms * 1e3:.2f} us/step ({sq_tops:.0f} TOP/s, "
+              f"{sq_tops / INT8_PEAK_TOPS:.1%} of MFMA) {sq_plan}", file=sys.stderr, flush=True)
+
         configs = None
         if not args.no_configs:
             L.ork_npu_set_async(npu.h, 1)
@@ -852,6 +879,11 @@ def main():
                          "unit": "GB/s", "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
                          "note": "the same kernel as `value` in the same HIP-graph harness, on a weight large enough "
                                  "that the ~1.6 us launch no longer dominates; checked against the oracle"},
+        "gemm_large": {"workload": f"int8 GEMM ork_i8_mm_run M=K=N={SQ} (40 rotated resident weights)", "kernel": sq_plan,
+                       "us_per_step": round(sq_ms * 1e3, 3), "value": round(sq_tops, 1), "unit": "TOP/s",
+                       "frac": round(sq_tops / INT8_PEAK_TOPS, 4),
+                       "note": "the M=512 kernel family in the same HIP-graph harness on a shape with far more "
+                               "multiply-accumulates per operand byte a CU receives; rows spot-checked against the oracle"},
         "chain8": {"value": round(chain_gbs, 1), "unit": "GB/s", "us_per_call": round(chain_ms * 1e3, 3),
                    "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("chain8_i8_m1"),
                    "note": "ork_i8_mm_run_chain: 8 M=1 GEMVs of the same shape (distinct resident weights) per call, "
