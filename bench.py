@@ -37,6 +37,7 @@ MALL_BYTES = 256 << 20          # MI355X Infinity Cache
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
 INT8_PEAK_TOPS = 5000.0         # MI355X dense int8 MFMA, TOP/s
 WARM_S = 0.05                   # untimed replays of a timed graph before its timed replay (steady state)
+EAGER_ONLY = False              # --eager-only: no graphs, events or other HIP calls from Python (profiler runs)
 FP16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 MFMA, TFLOP/s
 
 
@@ -117,6 +118,16 @@ def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scale
     # eager: warmup, then steps individually launched (host launch rate included)
     for i in range(warmup):
         run(i)
+    if EAGER_ONLY:
+        # profiler runs: only the library's own calls reach the HIP runtime (host clock around the launches and
+        # the library's stream sync); the profiler's per-dispatch durations are what such a run is for
+        assert L.ork_npu_sync(npu.h) == 0
+        t0 = time.perf_counter()
+        for i in range(steps):
+            run(i)
+        assert L.ork_npu_sync(npu.h) == 0
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        return ms, ms
     eager = hip.time_ms(stream, lambda: [run(i) for i in range(steps)]) / steps
     # graph: timestamp node, exactly `steps` launches, timestamp node; warm it, stream the other weights, then time
     # one replay
@@ -151,6 +162,16 @@ def measure(npu, hip, ws, M, dA, dC, steps, warmup, entry="ork_i8_mm_run", scale
     if outer is not None:
         outer.append(launch_incl / steps)
     return inner / steps, eager
+
+
+def measure_marks(npu, hip, L, dA, dC, steps, warmup):
+    """ms per step of measure()'s graph harness around ork_npu_mark alone (one one-thread kernel writing the wall
+    clock): the per-dispatch floor of a launch that does no work, beside the K=32, N=32 GEMV's."""
+    slot = L.ork_dev_alloc(npu.h, 256)
+    assert slot
+    ms, _ = measure(npu, hip, [slot], 1, dA, dC, steps, warmup, call=lambda p: L.ork_npu_mark(npu.h, p))
+    L.ork_dev_free(npu.h, slot)
+    return ms
 
 
 def graph_stamps_ms(npu, L, ts):
@@ -292,6 +313,28 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC, codes1, A512, cpu_s, only=None):
         g, _ = measure(npu, hip, ws_c1, 16, dA, dC, 960, 48)
         rec("C1 w8a8 K=2048 N=6144", npu.plan_name(ws_c1[0], 16), 16, g, K * N + 16 * K + 4 * 16 * N, 2 * 16 * N * K, "hbm",
             (lambda r: gemm(A512[:r], codes1), gkind, gwhat))
+
+    if want("shard"):
+        # ---- one GPU's share of config 1 split 8 ways over N (output channels), the natural split of the path
+        # across GPUs: K=2048, N=768, M=1 and 16. 336 rotated copies of the 1.57 MB share (528 MB > 2x the MALL).
+        NS = N // 8
+        Ws = np.ascontiguousarray(codes1[:, :NS])
+        wss = [npu.pack_i8(Ws) for _ in range(336)]
+        assert all(wss)
+        for M in (1, 16):
+            g, _ = measure(npu, hip, wss, M, dA, dC, steps_for(0.002), 64)
+            rec("C1 one-GPU share of an 8-way N split, K=2048 N=768", npu.plan_name(wss[0], M), M, g,
+                K * NS + M * K + 4 * M * NS, 2 * M * NS * K, "hbm",
+                (lambda r: gemm(A512[:r], Ws), gkind, gwhat))
+        L.ork_npu_set_async(npu.h, 0)
+        A1 = np.empty((16, K), np.int8)
+        assert L.ork_dev_download(npu.h, ork.ptr(A1), dA, A1.nbytes) == 0
+        Cs = np.empty((16, NS), np.int32)
+        assert L.ork_dev_download(npu.h, ork.ptr(Cs), dC, Cs.nbytes) == 0   # the timed M=16 launches wrote it
+        assert np.array_equal(Cs, O.gemm_i32(A1, Ws)), "N-split share spot check"
+        L.ork_npu_set_async(npu.h, 1)
+        for w in wss:
+            L.ork_mm_free(npu.h, w)
 
     if want("c2"):
         # ---- config 2: fp16, K = N = 2048, M in {1, 16, 128, 512}
@@ -626,6 +669,20 @@ def cpu_baseline_m512(W_codes, A512, budget_s):
     return out
 
 
+def trace_from_profiles(kernel_tag):
+    """The rocprofv3 kernel-trace summary of the dominant kernel (profiles/*_trace.json): its traced per-dispatch
+    duration, the tracer's per-dispatch overhead measured in the same traced run on the K=32, N=32 GEMV and the
+    one-thread wall-clock kernel against their untraced graph steps, and the step time and roofline fraction that
+    follow from them; or None."""
+    p = os.path.join(ROOT, "profiles", f"{kernel_tag}_trace.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        return json.load(open(p)).get("roofline_from_trace")
+    except Exception:
+        return None
+
+
 def traffic_from_profiles(kernel_tag):
     """HBM bytes per launch from committed rocprofv3 --pmc summaries (profiles/*_pmc.json), or None."""
     p = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.json")
@@ -652,8 +709,12 @@ def main():
     ap.add_argument("--only", choices=["gemv", "m512", "chain", "decoder", "configs"],
                     help="profiling: time only one kernel (decoder: only BASELINE config 5, w8a8; configs: the "
                          "config sweep's sections named by --configs)")
-    ap.add_argument("--configs", default="c1,c2,c3,c4,grouped",
-                    help="with --only configs: comma-separated sections of the config sweep (c1 c2 c3 c4 grouped)")
+    ap.add_argument("--configs", default="c1,shard,c2,c3,c4,grouped",
+                    help="with --only configs: comma-separated sections of the config sweep (c1 shard c2 c3 c4 "
+                         "grouped; shard = one GPU's share of config 1 split 8 ways over N)")
+    ap.add_argument("--eager-only", action="store_true",
+                    help="profiling: time eager launches by the host clock only (no graphs, events or HIP calls "
+                         "from Python); with --only configs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling: run device-to-device copies of one weight's bytes (a plain copy kernel of "
                          "known size) instead of the bench, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -667,7 +728,11 @@ def main():
     import oracle as O
 
     L = ork.lib()
-    hip = Hip()
+    global EAGER_ONLY
+    EAGER_ONLY = args.eager_only
+    if EAGER_ONLY and args.only != "configs":
+        ap.error("--eager-only goes with --only configs")
+    hip = None if EAGER_ONLY else Hip()
     if args.copy_calibration:
         copy_calibration(hip, L)
         return
@@ -707,7 +772,7 @@ def main():
         print(f"[bench] packed {R} x {K}x{N} int8 weights ({pack_s * 1e3:.1f} ms/pack); plans M=1 {gemv_plan}, "
               f"M=512 {gemm_plan}", file=sys.stderr, flush=True)
 
-        g1 = e1 = g512 = e512 = floor_ms = copy_ms = read_ms = float("nan")
+        g1 = e1 = g512 = e512 = floor_ms = copy_ms = read_ms = mark_ms = float("nan")
         if args.only == "chain":
             ms = measure_chain(npu, hip, L, ws, dA, dC, 8, 300)
             print(f"[bench] chain of 8: {ms * 1e3:.2f} us/call", file=sys.stderr, flush=True)
@@ -718,12 +783,18 @@ def main():
         if args.only not in ("m512",):
             g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup, outer=o1)
             print(f"[bench] M=1: graph {g1 * 1e3:.2f} us/step, eager {e1 * 1e3:.2f} us/step", file=sys.stderr, flush=True)
-        if not args.only:
-            # the same graph harness around a launch that moves almost nothing (K=32, N=32), and around the runtime's
-            # copy kernel moving the weight's bytes: what one launch costs on this box before any data
+        if args.only in (None, "gemv"):
+            # the same graph harness around a launch that moves almost nothing (K=32, N=32) and around the one-thread
+            # wall-clock kernel alone: what one launch costs on this box before any data (in a traced run, the
+            # tracer's own cost per dispatch beside the GEMV's)
             tiny = npu.pack_i8(np.ones((32, 32), np.int8))
             floor_ms, _ = measure(npu, hip, [tiny], 1, dA, dC, args.steps, args.warmup)
             ork.lib().ork_mm_free(npu.h, tiny)
+            mark_ms = measure_marks(npu, hip, L, dA, dC, args.steps, args.warmup)
+            print(f"[bench] K=32 N=32 GEMV: {floor_ms * 1e3:.3f} us/step; wall-clock mark alone: {mark_ms * 1e3:.3f} "
+                  f"us/step", file=sys.stderr, flush=True)
+        if not args.only:
+            # and around the runtime's copy kernel moving the weight's bytes, and a plain read of them
             copy_ms = measure_copy(hip, L, npu, K * N, args.steps)
             read_ms = measure_read(npu, hip, L, ws, dA, dC, args.steps, args.warmup)
             print(f"[bench] launch floor (K=32 N=32 GEMV): {floor_ms * 1e3:.2f} us/step; D2D copy of {K * N} B: "
@@ -872,15 +943,18 @@ def main():
                                    "note": "the same replay timed by events recorded around hipGraphLaunch: adds the "
                                            "host's one submission of the graph, spread over `steps`"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_i8_m1")},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_i8_m1"),
+                     "rocprof": trace_from_profiles("gemv_i8_m1")},
         "eager_value": round(algo_bytes(1) / (e1 * 1e-3) / 1e9, 1),
         "launch_floor": {"gemv_k32_n32_us": round(floor_ms * 1e3, 3),
+                         "mark_us": round(mark_ms * 1e3, 3),
                          "d2d_copy_us": round(copy_ms * 1e3, 3),
                          "d2d_copy_gbs": round(2 * K * N / (copy_ms * 1e-3) / 1e9, 1),
                          "read_us": round(read_ms * 1e3, 3),
                          "read_gbs": round(K * N / (read_ms * 1e-3) / 1e9, 1),
                          "note": "same HIP-graph harness and step count as `value`: ork_i8_mm_run on a K=32, N=32 weight "
-                                 "(a launch that moves almost nothing), hipMemcpyAsync device-to-device of the "
+                                 "(a launch that moves almost nothing), ork_npu_mark alone (a one-thread kernel), "
+                                 "hipMemcpyAsync device-to-device of the "
                                  "weight's 12,582,912 bytes from the same rotation (read + write counted), and "
                                  "ork_npu_read_probe reading those panel bytes alone (the GEMV's loads without its "
                                  "arithmetic: 1,536 workgroups of 4 waves, 2 loads of 16 bytes per lane, the fastest of 1-4 KiB per wave)"},
@@ -905,7 +979,8 @@ def main():
                  "value": round(tops, 1), "unit": "TOP/s", "ms_per_step": round(g512, 6), "steps": args.m512_steps,
                  "graph_launch_inclusive_ms_per_step": round(o512[0], 6) if o512 else None,
                  "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                              "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": traffic_from_profiles("gemm_i8_m512")},
+                              "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": traffic_from_profiles("gemm_i8_m512"),
+                              "rocprof": trace_from_profiles("gemm_i8_m512")},
                  "hbm_gbs": round(algo_bytes(512) / (g512 * 1e-3) / 1e9, 1),
                  "eager_value": round(algo_ops(512) / (e512 * 1e-3) / 1e12, 1)},
     }

@@ -21,10 +21,50 @@ int          ork_npu_sync(ork_npu *ctx);
 void        *ork_npu_stream(ork_npu *ctx);
 /* No counterpart in the reference: ork_i8_mm_run (include/ork/run.h:21) for callers that cannot allocate --
  * code under HIP graph capture, serving loops and harnesses that forbid hipMalloc. A and C must be device memory
- * (ork_dev_alloc or any hipMalloc); a split-K plan keeps its partials in a static 8 MiB per-GPU scratch array
- * instead of a grown workspace, and a plan needing more is refused (-1). No call allocates. Calls that overlap
- * on one GPU share that array and race. Same results and return codes as ork_i8_mm_run otherwise. */
+ * (ork_dev_alloc or any hipMalloc) and A 16-byte aligned (ork_i8_mm_run stages a misaligned A; this call refuses
+ * it, -1); a split-K plan keeps its partials in a static 8 MiB per-GPU scratch array instead of a grown
+ * workspace, and a plan needing more is refused (-1). No call allocates. Under HIP graph capture async mode is
+ * required (ork_npu_set_async(ctx, 1)): outside it the call ends with a stream synchronisation, so on a capturing
+ * stream it is refused (-1) before anything is enqueued. Calls that overlap on one GPU share that array and race.
+ * Same results and return codes as ork_i8_mm_run otherwise. */
 int          ork_i8_mm_run_noalloc(ork_npu *ctx, ork_w *w, int M, const int8_t *A, int32_t *C);
+/* No counterpart in the reference, whose harness prepares each activation row on the host, runs ork_i8_mm_run and
+ * uses the output columns on the host (examples/bench.c:83-90 quantise / dequantise, :105-113 mm(), :128-145 the
+ * layer's norm, residual add and SwiGLU): ork_i8_mm_run for ONE activation row with the row's preparation and each
+ * output column's use fused into the matmul launch, for decode loops on device-resident rows. S weights from
+ * ork_i8_mm_pack(_f32) or ork_i4a8_mm_pack(_im) / ork_i4a8_mm_load (int8, uniform int4 or NF4 resident), one K
+ * (K <= ORK_ROW_KMAX).
+ *   prologue  ORK_ROW_RMSNORM  y = (row * (1 / sqrt(ss / K + eps))) * norm_w, ss = sum of row^2 (taken as a
+ *                              512-thread workgroup takes it: thread t sums elements t, t + 512, ... in order, then
+ *                              the waves' partials by a fixed tree)
+ *             ORK_ROW_QUANT    y = row
+ *             then the int8 row a = clamp(rint(y / s), -127, 127), s = max|y| / 127 (1 for a zero row), the
+ *             per-row quantisation of examples/quant.c:34-37; s is written to *row_scale when non-NULL.
+ *   epilogue  on each output column's exact int32 sum c[n] = sum_k a[k] * B[k][n]:
+ *             ORK_COL_STORE    C[i][n] = c (S = 1..3 weights, e.g. q / k / v, each into its own C[i])
+ *             ORK_COL_RESID    out[n] += (c * s) * w_scale[0][n]                            (S = 1: a residual add)
+ *             ORK_COL_SWIGLU   out[n] = silu(g) * u, g = (c_gate * s) * w_scale[0][n], u = (c_up * s) * w_scale[1][n],
+ *                              silu(g) = g / (1 + exp(-g))         (S = 2: gate and up weights of one shape and kind)
+ * Built combinations: RMSNORM + STORE (int8 weights), QUANT + RESID and RMSNORM + SWIGLU (every kind); others -2.
+ * Every pointer is device memory (ork_dev_alloc or hipMalloc); `out` and the C[i] must not overlap the row. Products
+ * and sums round as written (no fused multiply-add), so a caller that prepares the row by these operations in this
+ * order and runs ork_i8_mm_run gets the same results bit for bit. Returns 0 after the launch in async mode, else
+ * after the stream sync; -2 for bad arguments or an unbuilt combination; -1 on a device failure. */
+#define ORK_ROW_KMAX 8192
+enum { ORK_ROW_RMSNORM = 0, ORK_ROW_QUANT = 1 };
+enum { ORK_COL_STORE = 0, ORK_COL_RESID = 1, ORK_COL_SWIGLU = 2 };
+typedef struct ork_row_op {
+    int prologue;              /* ORK_ROW_* */
+    const float *row;          /* f32[K] */
+    const float *norm_w;       /* f32[K], ORK_ROW_RMSNORM */
+    float eps;                 /* ORK_ROW_RMSNORM */
+    float *row_scale;          /* nullable: s */
+    int epilogue;              /* ORK_COL_* */
+    int32_t *C[3];             /* ORK_COL_STORE: int32[N] of weight i */
+    const float *w_scale[2];   /* per-output-channel weight scales f32[N]: RESID [0]; SWIGLU gate [0], up [1] */
+    float *out;                /* RESID: f32[N] updated in place; SWIGLU: f32[N] written */
+} ork_row_op;
+int          ork_i8_mm_run_row(ork_npu *ctx, int S, ork_w *const *w, const ork_row_op *op);
 /* Profiling: enqueue on the context's stream a timestamp of the device wall clock, written to 8-byte aligned
  * device memory dev_u64 when the stream reaches it (a tiny kernel, so it also works inside a captured HIP graph,
  * where event timestamps are not available). ork_npu_wallclock_khz gives the clock's constant rate. 0 / -1. */

@@ -106,37 +106,47 @@ class Qwen3Ref:
 
     def forward(self, tokens, pos0):
         """Rows `tokens` at positions pos0.. (the cache holds 0..pos0-1); returns the last row's logits."""
+        x = self.emb[np.asarray(tokens)]
+        for l in range(self.c.layers):
+            x = self.layer(l, x, pos0)
+        return self.head(x)
+
+    def layer(self, l, x, pos0):
+        """Decoder layer l (examples/bench.c:128-145) on the residual rows x [M][H] at positions pos0..: appends
+        their keys and values to layer l's cache (which holds positions 0..pos0-1) and returns the rows leaving the
+        layer. Fed another engine's rows, it checks one layer on that engine's input (teacher forcing)."""
         c = self.c
         NH, NKV, HD, eps = c.heads, c.kv_heads, c.head_dim, c.eps
         G = NH // NKV
         scale = F32(1.0) / np.sqrt(F32(HD))
-        x = self.emb[np.asarray(tokens)]
+        x = np.asarray(x, F32)
         M = x.shape[0]
-        for l in range(c.layers):
-            h = rmsnorm(x, self.norms[(l, 0)], eps)
-            q, k, v = self.lin[(l, 0)](h), self.lin[(l, 1)](h), self.lin[(l, 2)](h)
-            att = np.zeros_like(q)
-            for t in range(M):
-                pos = pos0 + t
-                cs, sn = self.cos[pos], self.sin[pos]
-                qh = rope(rmsnorm(q[t].reshape(NH, HD), self.norms[(l, 2)], eps), cs, sn)
-                kh = rope(rmsnorm(k[t].reshape(NKV, HD), self.norms[(l, 3)], eps), cs, sn)
-                self.kc[l, pos] = kh.reshape(-1)
-                self.vc[l, pos] = v[t]
-            for t in range(M):
-                L = pos0 + t + 1
-                cs, sn = self.cos[pos0 + t], self.sin[pos0 + t]
-                qh = rope(rmsnorm(q[t].reshape(NH, HD), self.norms[(l, 2)], eps), cs, sn)
-                for hh in range(NH):
-                    g = hh // G
-                    K = self.kc[l, :L, g * HD:(g + 1) * HD]
-                    V = self.vc[l, :L, g * HD:(g + 1) * HD]
-                    att[t, hh * HD:(hh + 1) * HD] = attend(qh[hh], K, V, scale)
-            x = x + self.lin[(l, 3)](att)
-            h2 = rmsnorm(x, self.norms[(l, 1)], eps)
-            a = silu_mul(self.lin[(l, 4)](h2), self.lin[(l, 5)](h2))
-            x = x + self.lin[(l, 6)](a)
-        hf = rmsnorm(x, self.norms[(-1, 0)], eps)
+        h = rmsnorm(x, self.norms[(l, 0)], eps)
+        q, k, v = self.lin[(l, 0)](h), self.lin[(l, 1)](h), self.lin[(l, 2)](h)
+        att = np.zeros_like(q)
+        for t in range(M):
+            pos = pos0 + t
+            cs, sn = self.cos[pos], self.sin[pos]
+            kh = rope(rmsnorm(k[t].reshape(NKV, HD), self.norms[(l, 3)], eps), cs, sn)
+            self.kc[l, pos] = kh.reshape(-1)
+            self.vc[l, pos] = v[t]
+        for t in range(M):
+            L = pos0 + t + 1
+            cs, sn = self.cos[pos0 + t], self.sin[pos0 + t]
+            qh = rope(rmsnorm(q[t].reshape(NH, HD), self.norms[(l, 2)], eps), cs, sn)
+            for hh in range(NH):
+                g = hh // G
+                K = self.kc[l, :L, g * HD:(g + 1) * HD]
+                V = self.vc[l, :L, g * HD:(g + 1) * HD]
+                att[t, hh * HD:(hh + 1) * HD] = attend(qh[hh], K, V, scale)
+        x = x + self.lin[(l, 3)](att)
+        h2 = rmsnorm(x, self.norms[(l, 1)], eps)
+        a = silu_mul(self.lin[(l, 4)](h2), self.lin[(l, 5)](h2))
+        return x + self.lin[(l, 6)](a)
+
+    def head(self, x):
+        """Final norm and LM head of the last row of x [M][H]: its logits."""
+        hf = rmsnorm(np.asarray(x, F32), self.norms[(-1, 0)], self.c.eps)
         return self.lin[(-1, 0)](hf[-1:])[0]
 
 

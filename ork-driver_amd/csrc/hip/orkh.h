@@ -77,6 +77,14 @@ int         orkh_mark(void *dev_u64, void *stream);
 /* streaming read of `bytes` device bytes, one XOR word per workgroup into sink; the workgroup count, or -1 */
 long long   orkh_read_probe(const void *dev, size_t bytes, unsigned *sink, void *stream);
 int         orkh_device_sync(void);
+/* Timing events: a HIP event (NULL on failure), recorded in stream order; orkh_event_ms waits for e1 and gives the
+ * milliseconds between the two recordings (-1 on a HIP error). */
+void       *orkh_event_new(void);
+void        orkh_event_free(void *ev);
+int         orkh_event_record(void *ev, void *stream);
+float       orkh_event_ms(void *e0, void *e1);
+/* 1 if the stream is being captured into a HIP graph, 0 if not, -1 on a HIP error. */
+int         orkh_stream_capturing(void *stream);
 /* 1 if p is device (or device-mapped) memory known to the HIP runtime, 0 if plain host memory. */
 int         orkh_ptr_is_device(const void *p);
 
@@ -149,6 +157,34 @@ typedef struct orkh_group {
 int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *plan, int G, const float *aS, const float *bS, float *C,
                            int ldc, void *stream);
 int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream);
+/* One-row run with a fused row prologue and column epilogue (k_gemv_row, orkh_rowrun.hip): every workgroup builds the
+ * int8 row in LDS from a float row (pro: ORKH_ROW_RMSNORM = RMSNorm with weight nw, then the per-row quant;
+ * ORKH_ROW_QUANT = the per-row quant), runs the M = 1 GEMV on its panel or half panel, and applies epi to its
+ * columns' int32 sums: ORKH_COL_STORE C[t][n] = c; ORKH_COL_RESID x[n] += (c * s) * ws0[n]; ORKH_COL_SWIGLU
+ * y[n] = silu((c_gate * s) * ws0[n]) * ((c_up * s) * ws1[n]), s the row's scale (written to *as_out by workgroup 0
+ * when non-NULL). Built: RMSNORM + STORE (ORKH_I8), QUANT + RESID and RMSNORM + SWIGLU (ORKH_I8 / I4U / NF4). */
+enum { ORKH_ROW_RMSNORM = 0, ORKH_ROW_QUANT = 1 };
+enum { ORKH_COL_STORE = 0, ORKH_COL_RESID = 1, ORKH_COL_SWIGLU = 2 };
+#define ORKH_ROW_KMAX 8192 /* bytes of the int8 row in LDS: KB * (64 or 128) <= this */
+typedef struct orkh_row {
+    int kind, K, KB;      /* panel kind (ORKH_I8 / ORKH_I4U / ORKH_NF4), row length, K-blocks per panel */
+    uint32_t lut[4];      /* ORKH_NF4 codebook */
+    int pro, epi;
+    int nt;               /* STORE: 1..3 weights, their workgroups back to back; RESID 1; SWIGLU 2 (gate, up) */
+    const void *B[3];     /* panels of each weight */
+    int nb[3];            /* 16-column panels (N / 16) of each weight */
+    int32_t *C[3];        /* STORE */
+    const float *row;     /* the float row, K elements */
+    const float *nw;      /* RMSNORM weight, K elements */
+    float eps;
+    float *as_out;        /* nullable */
+    const float *ws0, *ws1;
+    float *x;             /* RESID: updated in place (must not overlap row) */
+    float *y;             /* SWIGLU: output (must not overlap row) */
+    int half;             /* 1: half a panel (8 columns) per workgroup */
+} orkh_row;
+/* 0 / -2 an unbuilt combination or bad fields / -1 HIP error */
+int orkh_row_launch(const orkh_row *p, void *stream);
 /* Bytes of LDS the stage ring of k_tiled2 takes for (kind, bm x bn); -1 for a tile that is not built. */
 int orkh_tiled2_ring_lds(int kind, int bm, int bn);
 /* Names of the compiled kernel variants, for diagnostics ("stream_i8_mt1_w4", ...). */

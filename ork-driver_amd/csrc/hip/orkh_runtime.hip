@@ -202,6 +202,35 @@ int orkh_sync(void *stream) {
     return 0;
 }
 
+void *orkh_event_new(void) {
+    hipEvent_t e = nullptr;
+    hipError_t r = hipEventCreate(&e);
+    if (r != hipSuccess) { fail(r, "hipEventCreate"); return nullptr; }
+    return (void *)e;
+}
+
+void orkh_event_free(void *ev) {
+    if (ev) (void)hipEventDestroy((hipEvent_t)ev);
+}
+
+int orkh_event_record(void *ev, void *stream) {
+    CK(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream), "hipEventRecord");
+    return 0;
+}
+
+float orkh_event_ms(void *e0, void *e1) {
+    if (hipEventSynchronize((hipEvent_t)e1) != hipSuccess) return -1.f;
+    float ms = -1.f;
+    if (hipEventElapsedTime(&ms, (hipEvent_t)e0, (hipEvent_t)e1) != hipSuccess) return -1.f;
+    return ms;
+}
+
+int orkh_stream_capturing(void *stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &st) != hipSuccess) return -1;
+    return st == hipStreamCaptureStatusActive ? 1 : 0;
+}
+
 int orkh_device_sync(void) {
     CK(hipDeviceSynchronize(), "hipDeviceSynchronize");
     return 0;

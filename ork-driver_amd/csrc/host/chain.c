@@ -32,6 +32,12 @@ typedef struct {
 
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+/* An fp16 GEMV task whose own plan splits K exactly as the grouped whole-panel launch would (wpg waves, each over
+ * one run of ceil(KB / wpg) blocks): its fp32 results in a group equal its single run's bit for bit. */
+static int f16_groupable(const orkh_plan *q, int KB, int wpg) {
+    return !q->half && q->wpg == wpg && q->kbw == (KB + wpg - 1) / wpg;
+}
+
 /* esz_a: bytes per A element. tasks arrive as (w, M, A, C, cstride) in a normalised array. */
 static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_dt, int esz_a) {
     if (orki_need_device(c, who)) return -1;
@@ -60,6 +66,8 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
             return -1;
     }
 
+    orki_ptok pt;
+    orki_prof_begin(c, &pt, 1);
     /* residency: device buffers are used in place, host operands go through one staging pass */
     size_t ha = 0, hc = 0, ws = 0;
     for (int i = 0; i < S; i++) {
@@ -102,21 +110,26 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
         if (wsi > ws) ws = wsi;
     }
     void *dws = NULL;
-    if (ws && !(dws = orki_stage(c, &c->sW, ws))) { free(q); orki_hip_fail(who); return -1; }
+    if (ws && !(dws = orki_ws_stage(c, ws, NULL))) { free(q); orki_hip_fail(who); return -1; }
 
     int rc = 0;
     char *done = calloc((size_t)S, 1);
     if (!done) { free(q); orki_err("%s: out of memory", who); return -1; }
-    /* grouped launches: M = 1 GEMV tasks of one resident kind, in task order, ORKH_GROUP_MAX at a time */
+    /* grouped launches: M = 1 GEMV tasks of one resident kind, in task order, ORKH_GROUP_MAX at a time. The grouped
+     * kernel runs whole panels with one wave split per launch; integer sums are exact under any split, but an fp16
+     * task joins only when its own plan has that same geometry (whole panels, the same waves and K-blocks per wave),
+     * so that its fp32 sums run in the order of its single run. Others launch below with their own plans. */
     for (int i = 0; i < S && !rc; i++) {
         if (done[i] || q[i].algo != ORKH_ALGO_GEMV || q[i].ksplit != 1) continue;
         orkh_group g;
         memset(&g, 0, sizeof g);
         /* the grouped kernel runs whole panels: their wave count, whatever geometry the task's own plan has */
         const int wpg = orki_gemv_panel_wpg(c, t[i].w->rkind, t[i].w->KB, t[i].w->N / 16);
+        if (t[i].w->rkind == ORKH_F16 && !f16_groupable(&q[i], t[i].w->KB, wpg)) continue;
         int wg = 0;
         for (int j = i; j < S && g.n < ORKH_GROUP_MAX; j++) {
             if (done[j] || q[j].algo != ORKH_ALGO_GEMV || q[j].ksplit != 1 || t[j].w->rkind != t[i].w->rkind) continue;
+            if (t[j].w->rkind == ORKH_F16 && !f16_groupable(&q[j], t[j].w->KB, wpg)) continue;
             orkh_gtask *gt = &g.t[g.n++];
             gt->p.kind = t[j].w->rkind;
             gt->p.M = 1;
@@ -206,8 +219,15 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
         }
     }
     for (int i = 0; i < S; i++) all_dev &= t[i].a_dev;
-    if (c->async && all_dev) return 0;
+    orki_prof_launched(c, &pt);
+    char pname[32];
+    snprintf(pname, sizeof pname, "%d tasks", S);
+    if (c->async && all_dev && !(ws && c->ws_guard)) {
+        orki_prof_end(c, &pt, who, pname);
+        return 0;
+    }
     if (orkh_sync(c->stream)) { orki_hip_fail(who); return -1; }
+    if (ws && orki_ws_check(c, dws, ws, who)) return -1;
     size_t o = 0;
     if (c_pinned)
         for (int i = 0; i < S; i++) {
@@ -217,6 +237,8 @@ static int chain_common(const char *who, ork_npu *c, int S, ctask *t, int want_d
                 memcpy((char *)t[i].C + (size_t)m * t[i].ldc * 4, hc_h + o + (size_t)m * row, row);
             o += al256((size_t)t[i].M * row);
         }
+    orki_prof_end(c, &pt, who, pname);
+    orki_prof_settle(c);
     return 0;
 }
 

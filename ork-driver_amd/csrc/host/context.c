@@ -78,6 +78,8 @@ static ork_npu *ctx_new(void) {
     pthread_mutex_init(&c->mu, NULL);
     const char *dbg = getenv("ORK_PLAN_DEBUG");
     c->plan_knobs = dbg && *dbg && strcmp(dbg, "0") != 0;
+    const char *gd = getenv("ORK_WS_GUARD");
+    c->ws_guard = c->plan_knobs && gd && *gd && strcmp(gd, "0") != 0;
     return c;
 }
 
@@ -103,6 +105,7 @@ ork_npu *ork_npu_init(void) {
     c->soc[i] = 0;
     c->cores = c->dev.cu_count;
     c->core_budget = c->cores;
+    orki_prof_init(c);
     if (strcmp(c->soc, "gfx950") != 0)
         orki_err("ork_npu_init: device is %s, kernels are built for gfx950 only", c->soc);
     return c;
@@ -124,11 +127,13 @@ ork_npu *ork_npu_init_offline(const char *soc_id) {
     snprintf(c->soc, sizeof c->soc, "%s", known[hit].id);
     c->cores = known[hit].cores;
     c->core_budget = c->cores;
+    orki_prof_init(c);
     return c;
 }
 
 void ork_npu_free(ork_npu *c) {
     if (!c) return;
+    orki_prof_dump(c);
     if (!c->offline) {
         if (c->stream) (void)orkh_sync(c->stream);
         orkh_free(c->sA.p);
@@ -179,6 +184,43 @@ void *orki_stage(ork_npu *c, struct ork_buf *b, size_t n) {
     b->n = b->p ? want : 0;
     if (!b->p) orki_hip_fail("staging alloc");
     return b->p;
+}
+
+/* The guard pattern: a byte sequence no kernel's partials produce by accident in a whole band. */
+static unsigned char g_guard_pat[ORKI_WS_GUARD];
+static pthread_once_t g_guard_once = PTHREAD_ONCE_INIT;
+static void guard_pat_init(void) {
+    for (int i = 0; i < ORKI_WS_GUARD; i++) g_guard_pat[i] = (unsigned char)(0xA5 ^ (i * 31) ^ (i >> 8));
+}
+
+void *orki_ws_stage(ork_npu *c, size_t ws, void *fixed) {
+    if (!c->ws_guard) return fixed ? fixed : orki_stage(c, &c->sW, ws);
+    pthread_once(&g_guard_once, guard_pat_init);
+    char *base = fixed ? fixed : orki_stage(c, &c->sW, ws + 2 * ORKI_WS_GUARD);
+    if (!base) return NULL;
+    if (orkh_h2d(base, g_guard_pat, ORKI_WS_GUARD, c->stream) ||
+        orkh_h2d(base + ORKI_WS_GUARD + ws, g_guard_pat, ORKI_WS_GUARD, c->stream))
+        return NULL;
+    return base + ORKI_WS_GUARD;
+}
+
+int orki_ws_check(ork_npu *c, const void *ws_base, size_t ws, const char *who) {
+    if (!c->ws_guard || !ws_base) return 0;
+    unsigned char got[2][ORKI_WS_GUARD];
+    const char *b = ws_base;
+    if (orkh_d2h(got[0], b - ORKI_WS_GUARD, ORKI_WS_GUARD, c->stream) ||
+        orkh_d2h(got[1], b + ws, ORKI_WS_GUARD, c->stream) || orkh_sync(c->stream)) {
+        orki_hip_fail(who);
+        return -1;
+    }
+    for (int s = 0; s < 2; s++)
+        for (int i = 0; i < ORKI_WS_GUARD; i++)
+            if (got[s][i] != g_guard_pat[i]) {
+                orki_err("%s: split-K partials overran their workspace: guard byte %s%d changed", who,
+                         s ? "+" : "-", s ? i : ORKI_WS_GUARD - i);
+                return -1;
+            }
+    return 0;
 }
 
 /* Pinned, device-mapped host staging, grown on demand like orki_stage. */
@@ -360,6 +402,7 @@ void ork_npu_set_async(ork_npu *c, int on) { if (c) c->async = on ? 1 : 0; }
 int ork_npu_sync(ork_npu *c) {
     if (orki_need_device(c, "ork_npu_sync")) return -1;
     if (orkh_sync(c->stream)) { orki_hip_fail("ork_npu_sync"); return -1; }
+    orki_prof_settle(c);
     return 0;
 }
 

@@ -23,6 +23,7 @@ enum { DT_F16 = 0, DT_I8 = 1, DT_I4 = 2 };
 #define ORK_DMA_MAX 64 /* zero-copy table size, as the reference (src/npu/internal.h:94-96) */
 
 struct ork_buf { void *p; size_t n; };
+struct orki_prof;
 
 struct ork_npu {
     int offline;           /* ork_npu_init_offline: caps only, no device */
@@ -35,6 +36,10 @@ struct ork_npu {
      * ORK_TILE, ORK_KSPLIT, ORK_ALINE, ORK_STREAM_NP, ORK_WPG), read at each plan so a test can switch them
      * between runs. Without it the planner reads no environment at all. */
     int plan_knobs;
+    /* ORK_WS_GUARD set as well (tests): split-K partials get ORKI_WS_GUARD bytes of a fixed pattern on each side,
+     * checked after the run's sync (which async mode then does not skip), so a kernel that writes past them fails
+     * the run with -1 */
+    int ws_guard;
     /* device staging for host-side A / C, split-K / grouped partials and grouped-run scales, grown on demand */
     struct ork_buf sA, sC, sW, sS;
     /* pinned, device-mapped host staging for host-side A (filled by the CPU, uploaded by one DMA copy) and
@@ -45,6 +50,8 @@ struct ork_npu {
     int dma_n;
     struct ork_buf *devb;
     int devb_n, devb_cap;
+    /* ORK_PROFILE set when the context was made: per-call timing, printed at ork_npu_free (prof.c); else NULL */
+    struct orki_prof *prof;
     /* device memory of weights whose handles were released with ork_w_free */
     void **orphan;
     int orphan_n, orphan_cap;
@@ -122,6 +129,26 @@ void  orki_host_c_done(ork_npu *c, void *C, size_t n, int mode);
 void  orki_orphan(ork_npu *c, void *dptr);
 ork_w *orki_w_new(ork_npu *c, int K, int N, int dtype, int rkind);
 int   orki_w_upload(ork_w *w, const void *panels);
+
+/* ---- split-K workspace guard bands (ork_npu.ws_guard) ---- */
+#define ORKI_WS_GUARD 4096
+/* Stage a split-K workspace of ws bytes for one run or chain: the context's grown buffer (or `fixed`, holding at
+ * least ws + 2 * ORKI_WS_GUARD bytes when guarded, for the no-allocation run), with the guard bands filled on the
+ * stream when the context guards. NULL on failure. */
+void *orki_ws_stage(ork_npu *c, size_t ws, void *fixed);
+/* After the stream sync: 0 if the guard bands around the workspace orki_ws_stage returned are intact (or the
+ * context does not guard), -1 with a message naming `who` if a kernel wrote into them. */
+int   orki_ws_check(ork_npu *c, const void *ws_base, size_t ws, const char *who);
+
+/* ---- ORK_PROFILE (prof.c): around each successful run call, begin (device: 1 to time its launches with events
+ * on the stream), launched (after its last launch), end (on return; host wall time). No-ops without ORK_PROFILE. */
+typedef struct { double t0; int pair; } orki_ptok;
+void orki_prof_init(ork_npu *c);
+void orki_prof_begin(ork_npu *c, orki_ptok *t, int device);
+void orki_prof_launched(ork_npu *c, orki_ptok *t);
+void orki_prof_end(ork_npu *c, orki_ptok *t, const char *who, const char *plan);
+void orki_prof_settle(ork_npu *c); /* after a stream sync: read back the pending event pairs */
+void orki_prof_dump(ork_npu *c);   /* print the rows, release the profile */
 
 /* ---- host GEMMs of an offline context (cpu_gemm.c): exact int32, and the grouped float accumulate ---- */
 int orki_cpu_gemm_grouped(int M, int K, int N, int G, const int8_t *A, const int8_t *B_kn, const float *aS,

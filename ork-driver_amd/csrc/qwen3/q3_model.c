@@ -26,9 +26,6 @@ struct q3_lin {
     ork_w *w;
     float *ws; /* device: per-output-channel scales */
     int K, N;
-    const void *pan; /* the weight's resident panels (ork_w_device_panels), for the fused decode kernels */
-    int KB, kind;
-    unsigned lut[4];
 };
 
 struct q3_layer {
@@ -59,6 +56,8 @@ struct q3_model {
     int last_row; /* row of the last LM-head input in asx */
     int fused;    /* decode with the fused M = 1 kernels where the weights allow (default 1) */
     void *graph;  /* captured decode step */
+    float *trace; /* q3_set_trace: [layers + 1][max_rows][hidden] layer-input rows of the last pass */
+    int trace_on, trace_rows;
     void **dev;   /* every device buffer of the model */
     int ndev, capdev;
 };
@@ -342,8 +341,6 @@ int q3_set_linear(q3_model *m, int layer, int which, const float *w) {
     }
     if (L->w) ork_mm_free(m->ctx, L->w);
     L->w = pw;
-    L->pan = NULL;
-    if (ork_w_device_panels(pw, &L->pan, &L->KB, &L->kind, L->lut)) L->pan = NULL;
     /* a captured decode step holds the old weight's addresses */
     if (m->graph) {
         (void)ork_npu_sync(m->ctx);
@@ -402,6 +399,36 @@ int q3_init_random(q3_model *m, uint64_t seed, float std) {
     return rc;
 }
 
+/* ---- layer-input trace (q3_set_trace) ---------------------------------------------------------------------- */
+static int trace_x(q3_model *m, int l, int M) {
+    if (!m->trace_on) return 0;
+    const size_t H = (size_t)m->c.hidden;
+    return q3k_copy_f32(m->trace + (size_t)l * m->c.max_rows * H, m->x, (long long)M * (long long)H, m->stream);
+}
+
+int q3_set_trace(q3_model *m, int on) {
+    if (!m) return -2;
+    if (on && !m->trace) {
+        m->trace = dalloc(m, (size_t)(m->c.layers + 1) * m->c.max_rows * m->c.hidden * 4);
+        if (!m->trace) return -1;
+    }
+    if ((on != 0) != m->trace_on) { /* a captured step holds the other form */
+        if (ork_npu_sync(m->ctx)) return -1;
+        q3g_destroy(m->graph);
+        m->graph = NULL;
+    }
+    m->trace_on = on != 0;
+    m->trace_rows = 0;
+    return 0;
+}
+
+int q3_layer_rows(q3_model *m, int l, float *out, int rows) {
+    if (!m || !out || !m->trace || l < 0 || l > m->c.layers || rows < 1 || rows > m->trace_rows) return -2;
+    if (ork_npu_sync(m->ctx)) return -1;
+    const size_t H = (size_t)m->c.hidden;
+    return ork_dev_download(m->ctx, out, m->trace + (size_t)l * m->c.max_rows * H, (size_t)rows * H * 4) ? -1 : 0;
+}
+
 /* ---- one pass of the decoder over M rows ------------------------------------------------------------------- */
 static int pass(q3_model *m, int M, int decode) {
     const q3_cfg *c = &m->c;
@@ -430,6 +457,7 @@ static int pass(q3_model *m, int M, int decode) {
             nq.acc_ws = m->L[l - 1].l[Q3_WD].ws;
         }
         CK(q3k_norm_quant(&nq, s));
+        CK(trace_x(m, l, M));
         ork_mm_task_i8 qkv[3] = {{Ly->l[Q3_WQ].w, M, m->a8x, m->cq, 0},
                                  {Ly->l[Q3_WK].w, M, m->a8x, m->ck, 0},
                                  {Ly->l[Q3_WV].w, M, m->a8x, m->cv, 0}};
@@ -494,47 +522,33 @@ static int pass(q3_model *m, int M, int decode) {
     fn.a8 = m->a8x;
     fn.as = m->asx;
     CK(q3k_norm_quant(&fn, s));
+    CK(trace_x(m, c->layers, M));
     CK(ork_i8_mm_run(m->ctx, m->lm.w, 1, m->a8x + (size_t)(M - 1) * H, m->clog));
     const q3_amax am = {c->vocab, m->clog, m->asx + (M - 1), m->lm.ws, m->best};
     CK(q3k_argmax(&am, s));
     m->last_row = M - 1;
+    m->trace_rows = m->trace_on ? M : 0;
     return 0;
 }
 
 /* ---- the fused decode step (M = 1) --------------------------------------------------------------------------- *
- * Per layer: q/k/v as one k_fgemv whose prologue is the attention RMSNorm + int8 row (layer 0: the embedding
- * kernel and the q/k/v chain, as in pass()); attention partials; the chunk combine into an fp32 row; o with the
- * row's quant in its prologue and the residual add in its epilogue; gate/up with the FFN RMSNorm prologue and the
- * silu(g) * u epilogue; down with the quant prologue and the residual add. 6 launches per layer instead of 9, with
- * the same float operations in the same order, so logits and tokens equal those of pass(). */
+ * Per layer: q/k/v as one ork_i8_mm_run_row (the library's one-row run: RMSNorm + int8 row in its prologue, the
+ * three int32 results stored; layer 0: the embedding kernel and the q/k/v chain, as in pass()); attention partials;
+ * the chunk combine into an fp32 row; o (the row's quant in the prologue, the residual add in the epilogue);
+ * gate/up (the FFN RMSNorm prologue, the silu(g) * u epilogue); down (quant prologue, residual add). 6 launches per
+ * layer instead of 9, with the same float operations in the same order (orkh_rowops.h), so logits and tokens equal
+ * those of pass(). */
 static int fused_ok(const q3_model *m) {
     const q3_cfg *c = &m->c;
     if (!m->fused) return 0;
-    for (int l = 0; l < c->layers; l++) {
-        const struct q3_lin *L = m->L[l].l;
-        for (int i = 0; i < Q3_NLIN; i++) {
-            const int kpb = L[i].kind == 0 ? 64 : 128;
-            if (!L[i].pan || L[i].kind < 0 || L[i].kind > 2 || L[i].N % 16 || L[i].KB * kpb > Q3_FG_KMAX) return 0;
-        }
-        if (L[Q3_WQ].kind || L[Q3_WK].kind || L[Q3_WV].kind || L[Q3_WQ].KB != L[Q3_WK].KB ||
-            L[Q3_WQ].KB != L[Q3_WV].KB || L[Q3_WG].kind != L[Q3_WU].kind || L[Q3_WG].KB != L[Q3_WU].KB)
-            return 0;
-    }
-    return 1;
-}
-
-/* A fused matmul over P panels runs half a panel per workgroup unless whole panels already spread evenly over the
- * CUs (P a multiple of the CU count), the rule of the library's M = 1 planner: o and down (128 panels) and the
- * gate/up pair (384) take halves, q/k/v (256) whole panels. */
-static int fg_half(const q3_model *m, int P) {
-    const int cu = ork_npu_cores(m->ctx) > 0 ? ork_npu_cores(m->ctx) : 256;
-    return !(P >= cu && (2 * P + cu - 1) / cu >= 2 * ((P + cu - 1) / cu));
+    /* the row bound of the fused run; q/k/v / o are int8, the FFN weights int8, uniform int4 or NF4 */
+    return c->hidden <= ORK_ROW_KMAX && c->ffn <= ORK_ROW_KMAX && c->heads * c->head_dim <= ORK_ROW_KMAX;
 }
 
 static int pass_fused(q3_model *m) {
     const q3_cfg *c = &m->c;
     void *s = m->stream;
-    const int H = c->hidden, NH = c->heads, NKV = c->kv_heads, HD = c->head_dim, F = c->ffn;
+    const int H = c->hidden, NH = c->heads, NKV = c->kv_heads, HD = c->head_dim;
     for (int l = 0; l < c->layers; l++) {
         struct q3_layer *Ly = &m->L[l];
         const struct q3_lin *Lq = &Ly->l[Q3_WQ], *Lk = &Ly->l[Q3_WK], *Lv = &Ly->l[Q3_WV], *Lo = &Ly->l[Q3_WO],
@@ -554,31 +568,24 @@ static int pass_fused(q3_model *m) {
             nq.emb = m->emb;
             nq.best = m->best;
             CK(q3k_norm_quant(&nq, s));
+            CK(trace_x(m, 0, 1));
             ork_mm_task_i8 qkv[3] = {{Lq->w, 1, m->a8x, m->cq, 0}, {Lk->w, 1, m->a8x, m->ck, 0},
                                      {Lv->w, 1, m->a8x, m->cv, 0}};
             CK(ork_i8_mm_run_chain(m->ctx, 3, qkv));
         } else {
-            q3_fg f = {0};
-            f.K = H;
-            f.KB = Lq->KB;
-            f.kind = 0;
-            f.epi = Q3_EPI_STORE;
-            f.nt = 3;
-            f.B[0] = Lq->pan;
-            f.B[1] = Lk->pan;
-            f.B[2] = Lv->pan;
-            f.nb[0] = Lq->N / 16;
-            f.nb[1] = Lk->N / 16;
-            f.nb[2] = Lv->N / 16;
+            CK(trace_x(m, l, 1)); /* the previous layer's down epilogue completed the residual row */
+            ork_w *const wq[3] = {Lq->w, Lk->w, Lv->w};
+            ork_row_op f = {0};
+            f.prologue = ORK_ROW_RMSNORM;
+            f.row = m->x;
+            f.norm_w = Ly->n1;
+            f.eps = c->eps;
+            f.row_scale = m->asx;
+            f.epilogue = ORK_COL_STORE;
             f.C[0] = m->cq;
             f.C[1] = m->ck;
             f.C[2] = m->cv;
-            f.row = m->x;
-            f.nw = Ly->n1;
-            f.eps = c->eps;
-            f.as_out = m->asx;
-            f.half = fg_half(m, f.nb[0] + f.nb[1] + f.nb[2]);
-            CK(q3k_fgemv(&f, s));
+            CK(ork_i8_mm_run_row(m->ctx, 3, wq, &f));
         }
         q3_att at = {.M = 1, .NH = NH, .NKV = NKV, .HD = HD, .S = m->S, .max_ctx = c->max_ctx, .q = m->q,
                      .kc = Ly->kc, .vc = Ly->vc, .st = m->st, .scale = 1.0f / sqrtf((float)HD), .part = m->part,
@@ -587,53 +594,33 @@ static int pass_fused(q3_model *m) {
         CK(q3k_attn_part(&at, s));
         const q3_comb cb = {NH, HD, m->S, m->part, m->att};
         CK(q3k_attn_combine(&cb, s));
-        q3_fg fo = {0};
-        fo.K = NH * HD;
-        fo.KB = Lo->KB;
-        fo.kind = Lo->kind;
-        fo.epi = Q3_EPI_RESID;
-        fo.nt = 1;
-        fo.B[0] = Lo->pan;
-        fo.nb[0] = H / 16;
+        ork_row_op fo = {0};
+        fo.prologue = ORK_ROW_QUANT;
         fo.row = m->att;
-        fo.ws0 = Lo->ws;
-        fo.x = m->x;
-        fo.half = fg_half(m, fo.nb[0]);
-        CK(q3k_fgemv(&fo, s));
-        q3_fg fg = {0};
-        fg.K = H;
-        fg.KB = Lg->KB;
-        fg.kind = Lg->kind;
-        memcpy(fg.lut, Lg->lut, sizeof fg.lut);
-        fg.epi = Q3_EPI_SWIGLU;
-        fg.nt = 2;
-        fg.B[0] = Lg->pan;
-        fg.B[1] = Lu->pan;
-        fg.nb[0] = F / 16;
-        fg.nb[1] = F / 16;
+        fo.epilogue = ORK_COL_RESID;
+        fo.w_scale[0] = Lo->ws;
+        fo.out = m->x;
+        CK(ork_i8_mm_run_row(m->ctx, 1, &Lo->w, &fo));
+        ork_w *const wgu[2] = {Lg->w, Lu->w};
+        ork_row_op fg = {0};
+        fg.prologue = ORK_ROW_RMSNORM;
         fg.row = m->x;
-        fg.nw = Ly->n2;
+        fg.norm_w = Ly->n2;
         fg.eps = c->eps;
-        fg.ws0 = Lg->ws;
-        fg.ws1 = Lu->ws;
-        fg.y = m->yffn;
-        fg.half = fg_half(m, fg.nb[0]);
-        CK(q3k_fgemv(&fg, s));
-        q3_fg fd = {0};
-        fd.K = F;
-        fd.KB = Ld->KB;
-        fd.kind = Ld->kind;
-        memcpy(fd.lut, Ld->lut, sizeof fd.lut);
-        fd.epi = Q3_EPI_RESID;
-        fd.nt = 1;
-        fd.B[0] = Ld->pan;
-        fd.nb[0] = H / 16;
+        fg.epilogue = ORK_COL_SWIGLU;
+        fg.w_scale[0] = Lg->ws;
+        fg.w_scale[1] = Lu->ws;
+        fg.out = m->yffn;
+        CK(ork_i8_mm_run_row(m->ctx, 2, wgu, &fg));
+        ork_row_op fd = {0};
+        fd.prologue = ORK_ROW_QUANT;
         fd.row = m->yffn;
-        fd.ws0 = Ld->ws;
-        fd.x = m->x;
-        fd.half = fg_half(m, fd.nb[0]);
-        CK(q3k_fgemv(&fd, s));
+        fd.epilogue = ORK_COL_RESID;
+        fd.w_scale[0] = Ld->ws;
+        fd.out = m->x;
+        CK(ork_i8_mm_run_row(m->ctx, 1, &Ld->w, &fd));
     }
+    CK(trace_x(m, c->layers, 1));
     q3_nq fn = {0}; /* the residual add is done: plain final norm */
     fn.M = 1;
     fn.H = H;
@@ -650,6 +637,7 @@ static int pass_fused(q3_model *m) {
     const q3_amax am = {c->vocab, m->clog, m->asx, m->lm.ws, m->best};
     CK(q3k_argmax(&am, s));
     m->last_row = 0;
+    m->trace_rows = m->trace_on ? 1 : 0;
     return 0;
 }
 

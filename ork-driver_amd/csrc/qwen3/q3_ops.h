@@ -92,46 +92,19 @@ typedef struct q3_amax { /* greedy sampling over one row of logits */
     unsigned long long *best;
 } q3_amax;
 
-/* Fused M = 1 matmul of the decode step (k_fgemv): every workgroup builds the int8 row in its prologue (RMSNorm +
- * quant of the residual row, or the quant of a float row), the output columns go through an epilogue, and the
- * weights are the library's resident panels (ork_w_device_panels; layout in ork-driver_amd/csrc/hip/orkh.h).
- * The prologue and epilogue do the operations of k_norm_quant / k_attn_quant / k_swiglu_quant in the same order,
- * so rows, scales and results equal those of the unfused kernels bit for bit. */
-enum { Q3_PRO_NORM = 0, Q3_PRO_QUANT = 1 };
-enum { Q3_EPI_STORE = 0, Q3_EPI_RESID = 1, Q3_EPI_SWIGLU = 2 };
-#define Q3_FG_KMAX 8192 /* bytes of the int8 row in LDS (K-blocks padded) */
-
-typedef struct q3_fg {
-    int K, KB, kind; /* row length; K-blocks per panel; panel kind (0 int8, 1 uniform int4, 2 NF4) */
-    unsigned lut[4]; /* NF4 codebook */
-    int epi;         /* Q3_EPI_*: STORE (int8 weights, RMSNorm prologue), RESID (quant prologue), SWIGLU (RMSNorm) */
-    int nt;          /* STORE: tasks 1..3, their workgroups back to back; RESID 1; SWIGLU 2 (gate, up) */
-    const void *B[3];
-    int nb[3];      /* panels (N / 16) of each task */
-    int32_t *C[3];  /* STORE: int32 results */
-    const float *row; /* PRO_NORM (nw set): the residual row x; PRO_QUANT: the row to quantise */
-    const float *nw;  /* RMSNorm weight [K], or NULL for the plain quant */
-    float eps;
-    float *as_out;  /* the row's int8 scale, written by workgroup 0 (nullable) */
-    const float *ws0, *ws1; /* column scales (RESID: ws0; SWIGLU: gate ws0, up ws1) */
-    float *x;       /* RESID: residual row, x[n] += (c * a_scale) * ws0[n], in place (not the row read) */
-    float *y;       /* SWIGLU: output row, silu(g) * u (not the row read) */
-    int half;       /* 1: half a panel (8 columns) per workgroup, 2 x the panels' workgroups; 0: one panel each */
-} q3_fg;
-
 typedef struct q3_comb { /* grid NH: one head's chunks combined into an fp32 row */
     int NH, HD, S;
     const float *part; /* [NH][S][HD + 2] */
     float *out;        /* [NH * HD] */
 } q3_comb;
 
-int q3k_fgemv(const q3_fg *p, void *stream);
 int q3k_attn_combine(const q3_comb *p, void *stream);
 
 /* LDS bytes of k_attn_part for a workgroup of G query heads (launches above 64 KiB are refused). */
 #define Q3_ATT_LDS(G, HD) ((size_t)(Q3_CHUNK * ((HD) + 4) + 2 * (G) * (HD) + (G) * Q3_CHUNK + 2 * (G) + 2 * (HD)) * 4)
 
 int q3k_norm_quant(const q3_nq *p, void *stream);
+int q3k_copy_f32(float *dst, const float *src, long long n, void *stream); /* n floats, device to device */
 int q3k_qkv_post(const q3_qkv *p, void *stream);
 int q3k_attn_part(const q3_att *p, void *stream);
 int q3k_attn_quant(const q3_aq *p, void *stream);

@@ -19,145 +19,11 @@
 #include <stdint.h>
 
 #include "q3_ops.h"
+#include "orkh_rowops.h"
 
 namespace {
+using namespace orkr;
 
-
-// Wave-wide sum / max in every lane, on the cross-lane paths of the VALU: DPP quad_perm swaps (lanes
-// l ^ 1, l ^ 2), DPP row_half_mirror and row_mirror (the other quad of an 8-lane half, the other half of a
-// 16-lane row), then v_permlane16_swap / v_permlane32_swap (l ^ 16, l ^ 32). Every step combines the same two
-// partials in every lane (a + b == b + a), so all lanes hold the identical result. Six LDS-crossbar shuffles
-// (ds_bpermute) did the same in ~5x the latency.
-template <int CTRL> __device__ inline float dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ inline float xor16(float v) {
-    const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
-    return __builtin_bit_cast(float, (int)((threadIdx.x & 16) == 0 ? s[1] : s[0]));
-}
-__device__ inline float xor32(float v) {
-    const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
-    return __builtin_bit_cast(float, (int)((threadIdx.x & 32) == 0 ? s[1] : s[0]));
-}
-__device__ inline float wave_sum(float v) {
-    v = v + dpp<0xB1>(v);  // quad_perm [1,0,3,2]
-    v = v + dpp<0x4E>(v);  // quad_perm [2,3,0,1]
-    v = v + dpp<0x141>(v); // row_half_mirror
-    v = v + dpp<0x140>(v); // row_mirror
-    v = v + xor16(v);
-    return v + xor32(v);
-}
-__device__ inline float wave_max(float v) {
-    v = fmaxf(v, dpp<0xB1>(v));
-    v = fmaxf(v, dpp<0x4E>(v));
-    v = fmaxf(v, dpp<0x141>(v));
-    v = fmaxf(v, dpp<0x140>(v));
-    v = fmaxf(v, xor16(v));
-    return fmaxf(v, xor32(v));
-}
-// The same over aligned groups of W lanes (W = 32 or 64): a group's result in each of its lanes.
-template <int W> __device__ inline float group_sum(float v) {
-    static_assert(W == 32 || W == 64, "group width");
-    v = v + dpp<0xB1>(v);
-    v = v + dpp<0x4E>(v);
-    v = v + dpp<0x141>(v);
-    v = v + dpp<0x140>(v);
-    v = v + xor16(v);
-    if constexpr (W == 64) v = v + xor32(v);
-    return v;
-}
-template <int W> __device__ inline float group_max(float v) {
-    static_assert(W == 32 || W == 64, "group width");
-    v = fmaxf(v, dpp<0xB1>(v));
-    v = fmaxf(v, dpp<0x4E>(v));
-    v = fmaxf(v, dpp<0x141>(v));
-    v = fmaxf(v, dpp<0x140>(v));
-    v = fmaxf(v, xor16(v));
-    if constexpr (W == 64) v = fmaxf(v, xor32(v));
-    return v;
-}
-
-// Block-wide sum / max (blockDim a multiple of 64, at most 1024). red[] holds 16 floats, 16-byte aligned, and
-// must not be in use by another reduction of the same workgroup (each call site has its own): one barrier,
-// after which every thread folds the waves' partials in wave order (float4 LDS reads where they fill).
-__device__ inline float block_sum(float v, float *red) {
-    v = wave_sum(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const int nw = (int)(blockDim.x >> 6);
-    float s = 0.f;
-    if ((nw & 3) == 0) {
-        const float4 *r4 = (const float4 *)red;
-        for (int i = 0; i < nw >> 2; i++) {
-            const float4 q = r4[i];
-            s = s + q.x;
-            s = s + q.y;
-            s = s + q.z;
-            s = s + q.w;
-        }
-    } else {
-        for (int i = 0; i < nw; i++) s = s + red[i];
-    }
-    return s;
-}
-__device__ inline float block_max(float v, float *red) {
-    v = wave_max(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const int nw = (int)(blockDim.x >> 6);
-    float m = -INFINITY;
-    if ((nw & 3) == 0) {
-        const float4 *r4 = (const float4 *)red;
-        for (int i = 0; i < nw >> 2; i++) {
-            const float4 q = r4[i];
-            m = fmaxf(fmaxf(m, q.x), fmaxf(q.y, fmaxf(q.z, q.w)));
-        }
-    } else {
-        for (int i = 0; i < nw; i++) m = fmaxf(m, red[i]);
-    }
-    return m;
-}
-
-// Rows live in registers: thread i holds elements i, i + blockDim, ... (E of them, E a compile-time
-// bound), so every global load of a row is issued before the first arithmetic that needs it. Loads are
-// unconditional (from a clamped index, zeroed after): a load under a per-lane condition becomes a branch
-// whose join waits for that load, which would serialise the row's loads into one round trip each.
-template <int E, typename T>
-__device__ inline void load_row(T (&v)[E], const T *__restrict__ src, int n) {
-#pragma unroll
-    for (int k = 0; k < E; k++) {
-        const int i = threadIdx.x + k * blockDim.x;
-        const T x = src[min(i, n - 1)];
-        v[k] = i < n ? x : T(0);
-    }
-}
-
-// Per-row symmetric int8 (examples/quant.c:34-37): s = max|x| / 127 (1 when the row is zero),
-// q = clamp(rint(x / s), -127, 127). x * (1/s) is within 2 ulp of the correctly rounded x / s, so it
-// rounds to the same integer unless it lies within 1e-4 of a half-way point (|x / s| <= 127.5, where
-// 2 ulp < 1.6e-5); there the exact quotient decides.
-template <int E>
-__device__ inline void quant_regs(const float (&y)[E], int n, int8_t *__restrict__ q, float *s_out) {
-    __shared__ __align__(16) float redq[16];
-    float mx = 0.f;
-#pragma unroll
-    for (int k = 0; k < E; k++)
-        if (threadIdx.x + k * blockDim.x < (unsigned)n) mx = fmaxf(mx, fabsf(y[k]));
-    mx = block_max(mx, redq);
-    const float s = mx > 0.f ? mx / 127.0f : 1.0f;
-    const float inv = 1.0f / s;
-#pragma unroll
-    for (int k = 0; k < E; k++) {
-        const int i = threadIdx.x + k * blockDim.x;
-        if (i < n) {
-            float r = y[k] * inv;
-            if (fabsf(r - floorf(r) - 0.5f) < 1e-4f) r = y[k] / s;
-            r = fminf(fmaxf(rintf(r), -127.f), 127.f);
-            q[i] = (int8_t)(int)r;
-        }
-    }
-    if (threadIdx.x == 0) *s_out = s;
-}
 
 // Token of a greedy-sampling key (see k_argmax): low 32 bits hold ~index.
 __device__ inline int key_token(unsigned long long k) { return (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)); }
@@ -633,240 +499,6 @@ __global__ void k_argmax(q3_amax p) {
     }
 }
 
-// ---- fused M = 1 matmul of the decode step ------------------------------------------------------------------
-// k_fgemv: one 16-column panel per workgroup (pair mode: the same columns of two weights), 8 waves splitting the
-// panel's K-blocks, on the library's resident layout (lane l of a 1 KiB block holds 16 bytes of column l % 16,
-// k-group l / 16); with H, half a panel per workgroup (8 columns, twice the workgroups: the bytes spread evenly
-// over the CUs where whole panels would leave some CUs one panel and others two, or none). Around that GEMV:
-//   prologue: the int8 row, built in LDS by every workgroup: PRO_NORM = RMSNorm of the residual row then the
-//     per-row quant (norm_quant_body's operations with its 512-thread element mapping, so the sum of squares is
-//     rounded identically: elements past K add exact zeros, so any E >= K / 512 gives the same sums);
-//     PRO_QUANT = the per-row quant of a float row (quant_regs' operations; the absmax is order-independent).
-//     Each wave's weight blocks (PRE >= its share, no more: a load past the share would fetch another wave's
-//     bytes again) are loaded once the row has arrived: their latency hides behind the reductions and the
-//     quant, and the row's own loads do not queue behind them in the CU's memory pipeline (measured: issuing
-//     them first delayed the row by 1-2 us).
-//   epilogue on each column's int32 sum: STORE; RESID x[n] += (c * a_scale) * ws[n] (the residual add that
-//     k_norm_quant_acc would do next); SWIGLU y[n] = silu(g) * u from the gate and up sums (k_swiglu_quant's
-//     operations).
-// So the rows, scales and results equal those of the unfused kernels bit for bit.
-typedef int v4i_t __attribute__((ext_vector_type(4)));
-
-struct FgLut { uint32_t l0, l1, l2, l3; };
-// One dword of NF4 codes -> the int8 codebook values of its low nibbles (lo) and of its high nibbles (hi):
-// v_perm selects within the 8 bytes of two LUT words by the low 3 bits of each code, and a second v_perm takes
-// that from the upper or the lower LUT half by the code's top bit.
-__device__ inline void fg_nf4_map8(uint32_t x, const FgLut &L, uint32_t &lo, uint32_t &hi) {
-    const uint32_t i0 = x & 0x07070707u, i1 = (x >> 4) & 0x07070707u;
-    const uint32_t s0 = ((x >> 1) & 0x04040404u) | 0x03020100u;
-    const uint32_t s1 = ((x >> 5) & 0x04040404u) | 0x03020100u;
-    lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L.l3, L.l2, i0), __builtin_amdgcn_perm(L.l1, L.l0, i0), s0);
-    hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L.l3, L.l2, i1), __builtin_amdgcn_perm(L.l1, L.l0, i1), s1);
-}
-
-// One lane's 16 bytes of a block against the row: int8 = 16 k; nibble kinds = 32 k, dword d holding
-// k = 8 d .. 8 d + 3 in its low nibbles and 8 d + 4 .. 8 d + 7 in its high nibbles. Uniform int4 codes are
-// widened as 16 v (the sum is shifted back once, exactly); NF4 codes map through the codebook.
-template <int KIND>
-__device__ inline int fg_dot(v4i_t raw, const int *__restrict__ a, int acc, const FgLut &L) {
-    const uint32_t xs[4] = {(uint32_t)raw.x, (uint32_t)raw.y, (uint32_t)raw.z, (uint32_t)raw.w};
-#pragma unroll
-    for (int d = 0; d < 4; d++) {
-        if constexpr (KIND == 0) {
-            acc = __builtin_amdgcn_sdot4(a[d], (int)xs[d], acc, false);
-        } else {
-            uint32_t lo, hi;
-            if constexpr (KIND == 1) {
-                lo = (xs[d] << 4) & 0xf0f0f0f0u;
-                hi = xs[d] & 0xf0f0f0f0u;
-            } else {
-                fg_nf4_map8(xs[d], L, lo, hi);
-            }
-            acc = __builtin_amdgcn_sdot4(a[2 * d], (int)lo, acc, false);
-            acc = __builtin_amdgcn_sdot4(a[2 * d + 1], (int)hi, acc, false);
-        }
-    }
-    return acc;
-}
-
-constexpr int FG_WAVES = 8; // 512 threads: norm_quant_body's element mapping
-
-template <int PRO, int EPI, int KIND, int E, int PRE, int H>
-__global__ __launch_bounds__(FG_WAVES * 64) void k_fgemv(q3_fg p) {
-    __shared__ __align__(16) int8_t arow[Q3_FG_KMAX];
-    __shared__ __align__(16) float red[16];
-    __shared__ __align__(16) float redq[16];
-    __shared__ int racc[FG_WAVES][2][16];
-    constexpr bool PAIR = EPI == Q3_EPI_SWIGLU;
-    constexpr int KPB = KIND == 0 ? 64 : 128;
-    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int K = p.K, KB = p.KB;
-
-    // ---- this workgroup's panel(s) and this wave's K-blocks; H: columns 8 hh .. 8 hh + 7 of the panel(s), lane l
-    // taking block kb + l / 32, k-group (l / 8) % 4, column 8 hh + l % 8 (a half block is four whole 128-byte lines)
-    int t = 0, pnl = H ? (int)(blockIdx.x >> 1) : (int)blockIdx.x;
-    const int hh = H ? (int)(blockIdx.x & 1) : 0, sub = H ? lane >> 5 : 0, grp = H ? (lane >> 3) & 3 : lane >> 4;
-    const int loff = H ? grp * 16 + hh * 8 + (lane & 7) : lane;
-    if constexpr (!PAIR) {
-        while (t < p.nt - 1 && pnl >= p.nb[t]) {
-            pnl -= p.nb[t];
-            t++;
-        }
-    }
-    const int kbw = (KB + FG_WAVES - 1) / FG_WAVES, kb0 = min(wv * kbw, KB), kb1 = min(kb0 + kbw, KB);
-    const v4i_t *b0 = (const v4i_t *)p.B[t] + (size_t)pnl * KB * 64 + loff;
-    const v4i_t *b1 = PAIR ? (const v4i_t *)p.B[1] + (size_t)pnl * KB * 64 + loff : b0;
-    // ---- prologue: the int8 row in LDS
-    float y[E], nw[E];
-    load_row(y, p.row, K);
-    if constexpr (PRO == Q3_PRO_NORM) load_row(nw, p.nw, K);
-    float mx = 0.f, ss = 0.f;
-    if constexpr (PRO == Q3_PRO_NORM) {
-#pragma unroll
-        for (int k = 0; k < E; k++) ss += y[k] * y[k];
-    } else {
-#pragma unroll
-        for (int k = 0; k < E; k++)
-            if (threadIdx.x + k * blockDim.x < (unsigned)K) mx = fmaxf(mx, fabsf(y[k]));
-    }
-    // the weight blocks, issued after the first use of the row (which waits for it); clamped to the wave's own
-    // last block, branch-free (a wave without blocks re-reads the panel's last one and discards it). H: PRE load
-    // instructions of two half blocks each
-    v4i_t r0[PRE], r1[PRE];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < PRE; u++) {
-        const size_t o = (size_t)min(kb0 + (H ? 2 * u + sub : u), kb1 - 1) * 64;
-        r0[u] = __builtin_nontemporal_load(b0 + o);
-        if constexpr (PAIR) r1[u] = __builtin_nontemporal_load(b1 + o);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (PRO == Q3_PRO_NORM) {
-        ss = block_sum(ss, red);
-        const float r = 1.0f / sqrtf(ss / (float)K + p.eps);
-#pragma unroll
-        for (int k = 0; k < E; k++) y[k] = (y[k] * r) * nw[k];
-#pragma unroll
-        for (int k = 0; k < E; k++)
-            if (threadIdx.x + k * blockDim.x < (unsigned)K) mx = fmaxf(mx, fabsf(y[k]));
-    }
-    mx = block_max(mx, redq);
-    const float as = mx > 0.f ? mx / 127.0f : 1.0f;
-    {
-        const float inv = 1.0f / as;
-#pragma unroll
-        for (int k = 0; k < E; k++) {
-            const int i = threadIdx.x + k * blockDim.x;
-            if (i < K) {
-                float r = y[k] * inv;
-                if (fabsf(r - floorf(r) - 0.5f) < 1e-4f) r = y[k] / as;
-                r = fminf(fmaxf(rintf(r), -127.f), 127.f);
-                arow[i] = (int8_t)(int)r;
-            }
-        }
-        for (int i = K + (int)threadIdx.x; i < KB * KPB; i += (int)blockDim.x) arow[i] = 0;
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0 && p.as_out) *p.as_out = as;
-    __syncthreads();
-
-    // ---- the GEMV: the preloaded blocks, then any further ones of this wave
-    const FgLut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
-    const int aoff = grp * (KPB / 4);
-    int acc0 = 0, acc1 = 0;
-    if constexpr (H) {
-        // a lane whose block lies past the run (the second half of an odd run's last instruction) adds nothing
-#pragma unroll
-        for (int u = 0; u < PRE; u++) {
-            const int blk = kb0 + 2 * u + sub;
-            const bool ok = blk < kb1;
-            const int *a = (const int *)(arow + min(blk, kb1 - 1) * KPB + aoff);
-            const int d0 = fg_dot<KIND>(r0[u], a, 0, L);
-            acc0 += ok ? d0 : 0;
-            if constexpr (PAIR) {
-                const int d1 = fg_dot<KIND>(r1[u], a, 0, L);
-                acc1 += ok ? d1 : 0;
-            }
-        }
-        for (int kb = kb0 + 2 * PRE; kb < kb1; kb += 2) {
-            const int blk = kb + sub;
-            const bool ok = blk < kb1;
-            const size_t o = (size_t)min(blk, kb1 - 1) * 64;
-            const v4i_t s0 = __builtin_nontemporal_load(b0 + o);
-            v4i_t s1 = s0;
-            if constexpr (PAIR) s1 = __builtin_nontemporal_load(b1 + o);
-            const int *a = (const int *)(arow + min(blk, kb1 - 1) * KPB + aoff);
-            const int d0 = fg_dot<KIND>(s0, a, 0, L);
-            acc0 += ok ? d0 : 0;
-            if constexpr (PAIR) {
-                const int d1 = fg_dot<KIND>(s1, a, 0, L);
-                acc1 += ok ? d1 : 0;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int u = 0; u < PRE; u++) {
-            if (kb0 + u < kb1) {
-                const int *a = (const int *)(arow + (kb0 + u) * KPB + aoff);
-                acc0 = fg_dot<KIND>(r0[u], a, acc0, L);
-                if constexpr (PAIR) acc1 = fg_dot<KIND>(r1[u], a, acc1, L);
-            }
-        }
-        for (int kb = kb0 + PRE; kb < kb1; kb++) {
-            const v4i_t s0 = __builtin_nontemporal_load(b0 + (size_t)kb * 64);
-            v4i_t s1 = s0;
-            if constexpr (PAIR) s1 = __builtin_nontemporal_load(b1 + (size_t)kb * 64);
-            const int *a = (const int *)(arow + kb * KPB + aoff);
-            acc0 = fg_dot<KIND>(s0, a, acc0, L);
-            if constexpr (PAIR) acc1 = fg_dot<KIND>(s1, a, acc1, L);
-        }
-    }
-    // the k-groups of a column are lanes l, l ^ 16, l ^ 32, l ^ 48 (H: l ^ 8, l ^ 16, ..., l ^ 56: blocks and
-    // k-groups); then the waves through LDS, in order
-    {
-        auto s32 = __builtin_amdgcn_permlane32_swap(acc0, acc0, false, false);
-        acc0 += (int)((lane & 32) == 0 ? s32[1] : s32[0]);
-        auto s16 = __builtin_amdgcn_permlane16_swap(acc0, acc0, false, false);
-        acc0 += (int)((lane & 16) == 0 ? s16[1] : s16[0]);
-        if constexpr (PAIR) {
-            auto t32 = __builtin_amdgcn_permlane32_swap(acc1, acc1, false, false);
-            acc1 += (int)((lane & 32) == 0 ? t32[1] : t32[0]);
-            auto t16 = __builtin_amdgcn_permlane16_swap(acc1, acc1, false, false);
-            acc1 += (int)((lane & 16) == 0 ? t16[1] : t16[0]);
-        }
-        if constexpr (H) {  // row_ror:8 -> lane l ^ 8 within its 16-lane row
-            acc0 += __builtin_amdgcn_update_dpp(0, acc0, 0x128, 0xF, 0xF, false);
-            if constexpr (PAIR) acc1 += __builtin_amdgcn_update_dpp(0, acc1, 0x128, 0xF, 0xF, false);
-        }
-    }
-    if (lane < (H ? 8 : 16)) {
-        racc[wv][0][lane] = acc0;
-        racc[wv][1][lane] = acc1;
-    }
-    __syncthreads();
-    if (threadIdx.x >= (H ? 8 : 16)) return;
-    const int j = threadIdx.x;
-    int c0 = 0, c1 = 0;
-#pragma unroll
-    for (int w = 0; w < FG_WAVES; w++) {
-        c0 += racc[w][0][j];
-        if constexpr (PAIR) c1 += racc[w][1][j];
-    }
-    if constexpr (KIND == 1) { // every block's partial is 16 x an integer
-        c0 >>= 4;
-        c1 >>= 4;
-    }
-    const int n = pnl * 16 + hh * 8 + j;
-    if constexpr (EPI == Q3_EPI_STORE) {
-        p.C[t][n] = c0;
-    } else if constexpr (EPI == Q3_EPI_RESID) {
-        p.x[n] = p.x[n] + ((float)c0 * as) * p.ws0[n];
-    } else {
-        const float gv = ((float)c0 * as) * p.ws0[n];
-        const float uv = ((float)c1 * as) * p.ws1[n];
-        p.y[n] = (gv / (1.0f + expf(-gv))) * uv;
-    }
-}
-
 // k_attn_combine: one workgroup per query head, thread d = dimension d: the log-sum-exp combine of the head's
 // chunks with attn_quant_body's operations in its order, so the row equals the one that kernel quantises.
 __global__ __launch_bounds__(Q3_MAX_HD) void k_attn_combine(q3_comb p) {
@@ -900,36 +532,11 @@ __global__ __launch_bounds__(Q3_MAX_HD) void k_attn_combine(q3_comb p) {
 
 inline int launch_ok() { return hipGetLastError() == hipSuccess ? 0 : -1; }
 
-// Fused M = 1 matmul (k_fgemv), the instantiations the decoder uses: PRO_NORM + STORE (q/k/v, int8), PRO_QUANT +
-// RESID (o, int8; down, int8 / uniform int4 / NF4), PRO_NORM + SWIGLU (gate/up pairs, int8 / uniform int4 / NF4).
-// E: row elements per thread, a bound of K / 512; PRE: the weight blocks per wave, a bound of its share (half
-// panels, q3_fg.half: the load instructions of two half blocks each that cover it).
-template <int PRO, int EPI, int KIND, int E>
-void fg_launch_pre(const q3_fg *p, int grid, int pre, hipStream_t s) {
-    const dim3 b(FG_WAVES * 64);
-    if (p->half) {
-        // load instructions (two half blocks each) covering the wave's share: every count the decoder's shapes take
-        const int ni = (pre + 1) / 2, g2 = 2 * grid;
-        if (ni <= 1) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 1, 1>), dim3(g2), b, 0, s, *p);
-        else if (ni <= 2) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 2, 1>), dim3(g2), b, 0, s, *p);
-        else if (ni <= 3) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 3, 1>), dim3(g2), b, 0, s, *p);
-        else if (ni <= 4) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 4, 1>), dim3(g2), b, 0, s, *p);
-        else if (ni <= 6) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 6, 1>), dim3(g2), b, 0, s, *p);
-        else hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 8, 1>), dim3(g2), b, 0, s, *p);
-        return;
-    }
-    if (pre <= 4) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 4, 0>), dim3(grid), b, 0, s, *p);
-    else if (pre <= 8) hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 8, 0>), dim3(grid), b, 0, s, *p);
-    else hipLaunchKernelGGL((k_fgemv<PRO, EPI, KIND, E, 16, 0>), dim3(grid), b, 0, s, *p);
-}
-template <int PRO, int EPI, int KIND> int fg_launch(const q3_fg *p, int grid, hipStream_t s) {
-    const int e = (p->K + FG_WAVES * 64 - 1) / (FG_WAVES * 64), pre = (p->KB + FG_WAVES - 1) / FG_WAVES;
-    if (e <= 4) fg_launch_pre<PRO, EPI, KIND, 4>(p, grid, pre, s);
-    else if (e <= 8) fg_launch_pre<PRO, EPI, KIND, 8>(p, grid, pre, s);
-    else if (e <= 12) fg_launch_pre<PRO, EPI, KIND, 12>(p, grid, pre, s);
-    else if (e <= 16) fg_launch_pre<PRO, EPI, KIND, 16>(p, grid, pre, s);
-    else return -2;
-    return 0;
+// A plain copy of n floats (the decoder's layer-input trace); a kernel rather than a copy command, so that it is
+// an ordinary node of a captured decode step.
+__global__ __launch_bounds__(256) void k_copy_f32(float *__restrict__ dst, const float *__restrict__ src, long long n) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = src[i];
 }
 
 } // namespace
@@ -956,6 +563,14 @@ int q3k_norm_quant(const q3_nq *p, void *stream) {
     if (p->emb) Q3_ROW_DISPATCH(k_norm_quant_emb, 512, p->H, dim3(p->M), 0, (hipStream_t)stream, *p);
     else if (p->acc) Q3_ROW_DISPATCH(k_norm_quant_acc, 512, p->H, dim3(p->M), 0, (hipStream_t)stream, *p);
     else Q3_ROW_DISPATCH(k_norm_quant_x, 512, p->H, dim3(p->M), 0, (hipStream_t)stream, *p);
+    return launch_ok();
+}
+
+int q3k_copy_f32(float *dst, const float *src, long long n, void *stream) {
+    if (n < 1 || !dst || !src) return -2;
+    const long long grid = (n + 255) / 256;
+    if (grid >= (1LL << 31)) return -2;
+    hipLaunchKernelGGL(k_copy_f32, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, dst, src, n);
     return launch_ok();
 }
 
@@ -1026,45 +641,6 @@ int q3k_argmax(const q3_amax *p, void *stream) {
     if (grid > 512) grid = 512;
     hipLaunchKernelGGL(k_argmax, dim3(grid), dim3(256), 0, (hipStream_t)stream, *p);
     return launch_ok();
-}
-
-int q3k_fgemv(const q3_fg *p, void *stream) {
-    const hipStream_t s_ = (hipStream_t)stream;
-    if (p->kind < 0 || p->kind > 2 || p->epi < Q3_EPI_STORE || p->epi > Q3_EPI_SWIGLU) return -2;
-    const int kpb = p->kind == 0 ? 64 : 128;
-    const int pro = p->nw ? Q3_PRO_NORM : Q3_PRO_QUANT;
-    const int nt = p->epi == Q3_EPI_SWIGLU ? 2 : p->epi == Q3_EPI_RESID ? 1 : p->nt;
-    if (p->K < 32 || p->KB < 1 || (long)p->KB * kpb < p->K || (long)p->KB * kpb > Q3_FG_KMAX || nt < 1 || nt > 3 ||
-        !p->row)
-        return -2;
-    int grid = 0;
-    for (int i = 0; i < nt; i++) {
-        if (!p->B[i] || p->nb[i] < 1) return -2;
-        grid += p->nb[i];
-    }
-    int rc = -2;
-    switch (p->epi) {
-    case Q3_EPI_STORE:
-        for (int i = 0; i < nt; i++)
-            if (!p->C[i]) return -2;
-        if (pro != Q3_PRO_NORM || p->kind != 0) return -2;
-        rc = fg_launch<Q3_PRO_NORM, Q3_EPI_STORE, 0>(p, grid, s_);
-        break;
-    case Q3_EPI_RESID:
-        if (pro != Q3_PRO_QUANT || !p->x || !p->ws0) return -2;
-        if (p->kind == 0) rc = fg_launch<Q3_PRO_QUANT, Q3_EPI_RESID, 0>(p, grid, s_);
-        else if (p->kind == 1) rc = fg_launch<Q3_PRO_QUANT, Q3_EPI_RESID, 1>(p, grid, s_);
-        else rc = fg_launch<Q3_PRO_QUANT, Q3_EPI_RESID, 2>(p, grid, s_);
-        break;
-    default:
-        if (pro != Q3_PRO_NORM || !p->y || !p->ws0 || !p->ws1 || p->nb[1] != p->nb[0]) return -2;
-        grid = p->nb[0];
-        if (p->kind == 0) rc = fg_launch<Q3_PRO_NORM, Q3_EPI_SWIGLU, 0>(p, grid, s_);
-        else if (p->kind == 1) rc = fg_launch<Q3_PRO_NORM, Q3_EPI_SWIGLU, 1>(p, grid, s_);
-        else rc = fg_launch<Q3_PRO_NORM, Q3_EPI_SWIGLU, 2>(p, grid, s_);
-        break;
-    }
-    return rc ? rc : launch_ok();
 }
 
 int q3k_attn_combine(const q3_comb *p, void *stream) {

@@ -64,6 +64,12 @@ int       q3_tokens(q3_model *m, int *out, int n);
 int       q3_positions(const q3_model *m);
 /* Dequantised logits of the last sampled row, f32[vocab]. */
 int       q3_last_logits(q3_model *m, float *out);
+/* Test aid: the residual rows entering each layer. With on = 1, every later prefill and decode step also copies x,
+ * the fp32 rows entering layer l (l = 0 .. layers - 1) and leaving the last layer (l = layers, before the final
+ * norm), into a device trace (kernels of the step, so captured decode graphs hold them too). q3_layer_rows reads
+ * `rows` rows of layer l from the last pass (a prefill's n rows, a decode step's one) into out f32[rows][hidden]. */
+int       q3_set_trace(q3_model *m, int on);
+int       q3_layer_rows(q3_model *m, int l, float *out, int rows);
 /* Resident weight bytes read per decode token (projections + LM head, scales included). */
 double    q3_weight_bytes(const q3_model *m);
 

@@ -66,6 +66,7 @@ API = {
     "ork_f16_mm_run": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "ork_i8_mm_run": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "ork_i8_mm_run_noalloc": (C.c_int, [_P, _P, C.c_int, _P, _P]),
+    "ork_i8_mm_run_row": (C.c_int, [_P, C.c_int, _P, _P]),
     "ork_i4_mm_run": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "ork_i8_mm_run_cpu": (None, [C.c_int, C.c_int, C.c_int, _P, _P, _P]),
     "ork_i8_mm_run_chain": (C.c_int, [_P, C.c_int, _P]),
@@ -102,9 +103,19 @@ class TaskI4(C.Structure):
 
 TaskF16 = TaskI4
 
+ROW_RMSNORM, ROW_QUANT = 0, 1                 # ork_row_op.prologue (include/ork/hip.h)
+COL_STORE, COL_RESID, COL_SWIGLU = 0, 1, 2    # ork_row_op.epilogue
+
+
+class RowOp(C.Structure):
+    """ork_row_op (include/ork/hip.h): device pointers as ints"""
+    _fields_ = [("prologue", C.c_int), ("row", _P), ("norm_w", _P), ("eps", C.c_float), ("row_scale", _P),
+                ("epilogue", C.c_int), ("C", _P * 3), ("w_scale", _P * 2), ("out", _P)]
+
 
 def tasks(cls, rows):
-    """A ctypes array of task structs from tuples (w, M, A, C[, cstride]); A and C are arrays or ints."""
+    """A ctypes array of task structs from tuples (w, M, A, C[, cstride]); A and C are arrays or ints. The structs
+    hold raw pointers only: the caller keeps the arrays alive until the run has returned."""
     arr = (cls * len(rows))()
     for i, r in enumerate(rows):
         arr[i].w = r[0]

@@ -47,6 +47,8 @@ API = {
     "q3_weight_bytes": (C.c_double, [_P]),
     "q3_set_fused": (C.c_int, [_P, C.c_int]),
     "q3_decode_fused": (C.c_int, [_P]),
+    "q3_set_trace": (C.c_int, [_P, C.c_int]),
+    "q3_layer_rows": (C.c_int, [_P, C.c_int, _P, C.c_int]),
 }
 
 _lib = None
@@ -145,6 +147,16 @@ class Model:
     def last_logits(self):
         out = np.empty(self.cfg.vocab, np.float32)
         assert lib().q3_last_logits(self.h, ork.ptr(out)) == 0
+        return out
+
+    def set_trace(self, on):
+        """Keep the residual rows entering each layer (and leaving the last) of every later pass."""
+        return lib().q3_set_trace(self.h, int(on))
+
+    def layer_rows(self, l, rows):
+        """f32[rows][hidden]: the rows entering layer l in the last pass (l = layers: leaving the last layer)."""
+        out = np.empty((rows, self.cfg.hidden), np.float32)
+        assert lib().q3_layer_rows(self.h, l, ork.ptr(out), rows) == 0
         return out
 
     def weight_bytes(self):

@@ -42,6 +42,12 @@ long long orkh_read_probe(const void *dev, size_t bytes, unsigned *sink, void *s
     return grid;
 }
 int orkh_device_sync(void) { return 0; }
+int orkh_stream_capturing(void *s) { (void)s; return 0; }
+int orkh_row_launch(const orkh_row *p, void *s) { (void)p; (void)s; return 0; }
+void *orkh_event_new(void) { return malloc(8); }
+void orkh_event_free(void *e) { free(e); }
+int orkh_event_record(void *e, void *s) { (void)s; memset(e, 0, 8); return 0; }
+float orkh_event_ms(void *e0, void *e1) { (void)e0; (void)e1; return 0.001f; }
 int orkh_ptr_is_device(const void *p) { for (int i = 0; i < ndev; i++) if ((const char *)p >= (char *)devp[i] && (const char *)p < (char *)devp[i] + (devn[i] ? devn[i] : 1)) return 1; return 0; }
 int orkh_mm_launch(const orkh_mm *p, const orkh_plan *q, void *s) { (void)p; (void)q; (void)s; return 0; }
 int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *q, int G, const float *aS, const float *bS, float *C, int ldc, void *s) { (void)ldc;

@@ -199,6 +199,32 @@ def test_f16_stream(npu):
         ork.free(w)
 
 
+def test_f16_stream_equals_single_runs(npu):
+    """An fp16 stream gives each task exactly its single run's result (include/ork/chain.h: results identical to S
+    single runs): fp32 sums in the same order, whether the task's own M = 1 plan is the half-panel GEMV (which the
+    grouped whole-panel launch would sum in another order, so such tasks launch with their own plans) or whole
+    panels (which group). Bit for bit, not to a tolerance."""
+    _say("f16 stream = single runs, bit for bit")
+    rng = np.random.default_rng(77)
+    shapes = [(1, 2048, 512), (1, 2048, 6144), (1, 2048, 4096), (1, 6144, 2048), (1, 96, 48), (1, 4096, 16),
+              (16, 1024, 256), (1, 2048, 2048)]
+    rows, singles, ws = [], [], []
+    for M, K, N in shapes:
+        A = rng.standard_normal((M, K)).astype(np.float16)
+        B = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+        w = npu.pack_f16(B)
+        rc, Cs = npu.run_f16(w, A)
+        assert rc == 0
+        rows.append((w, M, A, np.zeros((M, N), np.float32)))
+        singles.append((Cs, npu.plan_name(w, M)))
+        ws.append(w)
+    assert ork.lib().ork_f16_mm_run_stream(npu.h, len(rows), ork.tasks(ork.TaskF16, rows)) == 0
+    for (w, M, A, Cb), (Cs, name) in zip(rows, singles):
+        assert np.array_equal(Cb.view(np.uint32), Cs.view(np.uint32)), (A.shape, name)
+    for w in ws:
+        ork.free(w)
+
+
 def test_chain_errors(npu):
     _say("chain errors")
     L = ork.lib()

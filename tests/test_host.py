@@ -303,3 +303,37 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120, cwd=ROOT)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_ork_profile_rows_printed_at_free(capfd, monkeypatch):
+    """ORK_PROFILE (read when the context is made, src/npu/core/sched.c:53): ork_npu_free prints one
+    "[ork PROFILE]" row per entry point and plan with the call count and host time, as the reference prints its
+    run_i8 / run_i4 totals (src/npu/core/device.c:257-263). On an offline context the runs are the CPU's."""
+    rng = np.random.default_rng(13)
+    B = rng.integers(-128, 128, size=(128, 64), dtype=np.int8)
+    A = rng.integers(-128, 128, size=(3, 128), dtype=np.int8)
+    monkeypatch.setenv("ORK_PROFILE", "1")
+    c = ork.Npu(offline="gfx950")
+    monkeypatch.delenv("ORK_PROFILE")
+    w = c.pack_i8(B)
+    for _ in range(3):
+        rc, Cm = c.run_i8(w, A)
+        assert rc == 0 and np.array_equal(Cm, O.gemm_i32(A, B))
+    w4 = c.pack_i4(rng.integers(-8, 8, size=(128, 64), dtype=np.int8))
+    assert c.run_i4(w4, rng.integers(-8, 8, size=(2, 128), dtype=np.int8))[0] == 0
+    ork.free(w)
+    ork.free(w4)
+    capfd.readouterr()
+    c.close()
+    err = capfd.readouterr().err
+    rows = [l for l in err.splitlines() if l.startswith("[ork PROFILE]")]
+    assert any(l.startswith("[ork PROFILE] ork_i8_mm_run cpu: 3 calls,") for l in rows), err
+    assert any(l.startswith("[ork PROFILE] ork_i4_mm_run cpu: 1 calls,") for l in rows), err
+    # without the switch nothing is printed
+    c2 = ork.Npu(offline="gfx950")
+    w2 = c2.pack_i8(B)
+    assert c2.run_i8(w2, A)[0] == 0
+    ork.free(w2)
+    capfd.readouterr()
+    c2.close()
+    assert "[ork PROFILE]" not in capfd.readouterr().err

@@ -123,3 +123,83 @@ def test_noalloc_refusals(npu):
     L.ork_dev_free(npu.h, dA)
     L.ork_dev_free(npu.h, dC)
     ork.free(w)
+
+
+def test_noalloc_misaligned_a_refused(npu):
+    """A device A that is not 16-byte aligned is refused (-1) by the no-allocation entry point, which cannot stage
+    it; ork_i8_mm_run stages such an A and computes."""
+    L = ork.lib()
+    rng = np.random.default_rng(330)
+    K, N, M = 256, 64, 2
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    w = npu.pack_i8(B)
+    raw = np.zeros(A.nbytes + 16, np.int8)
+    raw[4:4 + A.nbytes] = A.reshape(-1)
+    dA = _dev(npu, raw)
+    dC = L.ork_dev_alloc(npu.h, M * N * 4)
+    assert L.ork_i8_mm_run_noalloc(npu.h, w, M, dA + 4, dC) == -1
+    assert L.ork_i8_mm_run(npu.h, w, M, dA + 4, dC) == 0
+    C = np.empty((M, N), np.int32)
+    assert L.ork_dev_download(npu.h, ork.ptr(C), dC, C.nbytes) == 0
+    assert np.array_equal(C, O.gemm_i32(A, B))
+    L.ork_dev_free(npu.h, dA)
+    L.ork_dev_free(npu.h, dC)
+    ork.free(w)
+
+
+def test_noalloc_under_graph_capture(npu):
+    """Under HIP graph capture: outside async mode the call is refused (-1) and enqueues nothing (the capture stays
+    valid); in async mode a forced split-K call is captured, and its graph, replayed twice with an eager call that
+    rewrites the scratch array in between, gives the oracle's C on every replay."""
+    import hipgraph
+
+    L = ork.lib()
+    G = hipgraph.Graphs()
+    stream = L.ork_npu_stream(npu.h)
+    rng = np.random.default_rng(340)
+    M, K, N = 16, 4096, 1024
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B2 = rng.integers(-128, 128, size=(2048, 512), dtype=np.int8)
+    A2 = rng.integers(-128, 128, size=(5, 2048), dtype=np.int8)
+    w, w2 = npu.pack_i8(B), npu.pack_i8(B2)
+    dA, dA2 = _dev(npu, A), _dev(npu, A2)
+    dC = L.ork_dev_alloc(npu.h, M * N * 4)
+    dC2 = L.ork_dev_alloc(npu.h, 5 * 512 * 4)
+    want = O.gemm_i32(A, B)
+    zero = np.zeros((M, N), np.int32)
+    try:
+        with _env(ORK_PLAN="stream", ORK_KSPLIT=4):
+            name = npu.plan_name(w, M)
+            assert "_ks4" in name, name
+            print("[case] noalloc under capture, sync mode (refused):", name, flush=True)
+            rc, g, ex = G.capture(stream, lambda: L.ork_i8_mm_run_noalloc(npu.h, w, M, dA, dC), instantiate=False)
+            assert rc == -1
+            G.destroy(g, ex)
+            print("[case] noalloc under capture, async mode:", name, flush=True)
+            L.ork_npu_set_async(npu.h, 1)
+            rc, g, ex = G.capture(stream, lambda: L.ork_i8_mm_run_noalloc(npu.h, w, M, dA, dC))
+            assert rc == 0
+        try:
+            for rep in range(2):
+                assert L.ork_dev_upload(npu.h, dC, ork.ptr(zero), zero.nbytes) == 0
+                G.replay(ex, stream)
+                C = np.empty((M, N), np.int32)
+                assert L.ork_dev_download(npu.h, ork.ptr(C), dC, C.nbytes) == 0
+                assert np.array_equal(C, want), rep
+                # eager work between replays: another split call through the same scratch array
+                with _env(ORK_PLAN="stream", ORK_KSPLIT=2):
+                    assert L.ork_i8_mm_run_noalloc(npu.h, w2, 5, dA2, dC2) == 0
+                assert L.ork_npu_sync(npu.h) == 0
+                C2 = np.empty((5, 512), np.int32)
+                assert L.ork_dev_download(npu.h, ork.ptr(C2), dC2, C2.nbytes) == 0
+                assert np.array_equal(C2, O.gemm_i32(A2, B2)), rep
+        finally:
+            G.destroy(g, ex)
+    finally:
+        L.ork_npu_set_async(npu.h, 0)
+        for d in (dA, dA2, dC, dC2):
+            L.ork_dev_free(npu.h, d)
+        ork.free(w)
+        ork.free(w2)
