@@ -457,3 +457,66 @@ def test_grouped_oracle_single_group_closed_form():
     C = O.gemm_grouped(A, B, aS, bS, 512)
     P = O.gemm_i32(A, B).astype(np.float32)
     assert np.array_equal(C, np.float32(0) + (P * aS) * bS)
+
+
+# ---- rowops_ref: the one-row run's row operations (ork_i8_mm_run_row) -------------------------------------------
+def test_rowops_quant_equals_the_division_quantiser():
+    """The restatement's per-row quantisation (y * (1/s), the exact quotient within 1e-4 of a half-way point) gives
+    exactly the codes and scale of the oracle's examples/quant.c:34-37 quantiser, which divides every element by s,
+    over rows with dozens of elements near half-way points, as well as exact ties and a zero row."""
+    import rowops_ref as R
+
+    rng = np.random.default_rng(41)
+    rows = [rng.standard_normal(2048).astype(np.float32) * np.float32(rng.uniform(0.01, 10)) for _ in range(96)]
+    rows.append(np.array([127.0, 63.5, -0.5, 1.5, -2.5, 0.0] * 8, np.float32))     # s = 1: exact ties, half-even
+    rows.append(np.zeros(64, np.float32))                                          # zero row: s = 1, codes 0
+    near = 0
+    for y in rows:
+        q, s = R.quant_row(y)
+        sref, qref = O.quant_test_acts(y[None, :])
+        assert s == sref[0] and np.array_equal(q, qref[0])
+        r = y * (np.float32(1) / s)
+        near += int(np.sum(np.abs(r - np.floor(r) - np.float32(0.5)) < np.float32(1e-4)))
+    assert near > 30   # the exact-quotient branch was exercised (72 elements at this seed)
+
+
+def test_rowops_rmsnorm_closed_forms_and_bound():
+    """RMSNorm in the documented summation order: exact where every partial sum is representable (dyadic rows), a
+    constant row normalises to 1 / sqrt(1 + eps / c^2) of itself, and random rows stay within K ulp-relative of the
+    float64 evaluation; a row that is not a multiple of 512 long pads with exact zeros."""
+    import rowops_ref as R
+
+    for K in (64, 512, 2048, 3000):
+        x = np.full(K, 0.5, np.float32)
+        assert R.sum_squares(x) == np.float32(0.25 * K)
+        x = (np.arange(K) % 8 - 4).astype(np.float32) / 4        # squares are multiples of 1/16: exact sums
+        assert R.sum_squares(x) == np.float32(np.sum(x.astype(np.float64) ** 2))
+        y = R.rmsnorm(np.full(K, 3.0, np.float32), np.ones(K, np.float32), 0.0)
+        assert np.all(y == np.float32(1.0))
+    rng = np.random.default_rng(43)
+    for K in (100, 2048, 6144, 8192):
+        x = rng.standard_normal(K).astype(np.float32)
+        ss, ss64 = R.sum_squares(x), np.sum(x.astype(np.float64) ** 2)
+        assert abs(float(ss) - ss64) <= K * 2.0 ** -24 * ss64
+        w = (1 + 0.02 * rng.standard_normal(K)).astype(np.float32)
+        y, y64 = R.rmsnorm(x, w, 1e-6), x.astype(np.float64) / np.sqrt(ss64 / K + 1e-6) * w
+        assert np.max(np.abs(y - y64)) <= 1e-5 * np.max(np.abs(y64))
+
+
+def test_rowops_epilogues_closed_forms():
+    """Residual add and SwiGLU: zero columns leave x as it is, unit scales add the integers exactly, silu(0) = 0 and
+    silu agrees with a float64 logistic to float32 precision."""
+    import rowops_ref as R
+    from scipy.special import expit
+
+    rng = np.random.default_rng(47)
+    x = rng.standard_normal(256).astype(np.float32)
+    c = rng.integers(-1000, 1000, 256).astype(np.int32)
+    assert np.array_equal(R.resid(x, np.zeros(256, np.int32), 0.37, np.ones(256, np.float32)), x)
+    assert np.array_equal(R.resid(np.zeros(256, np.float32), c, 1.0, np.ones(256, np.float32)), c.astype(np.float32))
+    assert np.all(R.swiglu(np.zeros(4, np.int32), c[:4], 0.5, np.ones(4, np.float32), np.ones(4, np.float32)) == 0)
+    cg, cu = rng.integers(-5000, 5000, 256).astype(np.int32), rng.integers(-5000, 5000, 256).astype(np.int32)
+    wg, wu = rng.uniform(1e-4, 1e-3, 256).astype(np.float32), rng.uniform(1e-4, 1e-3, 256).astype(np.float32)
+    y = R.swiglu(cg, cu, 0.9, wg, wu)
+    g, u = cg * 0.9 * wg.astype(np.float64), cu * 0.9 * wu.astype(np.float64)
+    assert np.max(np.abs(y - g * expit(g) * u)) <= 1e-6 * np.max(np.abs(g * expit(g) * u))
