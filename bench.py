@@ -783,7 +783,7 @@ def main():
         if args.only not in ("m512",):
             g1, e1 = measure(npu, hip, ws, 1, dA, dC, args.steps, args.warmup, outer=o1)
             print(f"[bench] M=1: graph {g1 * 1e3:.2f} us/step, eager {e1 * 1e3:.2f} us/step", file=sys.stderr, flush=True)
-        if args.only in (None, "gemv"):
+        if args.only in (None, "gemv", "m512"):
             # the same graph harness around a launch that moves almost nothing (K=32, N=32) and around the one-thread
             # wall-clock kernel alone: what one launch costs on this box before any data (in a traced run, the
             # tracer's own cost per dispatch beside the GEMV's)
