@@ -233,15 +233,16 @@ def test_grouped_guards(gnpu, M, K, N, G, env, want):
         L.ork_mm_free(gnpu.h, w)
 
 
-def test_chain_cstride_guards(gnpu):
+@pytest.mark.parametrize("ld", [1024 + 96, 1024 + 97])
+def test_chain_cstride_guards(gnpu, ld):
     """Three int8 tasks writing into one device C at row stride `ld` (the reference's cstride): a grouped one-row
     launch, a grouped LDS-ring launch of two M = 64 tasks sharing K, and a split-K task launched on its own (its
-    partials between the workspace's guard bands). Every
+    partials between the workspace's guard bands); a row stride that keeps every row 16-byte aligned and one that
+    does not (the tile epilogue's vector and scalar stores). Every
     byte of the buffer outside each task's M x N block (the guards, the gaps at the end of each row, the columns of
     the other tasks) keeps the pattern."""
     L = ork.lib()
     rng = np.random.default_rng(960)
-    ld = 1024 + 96
     specs = [(1, 2048, 512, 0), (64, 2048, 384, 512), (64, 2048, 160, 512 + 384), (40, 4096, 64, 0)]
     rows = sum(m for m, _, _, _ in specs)
     g = Guarded(gnpu, rows * ld * 4)
