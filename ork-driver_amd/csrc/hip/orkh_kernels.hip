@@ -675,7 +675,10 @@ template <int KIND, int BM, int BN, int KS, int XG = 0> struct T2 {
     static constexpr int SLOT = (NI + JUNK) * 1024;
     // NF4: a stage's B blocks are decoded once, into int8 MFMA operands in LDS, instead of by each of the
     // WM waves that read a block (the codebook decode is ~8x the VALU work of the uniform-int4 one)
-    static constexpr int DEC = KIND == ORKH_NF4 ? NIB * T::STEPS * 1024 : 0;
+    // Two stages of them where a ring of 3 slots still fits (the decode then runs a stage ahead: tiled2_body)
+    static constexpr int DEC1 = KIND == ORKH_NF4 ? NIB * T::STEPS * 1024 : 0;
+    static constexpr bool DEC2 = KIND == ORKH_NF4 && (163840 - 2 * DEC1) / SLOT >= 3;
+    static constexpr int DEC = DEC2 ? 2 * DEC1 : DEC1;
     // ring within 160 KiB: 4 slots, 8 for the small stages of the K-group tiles (more bytes in flight per CU);
     // 8 slots for the 12-16 KiB stages of the other tiles measured slower (int8 M=128 64 x 64 8.5 -> 9.4 us,
     // fp16 M=512 13.0 -> 14.0, grouped W4A4 M=256 21.9 -> 22.7)
@@ -891,28 +894,91 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         }
     }
 
+    // NF4 (plain runs): a stage's B blocks are decoded once, into int8 MFMA operands in LDS, one stage ahead of
+    // their MFMAs -- iteration s decodes stage s + 1 into one half of Dec while its MFMAs read stage s from the
+    // other, so the codebook decode (VALU) overlaps the matrix work and the stage keeps a single barrier.
+    // Measured against decoding each stage before its MFMAs behind a second barrier (us, K=2048 N=6144 unless
+    // given): 32 x 64 M=64 9.19 -> 8.63, K=6144 N=2048 17.96 -> 15.65; 64 x 64 M=256 15.77 -> 14.49, M=512
+    // K=6144 N=2048 27.50 -> 23.82; 128 x 128 M=512 18.84 -> 17.60, M=1024 34.83 -> 29.58.
+    // Who decodes, and when (measured, same shapes): on the K-group tiles (32 x 64: 8 blocks a stage) every wave
+    // takes an equal share of dwords and decodes before its MFMAs (8.74 -> 8.63, 16.04 -> 15.65 against a block
+    // per wave after them); on the others a block per wave decodes after the wave's MFMAs (64 x 64 M=256 15.54
+    // -> 14.49, 128 x 128 M=1024 32.96 -> 29.58 against equal shares before them). Equal shares with half the
+    // waves of each SIMD decoding first and half after measured slower than both.
+    constexpr bool PIPE = P::DEC2 && GR == 0;
+    constexpr bool EARLY = PIPE && P::WK > 1;
+    static_assert(!PIPE || R >= 3, "NF4 ring: the decode runs a stage ahead");
+    v4i *const Dec = sm + P::R * (P::SLOT / 16); // [stage parity][block][step]
+    auto decode_stage = [&](int st) {
+        const v4i *Bs = sm + (st % R) * (P::SLOT / 16) + P::NIA * 64;
+        v4i *D = Dec + (st & 1) * (P::NIB * T::STEPS * 64);
+        // every wave an equal share where the stage's NIB x 4 dword columns divide evenly (dword j of each lane's
+        // 16 bytes of block b is column 4 b + j): DPW of them, at wave-uniform offsets; dword j's low and high
+        // nibbles go where decode() puts them, operand j / 2, dwords 2 (j % 2) and 2 (j % 2) + 1
+        constexpr int DPW = P::NIB * 4 % P::NW ? 0 : P::NIB * 4 / P::NW;
+        if constexpr (EARLY && (DPW == 1 || DPW == 2 || DPW == 4)) {
+            const int c0 = wv * DPW, b = c0 >> 2, j0 = c0 & 3;
+            const uint32_t *src = (const uint32_t *)(Bs + b * 64 + lane) + j0;
+            uint32_t x[DPW], lo[DPW], hi[DPW];
+            if constexpr (DPW == 4) {
+                const v4i r = *(const v4i *)src;
+                x[0] = r.x, x[1] = r.y, x[2] = r.z, x[3] = r.w;
+            } else if constexpr (DPW == 2) {
+                const uint2 r = *(const uint2 *)src;
+                x[0] = r.x, x[1] = r.y;
+            } else {
+                x[0] = *src;
+            }
+#pragma unroll
+            for (int u = 0; u < DPW; u++) nf4_map8(x[u], L, lo[u], hi[u]);
+            uint32_t *dst = (uint32_t *)(D + (b * T::STEPS + (j0 >> 1)) * 64 + lane) + (j0 & 1) * 2;
+            if constexpr (DPW == 4) {
+                *(v4i *)dst = v4i{(int)lo[0], (int)hi[0], (int)lo[1], (int)hi[1]};
+                *(v4i *)(dst + 256) = v4i{(int)lo[2], (int)hi[2], (int)lo[3], (int)hi[3]};
+            } else if constexpr (DPW == 2) {
+                *(v4i *)dst = v4i{(int)lo[0], (int)hi[0], (int)lo[1], (int)hi[1]};
+            } else {
+                *(uint2 *)dst = make_uint2(lo[0], hi[0]);
+            }
+        } else {
+            for (int b = wv; b < P::NIB; b += P::NW) {
+                v4i op[T::STEPS];
+                decode<KIND>(Bs[b * 64 + lane], op, L);
+#pragma unroll
+                for (int u = 0; u < T::STEPS; u++) D[(b * T::STEPS + u) * 64 + lane] = op[u];
+            }
+        }
+    };
+
 #pragma unroll
     for (int st = 0; st < R - 1; st++) issue(st);
+    if constexpr (PIPE) {
+        if (nst > 0) {
+            wait_vmcnt<(R - 2) * P::IPW>(); // stage 0 (every wave's share: the barrier below)
+            __syncthreads();
+            decode_stage(0);
+        }
+    }
     for (int s = 0; s < nst; s++) {
-        wait_vmcnt<(R - 2) * P::IPW>();
+        // stage s has landed (NF4: stage s + 1, whose blocks this iteration decodes); the barrier also publishes
+        // the decode of stage s
+        wait_vmcnt<(PIPE ? R - 3 : R - 2) * P::IPW>();
         __syncthreads();
-        issue(s + R - 1); // into the slot of stage s - 1, which every wave finished before the barrier
+        // into the slot of stage s - 1, which every wave finished before the barrier (NF4: its blocks were decoded
+        // in iteration s - 2)
+        issue(s + R - 1);
         const v4i *As = sm + (s % R) * (P::SLOT / 16);
         const v4i *Bs = As + P::NIA * 64;
         if constexpr (GR) {
             if (s == 0) load_sc(0); // the scales landed with stage 0 (older loads, same wait)
         }
-        const v4i *Dec = sm + P::R * (P::SLOT / 16); // NF4: the stage's decoded B blocks, [block][step]
-        if constexpr (KIND == ORKH_NF4) {
-            // block b of the stage by wave b % NW, each lane its 16 bytes; one barrier publishes them. The
-            // previous stage's readers all passed the barrier above, so the buffer is free.
-            for (int b = wv; b < P::NIB; b += P::NW) {
-                v4i op[T::STEPS];
-                decode<KIND>(Bs[b * 64 + lane], op, L);
-#pragma unroll
-                for (int st = 0; st < T::STEPS; st++) ((v4i *)Dec)[(b * T::STEPS + st) * 64 + lane] = op[st];
-            }
+        const v4i *Ds = Dec + (s & 1) * (P::NIB * T::STEPS * 64);
+        if constexpr (KIND == ORKH_NF4 && !PIPE) {
+            decode_stage(s);
             __syncthreads();
+        }
+        if constexpr (EARLY) {
+            if (s + 1 < nst) decode_stage(s + 1);
         }
         if constexpr (GR != 1) {
 #pragma unroll
@@ -924,7 +990,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                     const int b = (wn * P::NTW + jn) * KS + kbl;
                     if constexpr (KIND == ORKH_NF4) {
 #pragma unroll
-                        for (int st = 0; st < T::STEPS; st++) op[jn][st] = Dec[(b * T::STEPS + st) * 64 + lane];
+                        for (int st = 0; st < T::STEPS; st++) op[jn][st] = Ds[(b * T::STEPS + st) * 64 + lane];
                     } else {
                         decode<KIND>(Bs[b * 64 + lane], op[jn], L);
                     }
@@ -938,6 +1004,9 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                         for (int jn = 0; jn < P::NTW; jn++) acc[i][jn] = mma(a, op[jn][st], acc[i][jn]);
                     }
             }
+        }
+        if constexpr (PIPE && !EARLY) {
+            if (s + 1 < nst) decode_stage(s + 1);
         }
         if constexpr (GR == 2) {
             // groups of whole stages: the stage ran as in the plain kernel; close the group it ends
