@@ -908,10 +908,11 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     constexpr bool PIPE = P::DEC2 && GR == 0;
     constexpr bool EARLY = PIPE && P::WK > 1;
     static_assert(!PIPE || R >= 3, "NF4 ring: the decode runs a stage ahead");
-    v4i *const Dec = sm + P::R * (P::SLOT / 16); // [stage parity][block][step]
+    v4i *const Dec = sm + P::R * (P::SLOT / 16); // [stage parity, if PIPE][block][step]
+    static_assert(P::DEC >= (PIPE ? 2 : 1) * P::DEC1, "NF4 decode buffers");
     auto decode_stage = [&](int st) {
         const v4i *Bs = sm + (st % R) * (P::SLOT / 16) + P::NIA * 64;
-        v4i *D = Dec + (st & 1) * (P::NIB * T::STEPS * 64);
+        v4i *D = Dec + (PIPE ? (st & 1) : 0) * (P::NIB * T::STEPS * 64); // one buffer unless pipelined
         // every wave an equal share where the stage's NIB x 4 dword columns divide evenly (dword j of each lane's
         // 16 bytes of block b is column 4 b + j): DPW of them, at wave-uniform offsets; dword j's low and high
         // nibbles go where decode() puts them, operand j / 2, dwords 2 (j % 2) and 2 (j % 2) + 1
@@ -972,7 +973,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         if constexpr (GR) {
             if (s == 0) load_sc(0); // the scales landed with stage 0 (older loads, same wait)
         }
-        const v4i *Ds = Dec + (s & 1) * (P::NIB * T::STEPS * 64);
+        const v4i *Ds = Dec + (PIPE ? (s & 1) : 0) * (P::NIB * T::STEPS * 64);
         if constexpr (KIND == ORKH_NF4 && !PIPE) {
             decode_stage(s);
             __syncthreads();
