@@ -10,13 +10,14 @@
  *            the CUs), waves split K in runs of ~8 KiB; K is split across workgroups only for long-K,
  *            few-panel shapes that leave the machine underfilled.
  *   M <= 64  the streaming kernel (same grid, runs of 1-4 KiB) or the LDS-ring tiled kernel, whichever a
- *            delivery model of both prices lower, each with its best K split (NF4: streaming, by the
- *            occupancy rule of the GEMV).
- *   M >  64  the LDS-ring tiled kernel (k_tiled for NF4 up to 128 rows): the tile and K split with the least
- *            modelled time.
+ *            delivery model of both prices lower, each with its best K split.
+ *   M >  64  the LDS-ring tiled kernel: the tile and K split with the least modelled time.
+ *   NF4      (M > 1) the streaming kernel, k_tiled and the LDS-ring kernel, every tile and split, each priced by
+ *            its own fit (nf4_best).
  * Both time models charge a workgroup for a fixed set-up, the operand bytes that must reach its CU and
  * its multiply-accumulates; a K split adds its partials' round trip and the reduce launch.
- * ORK_PLAN=stream|tiled, ORK_TILE=BMxBN and ORK_KSPLIT=n force a kernel, tile or split (tests, A/B); they and
+ * ORK_PLAN=stream|tiled, ORK_TILE=BMxBN (with ORK_PLAN=tiled: a k_tiled tile) and ORK_KSPLIT=n force a kernel,
+ * tile or split (tests, A/B); they and
  * the other overrides below are read only on a context made with ORK_PLAN_DEBUG set (knob()), so a stray
  * variable cannot change the kernels of a production context. */
 #include <stdio.h>
@@ -152,6 +153,72 @@ static double stream_us(const ork_npu *c, int rkind, int M, int N, int KB, int c
     return t;
 }
 
+/* NF4 above one row. Its codebook decode shifts each kernel's balance of operand delivery and VALU work differently
+ * per tile, so every candidate has its own least-squares fit (relative error) to graph-timed launches on MI355X:
+ * 45 shapes (K x N = 2048 x 6144, 6144 x 2048, 4096 x 4096, 2048 x 2048, 2048 x 12288; M = 32..1024), 896
+ * kernel / tile / split candidates in all (tests/golden/nf4_plan_sweep.json),
+ *   t = a + rounds * (b + c * KiB) + [ks > 1] (d + e * ks * M * N * 4 / 1e6)   us,
+ * KiB being the A and B bytes one workgroup loads (the streaming kernel: the form of stream_us). The fits are
+ * within 3-7% rms per candidate; over the 45 shapes the picks total 639 us against 633 for the fastest timed
+ * candidate of each (the row-count rules they replace: 687 -- e.g. K=6144 N=2048 M=64 15.6 -> 10.9 us, K=2048
+ * N=12288 M=64 14.9 -> 10.2, K=N=2048 M=192 9.8 -> 8.0). */
+static const struct nf4_fit {
+    int algo, bm, bn, ksmax;
+    double a, b, c, d, e;
+} nf4_fits[] = {
+    {ORKH_ALGO_TILED2, 128, 128, 4, 4.3789, 0.0, 0.0301, 2.3617, 0.4960},
+    {ORKH_ALGO_TILED2, 64, 64, 4, 4.6225, 0.0, 0.0289, 1.8197, 0.5224},
+    {ORKH_ALGO_TILED2, 32, 64, 4, 1.4873, 2.5357, 0.0320, 2.6686, 0.2686},
+    {ORKH_ALGO_TILED, 128, 128, 8, 5.3888, 3.6819, 0.0342, 2.9385, 0.4929},
+    {ORKH_ALGO_TILED, 128, 96, 8, 3.8799, 3.9957, 0.0294, 2.9103, 0.4592},
+    {ORKH_ALGO_TILED, 64, 64, 8, 3.5871, 1.4189, 0.0256, 2.7677, 0.4113},
+};
+
+static void nf4_best(const ork_npu *c, int M, int N, int KB, int cu, orkh_plan *q) {
+    const int NB = N / 16;
+    const double part = (double)M * N * 4 / 1e6; /* MB of one K slice's partials */
+    double best = -1;
+    for (int ks = 1; ks <= 8; ks *= 2) {
+        const int kbs = cdiv(KB, ks);
+        if (cdiv(KB, kbs) != ks || (ks > 1 && kbs < 2)) continue;
+        if (M <= 64 && ks <= 4) { /* the streaming kernel holds up to 64 rows */
+            orkh_plan g;
+            memset(&g, 0, sizeof g);
+            stream_geom(c, ORKH_NF4, M, KB, NB, cu, ks, &g);
+            const int pp = g.np == 2 ? 2 : 1;
+            const long wgs = g.np == 2 ? g.npg : (long)NB * g.ksplit;
+            const double per = (double)((wgs + cu - 1) / cu);
+            const double kib = ((double)M * 128 * g.kbs + pp * (1024.0 * g.kbs + 64.0 * M)) / 1024;
+            const double mmac = (double)pp * g.mt * 16 * 16 * g.kbs * 128 / 1e6;
+            double t = 2.0935 + per * (0.0245 * kib + 0.2674 * mmac);
+            if (ks > 1) t += 2.0600 + 0.6076 * ks * part;
+            if (best < 0 || t < best - 1e-9) {
+                best = t;
+                *q = g;
+                q->algo = ORKH_ALGO_STREAM;
+            }
+        }
+        for (size_t i = 0; i < sizeof nf4_fits / sizeof nf4_fits[0]; i++) {
+            const struct nf4_fit *f = &nf4_fits[i];
+            if (ks > f->ksmax) continue;
+            const long wgs = (long)cdiv(M, f->bm) * cdiv(NB, f->bn / 16) * ks;
+            const double rounds = (double)((wgs + cu - 1) / cu);
+            const double kib = ((double)f->bm * 128 + (double)f->bn * 64) * kbs / 1024;
+            double t = f->a + rounds * (f->b + f->c * kib);
+            if (ks > 1) t += f->d + f->e * ks * part;
+            if (best < 0 || t < best - 1e-9) {
+                best = t;
+                memset(q, 0, sizeof *q);
+                q->algo = f->algo;
+                q->bm = f->bm;
+                q->bn = f->bn;
+                q->ksplit = ks;
+                q->kbs = kbs;
+            }
+        }
+    }
+}
+
 /* The LDS-ring kernel (k_tiled2): every tile and split on offer priced by the model above; A counts the
  * whole tile height, since rows past M still issue (zero-filled) loads. Returns the modelled time of
  * the best and fills q with it. */
@@ -241,11 +308,11 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
     if (ks_force > KB) ks_force = KB;
     if (ks_force > 0) ks_force = cdiv(KB, cdiv(KB, ks_force)); /* as a split can realise it */
 
-    const char *tf = knob(c, "ORK_TILE"); /* "BMxBN": that tile of the LDS-ring kernel, at any M */
+    const char *tf = knob(c, "ORK_TILE"); /* "BMxBN": that tile of the LDS-ring kernel (of k_tiled with ORK_PLAN=tiled) */
     int fbm, fbn;
     if (tf && sscanf(tf, "%dx%d", &fbm, &fbn) == 2) {
         const int ks = ks_force > 0 ? ks_force : 1;
-        q->algo = ORKH_ALGO_TILED2;
+        q->algo = f_tiled ? ORKH_ALGO_TILED : ORKH_ALGO_TILED2;
         q->bm = fbm;
         q->bn = fbn;
         q->kbs = cdiv(KB, ks);
@@ -254,18 +321,13 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
         return 0;
     }
 
+    if (rkind == ORKH_NF4 && M > 1 && !f_stream && !f_tiled && ks_force <= 0) {
+        nf4_best(c, M, N, KB, cu, q);
+        if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
+        return 0;
+    }
+
     if (M <= 64 && !f_tiled) {
-        /* NF4 at 49-64 rows: the 32 x 64 K-group tile (its stage's blocks decoded once into LDS) beats streaming,
-         * whose four row tiles re-read A per panel, when its tiles fill one round: 9.7 vs 10.5 us at M=64, but
-         * 9.4 vs 8.4 at M=48 (K=2048 N=6144) */
-        if (rkind == ORKH_NF4 && M > 48 && !f_stream && ks_force <= 0 && 2L * cdiv(NB, 4) <= cu) {
-            q->algo = ORKH_ALGO_TILED2;
-            q->bm = 32;
-            q->bn = 64;
-            q->ksplit = 1;
-            q->kbs = KB;
-            return 0;
-        }
         int ks;
         if (M == 1 || f_stream || ks_force > 0 || rkind == ORKH_NF4) {
             ks = ks_force > 0 ? ks_force : stream_rule_ks(c, rkind, M, KB, NB, cu);
@@ -294,9 +356,7 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
         return 0;
     }
 
-    /* NF4 takes the LDS-ring kernel above 128 rows (its stage decode into LDS beats k_tiled there: 16.4 vs
-     * 19.6 us at M=192, 16.7 vs 20.7 us at M=256, 21.5 vs 22.6 us at M=512, K=2048 N=6144) and k_tiled up to
-     * 128 rows, where k_tiled's 64 x 64 tiles still fit one round on the CUs (11.3 vs 11.9 us at M=128) */
+    /* (NF4 reaches here only with ORK_KSPLIT forced: k_tiled up to 128 rows, the LDS-ring kernel above) */
     if ((rkind != ORKH_NF4 || M > 128) && !f_tiled) {
         /* uniform int4 skips the 256 x 256 tile: with the nibble decode its registers spill (20 B per lane) */
         tiled2_best(rkind, M, N, KB, cu, ks_force, rkind == ORKH_I4U, q);

@@ -144,9 +144,11 @@ CASES = [
     ("f16", 70, 1024, 80, {"ORK_TILE": "32x32", "ORK_KSPLIT": 2}, "tiled2_f16_32x32_ks2"),
     ("i4u", 100, 2048, 160, {"ORK_TILE": "64x192"}, "tiled2_i4u_64x192"),
     ("w4a4", 100, 1024, 192, {"ORK_TILE": "64x64"}, "tiled2_i4u_64x64"),
-    ("nf4", 150, 1024, 96, {}, "tiled2_nf4"),
-    ("nf4", 60, 2048, 96, {}, "tiled2_nf4_32x64"),
-    ("nf4", 100, 1024, 96, {}, "tiled_nf4"),
+    ("nf4", 150, 1024, 96, {"ORK_TILE": "64x64"}, "tiled2_nf4_64x64"),
+    ("nf4", 60, 2048, 96, {"ORK_TILE": "32x64"}, "tiled2_nf4_32x64"),
+    ("nf4", 60, 2048, 96, {}, "_nf4_"),
+    ("nf4", 100, 1024, 96, {"ORK_PLAN": "tiled"}, "tiled_nf4"),
+    ("nf4", 100, 1024, 96, {"ORK_PLAN": "tiled", "ORK_TILE": "128x96"}, "tiled_nf4_128x96"),
     ("i8", 100, 1024, 96, {"ORK_PLAN": "tiled"}, "tiled_i8"),
 ]
 

@@ -1,0 +1,59 @@
+"""The planner's NF4 picks against measurements, on the CPU.
+
+tests/planner/plan_names.c prints the planner's choice (plan.c alone, a 256-CU device) for each shape of
+tests/golden/nf4_plan_sweep.json, which holds graph-timed MI355X launches of every NF4 kernel, tile and K split on
+offer at 45 shapes (tests/golden/nf4_plan_sweep.py made it). Each pick must be a timed candidate, within 15% of the
+fastest at its shape, and the picks must total within 2% of the fastest candidates' total. The planner's fits
+were made on these launches, so this pins the fits as implemented in C against the data, not their accuracy on
+other shapes.
+"""
+import json
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLANG = "/opt/rocm/llvm/bin/clang"   # _Float16 in the public header needs clang on x86
+
+
+@pytest.fixture(scope="module")
+def planner(tmp_path_factory):
+    if not os.path.exists(CLANG):
+        pytest.skip("ROCm clang not installed")
+    exe = str(tmp_path_factory.mktemp("planner") / "plan_names")
+    hs = os.path.join(ROOT, "ork-driver_amd", "csrc", "host")
+    r = subprocess.run([CLANG, "-O1", "-std=gnu11", "-Wall", "-Werror", "-ffp-contract=off",
+                        "-I" + os.path.join(ROOT, "include"), "-I" + hs,
+                        "-I" + os.path.join(ROOT, "ork-driver_amd", "csrc", "hip"),
+                        os.path.join(ROOT, "tests", "planner", "plan_names.c"), os.path.join(hs, "plan.c"),
+                        "-o", exe, "-lm"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-3000:]
+
+    def pick(cases):
+        args = [str(x) for c in cases for x in c]
+        out = subprocess.run([exe] + args, capture_output=True, text=True, timeout=60, env={}).stdout.split("\n")
+        return [ln.split()[4] for ln in out if ln.strip()]
+    return pick
+
+
+def test_nf4_picks_against_the_sweep(planner):
+    data = json.load(open(os.path.join(ROOT, "tests", "golden", "nf4_plan_sweep.json")))
+    shapes = data["shapes"]
+    assert len(shapes) == 45
+    picks = planner([(2, s["M"], s["K"], s["N"]) for s in shapes])
+    tot_pick = tot_best = 0.0
+    for s, p in zip(shapes, picks):
+        best = min(s["us"].values())
+        assert p in s["us"], (s["K"], s["N"], s["M"], p)
+        assert s["us"][p] <= 1.15 * best, (s["K"], s["N"], s["M"], p, s["us"][p], best)
+        tot_pick += s["us"][p]
+        tot_best += best
+    assert tot_pick <= 1.02 * tot_best, (tot_pick, tot_best)
+
+
+def test_fixed_picks(planner):
+    """The benchmark's two halves and the NF4 decode row keep their kernels: the half-panel GEMV at M=1, the
+    64 x 192 LDS-ring tile with line-loaded A at M=512 (int8 K=2048 N=6144), the GEMV for NF4 at M=1."""
+    got = planner([(0, 1, 2048, 6144), (0, 512, 2048, 6144), (2, 1, 2048, 6144)])
+    assert got[0].startswith("gemvh_i8_") and got[1] == "tiled2_i8_64x192_al" and got[2].startswith("gemvh_nf4_"), got
