@@ -1062,6 +1062,52 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     }
     wait_vmcnt<0>();
 
+    // The 2 x 2 x 4 uniform-int4 tile (t2_xg 2): all four K groups park their partial tiles in the ring and all 16
+    // waves sum them, in group order, and store C, 16 bytes a thread. Measured against group 0 alone summing and
+    // storing (below): W4A4 M=256 K=N=4096 12.93 -> 12.62 us; slower on the other K-group tiles (int8 M=128 32 x 32
+    // 6.35 -> 6.57, W4A8 M=64 32 x 64 7.16 -> 7.20) and on the tiles without K groups (int8 M=512 64 x 192 13.88
+    // -> 14.51), so only here.
+    if constexpr (GR == 0 && t2_xg<KIND, BM, BN, GR>() == 2) {
+        constexpr int SPAD = BN + 4; // words per parked row: a row's 16-lane store groups start in different banks
+        static_assert((size_t)P::WK * BM * SPAD * sizeof(c_t) <= (size_t)R * P::SLOT, "partial tiles fit the ring");
+        c_t *Ts = (c_t *)sm;
+        __syncthreads(); // every wave's loads have landed (vmcnt 0) and its reads of the ring are done
+#pragma unroll
+        for (int i = 0; i < P::MTW; i++)
+#pragma unroll
+            for (int jn = 0; jn < P::NTW; jn++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    Ts[(wk * BM + (wm * P::MTW + i) * 16 + (lane >> 4) * 4 + r) * SPAD + (wn * P::NTW + jn) * 16 +
+                       (lane & 15)] = acc[i][jn][r];
+        __syncthreads();
+        const bool split = nT > ntiles_all;
+        const size_t ldc = split ? (size_t)p.N : (size_t)p.ldc;
+        c_t *Cb = split ? (c_t *)ws + (size_t)ks * p.M * p.N : (c_t *)p.C;
+        const bool vec = ldc % 4 == 0 && ((uintptr_t)Cb & 15) == 0;
+        constexpr int CPR = BN / 4; // 16-byte chunks per tile row
+        for (int e = (int)threadIdx.x; e < BM * CPR; e += P::NW * 64) {
+            const int row = e / CPR, c4 = (e % CPR) * 4;
+            const int m = m0 + row, n = nb0 * 16 + c4; // N % 16 == 0: a chunk lies wholly inside or outside N
+            if (m >= p.M || n >= p.N) continue;
+            c_t v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = Ts[row * SPAD + c4 + u];
+#pragma unroll
+            for (int g = 1; g < P::WK; g++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] += Ts[(g * BM + row) * SPAD + c4 + u];
+            c_t *dst = Cb + (size_t)m * ldc + n;
+            if (vec) {
+                *(v4i *)dst = v4i{finish<KIND>(v[0]), finish<KIND>(v[1]), finish<KIND>(v[2]), finish<KIND>(v[3])};
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; u++) dst[u] = finish<KIND>(v[u]);
+            }
+        }
+        return;
+    }
+
     if constexpr (P::WK > 1) {
         // K groups 1.. park their partial tiles in the ring (every load has landed: vmcnt 0 on every wave, then
         // the barrier), group 0 adds them in group order and stores
