@@ -123,7 +123,8 @@ typedef struct orkh_plan {
     int aline;
     /* STREAM: np = 2 pairs panels: npg workgroups, the first N/16 - npg owning two adjacent panels each */
     int np, npg;
-    /* GEMV: 1 = half a panel (8 columns) per workgroup, grid (N/8, ksplit) (k_gemv_half), else one panel */
+    /* GEMV and STREAM: 1 = half a panel (8 columns) per workgroup, grid (N/8, ksplit) (k_gemv_half, k_stream's
+     * half mode), else one panel (or two: np) */
     int half;
     void *ws;             /* split-K partials, >= ksplit*M*N*4 bytes (device) */
 } orkh_plan;

@@ -135,8 +135,12 @@ __device__ __forceinline__ v4i bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // NP = 2 (paired panels): grid (G, 1) with N/16 / 2 <= G < N/16; the first N/16 - G workgroups own two
 // adjacent panels each and the rest one, so every CU holds about the same bytes; a wave loads each A chunk
 // once for both of its panels.
-template <int KIND, int MT, int WPG, int KU, int NP = 1>
+// HF = 1 (half panels): grid (N/8, ksplit); workgroup x owns columns 8 (x % 2) .. 8 (x % 2) + 7 of panel x / 2:
+// only the lanes holding those columns load B (half of every block's lines), and only they store. The MFMA still
+// runs on 16 columns; the other 8 (their B lanes left zero, or NF4's code 0) are discarded.
+template <int KIND, int MT, int WPG, int KU, int NP = 1, int HF = 0>
 __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs, int ksplit, void *ws) {
+    static_assert(!(HF && NP == 2), "half panels are single panels");
     using T = KT<KIND>;
     typedef typename T::acc_t acc_t;
     typedef typename T::c_t c_t;
@@ -145,8 +149,11 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ks = blockIdx.y, NBtot = p.N / 16;
     const int two = NP == 2 ? NBtot - (int)gridDim.x : 0;   // workgroups that own two panels
-    const int nb = NP == 2 ? ((int)blockIdx.x < two ? 2 * (int)blockIdx.x : two + (int)blockIdx.x) : (int)blockIdx.x;
+    const int nb = HF ? (int)blockIdx.x >> 1
+                      : NP == 2 ? ((int)blockIdx.x < two ? 2 * (int)blockIdx.x : two + (int)blockIdx.x) : (int)blockIdx.x;
     const int np = NP == 2 && (int)blockIdx.x < two ? 2 : 1;
+    const int hh = HF ? (int)blockIdx.x & 1 : 0;             // half panels: which 8 columns
+    const bool bcol = !HF || ((threadIdx.x >> 3) & 1) == hh; // this lane's column (lane % 16) is one of them
     const int kb_hi = min(ks * kbs + kbs, p.KB);
     const int kb0 = ks * kbs + w * kbw;
     const int kb1 = min(kb0 + kbw, kb_hi);
@@ -186,7 +193,8 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
         for (int pi = 0; pi < NP; pi++)
             if (pi == 0 || np == 2) // workgroup-uniform
 #pragma unroll
-                for (int u = 0; u < U; u++) raw[pi][u] = __builtin_nontemporal_load(bp + pi * pstride + (size_t)(kb + u) * 64);
+                for (int u = 0; u < U; u++)
+                    raw[pi][u] = bcol ? __builtin_nontemporal_load(bp + pi * pstride + (size_t)(kb + u) * 64) : v4i{0, 0, 0, 0};
 #pragma unroll
         for (int u = 0; u < U; u++) {
 #pragma unroll
@@ -230,7 +238,7 @@ __global__ __launch_bounds__(WPG * 64) void k_stream(orkh_mm p, int kbw, int kbs
         const int mt = el >> 8, r = (el >> 6) & 3, ln = el & 63;
         const int m = mt * 16 + (ln >> 4) * 4 + r;
         const int n = (nb + pi) * 16 + (ln & 15);
-        if (m < p.M) {
+        if (m < p.M && (!HF || ((ln >> 3) & 1) == hh)) {
             if (ksplit == 1) C[(size_t)m * p.ldc + n] = finish<KIND>(s);
             else W[((size_t)ks * p.M + m) * p.N + n] = finish<KIND>(s);
         }
@@ -1431,6 +1439,15 @@ template <int KIND, int MT, int WPG>
 int launch_stream_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int KU = (KIND == ORKH_I4U || KIND == ORKH_NF4) ? 4 : 8;
     dim3 grid(p->N / 16, q->ksplit), block(WPG * 64);
+    if (q->half) {
+        if (q->np == 2) {
+            snprintf(g_lerr, sizeof g_lerr, "stream plan: half panels and paired panels exclude each other");
+            return -2;
+        }
+        hipLaunchKernelGGL((k_stream<KIND, MT, WPG, KU, 1, 1>), dim3(p->N / 8, q->ksplit), block, 0, s, *p, q->kbw, q->kbs,
+                           q->ksplit, q->ws);
+        return 0;
+    }
     if (q->np == 2) {
         // paired panels are built for one or two row tiles only (acc[2][MT] and both panels' raw blocks in registers)
         if constexpr (MT <= 2) {
@@ -1869,7 +1886,8 @@ extern "C" const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *q) {
     if (q->algo == ORKH_ALGO_GEMV)
         snprintf(b, sizeof b, "%s_%s_w%d_kbw%d_ks%d", q->half ? "gemvh" : "gemv", k, q->wpg, q->kbw, q->ksplit);
     else if (q->algo == ORKH_ALGO_STREAM)
-        snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d%s", k, q->mt, q->wpg, q->kbw, q->ksplit, q->np == 2 ? "_p2" : "");
+        snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d%s", k, q->mt, q->wpg, q->kbw, q->ksplit,
+                 q->np == 2 ? "_p2" : q->half ? "_h" : "");
     else if (q->ksplit > 1)
         snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
                  q->ksplit, q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");

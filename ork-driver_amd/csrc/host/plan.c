@@ -140,13 +140,27 @@ static double mac_rate(int rkind, int tiled) {
     return tiled ? 0.199 : 0.91;
 }
 
-static double stream_us(const ork_npu *c, int rkind, int M, int N, int KB, int cu, int ks) {
+/* Half panels on the streaming kernel (8 columns per workgroup, twice the workgroups): each workgroup loads half
+ * of its panel's B but all of its rows of A. Offered for int8 and fp16, whose panel bytes are a large share of a
+ * workgroup's; priced by the same model with the halved B and C bytes. Measured against whole panels (graph-timed,
+ * best split of each, us): fp16 K=N=2048 M=16 4.98 -> 4.41, M=8 4.18 -> 3.94; K=2048 N=768 M=16 4.74 -> 4.17; int8
+ * K=N=2048 M=32 4.54 -> 4.13, K=6144 N=2048 M=16 6.74 -> 5.87, K=8192 N=1024 M=8 5.88 -> 5.21; where the halves
+ * need a second round of the CUs they lose (int8 K=N=4096 M=16 5.55 -> 6.79). The uniform-int4 and NF4 nibbles are
+ * a small share of a workgroup's bytes next to its int8 rows of A: half panels lost 2-8% below 32 rows and gained
+ * 2-5% above, so they keep whole panels. Over 72 int8 / fp16 shapes (K x N = 2048 x 2048, 2048 x 768, 4096 x 4096,
+ * 6144 x 2048, 8192 x 1024, 2048 x 6144; M = 2..64) the model's picks come within 3% of the fastest streaming
+ * candidate of each. */
+static int stream_half_offered(int rkind) { return rkind == ORKH_I8 || rkind == ORKH_F16; }
+
+static double stream_us(const ork_npu *c, int rkind, int M, int N, int KB, int cu, int ks, int half) {
     orkh_plan g;
     stream_geom(c, rkind, M, KB, N / 16, cu, ks, &g);
+    if (half && g.np == 2) return -1; /* paired and half panels exclude each other */
     const int pp = g.np == 2 ? 2 : 1; /* panels of the busiest workgroup */
-    const long wgs = g.np == 2 ? g.npg : (long)(N / 16) * g.ksplit;
+    const long wgs = g.np == 2 ? g.npg : (long)(N / 16) * g.ksplit * (half ? 2 : 1);
     const double per = (double)((wgs + cu - 1) / cu);
-    const double kib = ((double)M * a_bytes_per_kb(rkind) * g.kbs + pp * (1024.0 * g.kbs + 64.0 * M)) / 1024;
+    const double kib = ((double)M * a_bytes_per_kb(rkind) * g.kbs +
+                        pp * ((half ? 512.0 : 1024.0) * g.kbs + (half ? 32.0 : 64.0) * M)) / 1024;
     const double mmac = (double)pp * g.mt * 16 * 16 * g.kbs * kpb_of(rkind) / 1e6;
     double t = 1.74 + per * (0.103 + 0.017 * kib + mac_rate(rkind, 0) * mmac);
     if (g.ksplit > 1) t += 2.81 + 0.327 * g.ksplit * (double)M * N * 4 / 1e6;
@@ -328,17 +342,20 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
     }
 
     if (M <= 64 && !f_tiled) {
-        int ks;
+        int ks, half = 0;
         if (M == 1 || f_stream || ks_force > 0 || rkind == ORKH_NF4) {
             ks = ks_force > 0 ? ks_force : stream_rule_ks(c, rkind, M, KB, NB, cu);
         } else {
-            /* both kernels priced, each at its best split; the streaming kernel wins ties */
+            /* both kernels priced, each at its best split (the streaming kernel also with half panels); the
+             * streaming kernel wins ties */
             ks = 1;
-            double ts = stream_us(c, rkind, M, N, KB, cu, 1);
-            for (int k = 2; k <= 8; k *= 2) {
-                if (cdiv(KB, cdiv(KB, k)) != k || cdiv(KB, k) < 4) continue;
-                const double t = stream_us(c, rkind, M, N, KB, cu, k);
-                if (t < ts - 1e-9) { ts = t; ks = k; }
+            double ts = stream_us(c, rkind, M, N, KB, cu, 1, 0);
+            for (int k = 1; k <= 8; k *= 2) {
+                if (k > 1 && (cdiv(KB, cdiv(KB, k)) != k || cdiv(KB, k) < 4)) continue;
+                for (int h = k == 1 ? 1 : 0; h <= stream_half_offered(rkind); h++) {
+                    const double t = stream_us(c, rkind, M, N, KB, cu, k, h);
+                    if (t >= 0 && t < ts - 1e-9) { ts = t; ks = k; half = h; }
+                }
             }
             orkh_plan t2;
             memset(&t2, 0, sizeof t2);
@@ -352,6 +369,9 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
         q->algo = (M == 1 && !f_stream) ? ORKH_ALGO_GEMV : ORKH_ALGO_STREAM;
         stream_geom(c, rkind, M, KB, NB, cu, ks, q);
         if (q->algo == ORKH_ALGO_GEMV) gemv_half_geom(c, rkind, NB, cu, q);
+        if (q->algo == ORKH_ALGO_STREAM) q->half = half && q->np == 1;
+        const char *fh = knob(c, "ORK_STREAM_HALF"); /* testing / A-B: half panels on or off on the streaming kernel */
+        if (q->algo == ORKH_ALGO_STREAM && q->np == 1 && fh) q->half = atoi(fh) != 0;
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }

@@ -19,7 +19,8 @@ static const char *name(int kind, const orkh_plan *q) {
     if (q->algo == ORKH_ALGO_GEMV)
         snprintf(b, sizeof b, "%s_%s_w%d_kbw%d_ks%d", q->half ? "gemvh" : "gemv", k, q->wpg, q->kbw, q->ksplit);
     else if (q->algo == ORKH_ALGO_STREAM)
-        snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d%s", k, q->mt, q->wpg, q->kbw, q->ksplit, q->np == 2 ? "_p2" : "");
+        snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d%s", k, q->mt, q->wpg, q->kbw, q->ksplit,
+                 q->np == 2 ? "_p2" : q->half ? "_h" : "");
     else if (q->ksplit > 1)
         snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
                  q->ksplit, q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");

@@ -131,6 +131,9 @@ CASES = [
     ("i8", 37, 2048, 96, {"ORK_PLAN": "stream", "ORK_KSPLIT": 2}, "stream_i8_mt3"),
     ("f16", 9, 1024, 80, {"ORK_PLAN": "stream"}, "stream_f16"),
     ("nf4", 20, 2048, 160, {"ORK_PLAN": "stream"}, "stream_nf4"),
+    ("f16", 16, 2048, 768, {}, "stream_f16_mt1_w8_kbw8_ks1_h"),
+    ("i8", 37, 2048, 96, {"ORK_PLAN": "stream", "ORK_STREAM_HALF": 1, "ORK_KSPLIT": 2}, "_ks2_h"),
+    ("w4a4", 21, 1024, 128, {"ORK_PLAN": "stream", "ORK_STREAM_HALF": 1}, "_h"),
     ("i8", 130, 2048, 4128, {"ORK_TILE": "64x192"}, "64x192"),
     ("i8", 200, 1024, 4128, {"ORK_TILE": "128x128"}, "128x128"),
     ("i8", 300, 1024, 544, {"ORK_TILE": "256x256"}, "256x256"),

@@ -656,6 +656,53 @@ def test_stream_paired_panels(npu, kind, np_):
         ork.free(w)
 
 
+@pytest.mark.parametrize("ks", [1, 2])
+@pytest.mark.parametrize("kind", ["i8", "i4a8", "nf4", "f16", "w4a4"])
+def test_stream_half_panels(npu, kind, ks):
+    """The streaming kernel with half panels (ORK_STREAM_HALF: each workgroup loads and stores 8 of a panel's 16
+    columns, twice the workgroups), every kind the kernel is built for, whole K and split K: exact for the integer
+    kinds, within the fp16 bar for fp16, and every column of C written by its own half (N = 128 and 320: 16 and 40
+    half panels; M = 1 row tile to 4, with tails; K tails)."""
+    _say("stream half", kind, ks)
+    rng = np.random.default_rng(131 + ks)
+    for (K, N, M) in [(1056, 128, 2), (2080, 320, 17), (512, 320, 64), (4096, 128, 37)]:
+        if kind == "w4a4":
+            B = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
+            A = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+            w = npu.pack_i4(B)
+            ref = O.gemm_i32(A, B)
+            run = npu.run_i4
+        elif kind == "f16":
+            B = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+            A = rng.standard_normal((M, K)).astype(np.float16)
+            w = npu.pack_f16(B)
+            ref = O.gemm_f16_f64acc(A, B)
+            run = npu.run_f16
+        elif kind == "i8":
+            B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+            A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            w = npu.pack_i8(B)
+            ref = O.gemm_i32(A, B)
+            run = npu.run_i8
+        else:
+            W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+            with _env(**({"ORK_NF4": 1} if kind == "nf4" else {})):
+                w, _ = npu.pack_i4a8(W)
+            _, _, codes = O.pack_i4a8(W, nf4=kind == "nf4")
+            A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            ref = O.gemm_i32(A, codes)
+            run = npu.run_i8
+        with _env(ORK_PLAN="stream", ORK_STREAM_HALF=1, ORK_KSPLIT=ks):
+            rc, C = run(w, A)
+            name = npu.plan_name(w, M)
+        assert rc == 0 and name.startswith("stream_") and name.endswith("_h") and f"_ks{ks}_" in name, name
+        if kind == "f16":
+            assert O.fp16_err(C, ref) <= FP16_TOL, name
+        else:
+            assert np.array_equal(C, ref), (name, K, N, M)
+        ork.free(w)
+
+
 @pytest.mark.parametrize("kind,K,N,M", [("i8", 2048, 6144, 48), ("i8", 6144, 2048, 64), ("i4a8", 2048, 6144, 64),
                                         ("f16", 2048, 6144, 32), ("i8", 2048, 22016, 24)])
 def test_planner_mid_m_default(npu, kind, K, N, M):

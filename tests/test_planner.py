@@ -57,3 +57,15 @@ def test_fixed_picks(planner):
     64 x 192 LDS-ring tile with line-loaded A at M=512 (int8 K=2048 N=6144), the GEMV for NF4 at M=1."""
     got = planner([(0, 1, 2048, 6144), (0, 512, 2048, 6144), (2, 1, 2048, 6144)])
     assert got[0].startswith("gemvh_i8_") and got[1] == "tiled2_i8_64x192_al" and got[2].startswith("gemvh_nf4_"), got
+
+
+def test_stream_half_panels_offered(planner):
+    """Half panels on the streaming kernel: taken for fp16 and int8 where the halves still fit one round of the CUs
+    (C2 fp16 K=N=2048 M=16: 4.98 -> 4.41 us measured; int8 K=6144 N=2048 M=16), not where they would need a second
+    round (int8 K=N=4096 M=16), not with paired panels (C1 M=16), never for the nibble kinds."""
+    got = planner([(3, 16, 2048, 2048), (0, 16, 6144, 2048), (0, 16, 4096, 4096), (0, 16, 2048, 6144),
+                   (1, 16, 2048, 2048), (2, 16, 2048, 2048)])
+    assert got[0].startswith("stream_f16_") and got[0].endswith("_h"), got
+    assert got[1].startswith("stream_i8_") and got[1].endswith("_h"), got
+    assert not got[2].endswith("_h") and got[3].endswith("_p2"), got
+    assert not got[4].endswith("_h") and not got[5].endswith("_h"), got
