@@ -1070,12 +1070,13 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     }
     wait_vmcnt<0>();
 
-    // The 2 x 2 x 4 uniform-int4 tile (t2_xg 2): all four K groups park their partial tiles in the ring and all 16
-    // waves sum them, in group order, and store C, 16 bytes a thread. Measured against group 0 alone summing and
-    // storing (below): W4A4 M=256 K=N=4096 12.93 -> 12.62 us; slower on the other K-group tiles (int8 M=128 32 x 32
-    // 6.35 -> 6.57, W4A8 M=64 32 x 64 7.16 -> 7.20) and on the tiles without K groups (int8 M=512 64 x 192 13.88
-    // -> 14.51), so only here.
-    if constexpr (GR == 0 && t2_xg<KIND, BM, BN, GR>() == 2) {
+    // The 2 x 2 x 4 uniform-int4 tile (t2_xg 2) and the fp16 32 x 32 tile (4 K groups): all the K groups park
+    // their partial tiles in the ring and all 16 waves sum them, in group order (the same fp32 sums as group 0
+    // adding them below), and store C, 16 bytes a thread. Measured against group 0 alone summing and storing:
+    // W4A4 M=256 K=N=4096 12.93 -> 12.62 us, fp16 M=128 K=N=2048 8.91 -> 8.77; slower on the other K-group tiles
+    // (int8 M=128 32 x 32 6.35 -> 6.57, W4A8 M=64 32 x 64 7.16 -> 7.20) and on the tiles without K groups (int8
+    // M=512 64 x 192 13.88 -> 14.51), so only here.
+    if constexpr (GR == 0 && (t2_xg<KIND, BM, BN, GR>() == 2 || (KIND == ORKH_F16 && BM == 32 && BN == 32))) {
         constexpr int SPAD = BN + 4; // words per parked row: a row's 16-lane store groups start in different banks
         static_assert((size_t)P::WK * BM * SPAD * sizeof(c_t) <= (size_t)R * P::SLOT, "partial tiles fit the ring");
         c_t *Ts = (c_t *)sm;
@@ -1107,7 +1108,8 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                 for (int u = 0; u < 4; u++) v[u] += Ts[(g * BM + row) * SPAD + c4 + u];
             c_t *dst = Cb + (size_t)m * ldc + n;
             if (vec) {
-                *(v4i *)dst = v4i{finish<KIND>(v[0]), finish<KIND>(v[1]), finish<KIND>(v[2]), finish<KIND>(v[3])};
+                typedef c_t v4c __attribute__((ext_vector_type(4)));
+                *(v4c *)dst = v4c{finish<KIND>(v[0]), finish<KIND>(v[1]), finish<KIND>(v[2]), finish<KIND>(v[3])};
             } else {
 #pragma unroll
                 for (int u = 0; u < 4; u++) dst[u] = finish<KIND>(v[u]);

@@ -240,21 +240,23 @@ def test_grouped_guards(gnpu, M, K, N, G, env, want):
 
 @pytest.mark.parametrize("shift", [0, 4, 8])
 @pytest.mark.parametrize("M", [150, 64])
-def test_w4a4_tile_c_alignment_guards(gnpu, shift, M):
-    """The W4A4 64 x 64 tile (all 16 waves store C, 16 bytes a thread where C is 16-byte aligned, else a word at a
-    time) into a C that starts 0, 4 or 8 bytes past a 16-byte boundary: exact, and the bytes either side untouched.
-    M = 150 leaves a partial row tile; N = 320 five panels of 64."""
-    rng = np.random.default_rng(980 + shift + M)
+@pytest.mark.parametrize("kind,tile", [("w4a4", "64x64"), ("f16", "32x32")])
+def test_allwave_epilogue_c_alignment_guards(gnpu, shift, M, kind, tile):
+    """The tiles whose 16 waves all store C (W4A4 64 x 64, fp16 32 x 32: 16 bytes a thread where C is 16-byte
+    aligned, else a word at a time) into a C that starts 0, 4 or 8 bytes past a 16-byte boundary: exact (fp16:
+    within its bar), and the bytes either side untouched. M = 150 leaves a partial row tile; N = 320 five panels
+    of 64."""
+    rng = np.random.default_rng(980 + shift + M + len(kind))
     K, N = 1024, 320
-    w, run, gen_a, ref = _weight(gnpu, "w4a4", K, N, rng)
+    w, run, gen_a, ref = _weight(gnpu, kind, K, N, rng)
     A = gen_a(M)
     g = Guarded(gnpu, M * N * 4 + 16)
     dA = _dev(gnpu, A)
     try:
-        with _env({"ORK_TILE": "64x64"}):
+        with _env({"ORK_TILE": tile}):
             name = gnpu.plan_name(w, M)
-            _say("w4a4 tile C alignment", M, shift, name)
-            assert name == "tiled2_i4u_64x64", name
+            _say("all-wave epilogue C alignment", kind, M, shift, name)
+            assert name == ("tiled2_i4u_" if kind == "w4a4" else "tiled2_f16_") + tile, name
             assert run(gnpu.h, w, M, dA, g.c + shift) == 0
         got = g.read()
         g.check(got, name)
@@ -262,7 +264,10 @@ def test_w4a4_tile_c_alignment_guards(gnpu, shift, M):
         init = g.init[GUARD:GUARD + M * N * 4 + 16]
         assert np.array_equal(body[:shift], init[:shift]) and np.array_equal(body[shift + M * N * 4:],
                                                                                init[shift + M * N * 4:])
-        assert np.array_equal(body[shift:shift + M * N * 4].view(np.int32).reshape(M, N), ref(A))
+        if kind == "f16":
+            assert O.fp16_err(body[shift:shift + M * N * 4].view(np.float32).reshape(M, N), ref(A)) <= 2e-3
+        else:
+            assert np.array_equal(body[shift:shift + M * N * 4].view(np.int32).reshape(M, N), ref(A))
     finally:
         g.free()
         ork.lib().ork_dev_free(gnpu.h, dA)
