@@ -856,8 +856,8 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     float cacc[P::MTW][P::NTW][4];
     float sa[P::MTW][4], sb[P::NTW]; // scales of the next group to close
     int gcur = 0, gend = GR ? gp.G : 0; // that group and the k where it ends
-    const int gps = GR == 2 ? gp.G / (KS * T::KPB) : 1; // stages per group (groups of whole stages)
-    int sgs = 0;                                          // stages of the current group done
+    const int gps = GR == 2 ? gp.G / T::KPB : 1; // K-blocks per group (groups of whole K-blocks)
+    int sgs = 0;                                   // K-blocks of the current group done
     auto load_sc = [&](int g) {
 #pragma unroll
         for (int i = 0; i < P::MTW; i++)
@@ -1012,17 +1012,18 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
 #pragma unroll
                         for (int jn = 0; jn < P::NTW; jn++) acc[i][jn] = mma(a, op[jn][st], acc[i][jn]);
                     }
+                if constexpr (GR == 2) {
+                    // groups of whole K-blocks: close the group this K-block ends (the zero-filled K-blocks past
+                    // the end, in a last stage of fewer, count for none)
+                    if (kb_lo + s * KS + kbl < kb_hi && ++sgs == gps) {
+                        sgs = 0;
+                        close_group();
+                    }
+                }
             }
         }
         if constexpr (PIPE && !EARLY) {
             if (s + 1 < nst) decode_stage(s + 1);
-        }
-        if constexpr (GR == 2) {
-            // groups of whole stages: the stage ran as in the plain kernel; close the group it ends
-            if (++sgs == gps) {
-                sgs = 0;
-                close_group();
-            }
         }
         if constexpr (GR == 1) {
             // every fragment of the stage is read first, as above, so the LDS latencies overlap; then the
@@ -1187,8 +1188,8 @@ __global__ __launch_bounds__(1024) void k_tiled2m(T2Multi g) {
 }
 
 // Grouped runs (never K-split: the groups close in order inside one workgroup). GR 2: every group is whole
-// stages (G % (KS * KPB) == 0), so the stage runs as in the plain kernel and a group closes between stages;
-// GR 1: any G % 32 == 0, walked K-block by K-block.
+// K-blocks (G % KPB == 0), so the stage runs as in the plain kernel and a group closes after the K-block that ends
+// it; GR 1: any G % 32 == 0, walked K-block by K-block with a group test per MFMA step.
 template <int KIND, int BM, int BN, int KS, int GR, bool AL>
 __global__ __launch_bounds__(1024) void k_tiled2g(orkh_mm p, int mtiles, int ntiles_all, T2Group gp) {
     tiled2_body<KIND, BM, BN, KS, GR, AL>(p, mtiles, ntiles_all, p.KB, nullptr, gp, (int)blockIdx.x, (int)gridDim.x);
@@ -1768,14 +1769,25 @@ extern "C" int orkh_mm_launch_group(const orkh_group *g, int wpg, void *stream) 
 }
 
 namespace {
-template <int KIND, int BM, int BN>
-int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s) {
-    constexpr int KS = t2_ks<KIND, BM, BN>();
+// Stage depth of a grouped run whose groups are whole K-blocks: the plain kernel's, except for uniform int4, whose
+// one-K-block stages (12 KiB on 64 x 64, whose plain runs take four K-blocks on the 2 x 2 x 4 wave grid that grouped
+// runs cannot use) keep too few bytes in flight per CU: four K-blocks on 64 x 64, two on 64 x 192, or two, or the plain
+// depth, where the larger ring and the tile's scales do not fit the LDS together. Measured against one K-block
+// (graph-timed, us, W4A4 K=N=4096 unless given): 64 x 64 G=128 M=256 20.11 -> 18.54, M=128 19.72 -> 18.10, G=256
+// 17.34 -> 15.65, K=8192 G=128 (two K-blocks) 36.49 -> 33.11; 64 x 192 M=512 35.79 -> 35.17, K=2048 N=6144 M=256
+// 19.83 -> 19.48. With groups inside a K-block (GR 1) two K-blocks measured slower (G=64 34.88 -> 35.34), so those
+// keep the plain depth.
+template <int KIND, int BM, int BN> constexpr int t2g_ks() {
+    return KIND != ORKH_I4U ? t2_ks<KIND, BM, BN>() : BN == 64 ? 4 : 2;
+}
+
+template <int KIND, int BM, int BN, int KS>
+int launch_tiled2g_k(const orkh_mm *p, const T2Group &gp, hipStream_t s, size_t sc) {
     using P = T2<KIND, BM, BN, KS>;
-    const bool whole = gp.G % (KS * KT<KIND>::KPB) == 0;
+    const bool whole = gp.G % KT<KIND>::KPB == 0;
     auto kern = whole ? k_tiled2g<KIND, BM, BN, KS, 2, false> : k_tiled2g<KIND, BM, BN, KS, 1, false>;
+    const size_t lds = P::LDS + sc;
     const int Sk = p->K / gp.G;
-    const size_t lds = P::LDS + (size_t)((BM * Sk * 4 + 1023) / 1024 + (Sk * BN * 4 + 1023) / 1024) * 1024;
     if (lds > 163840) {
         snprintf(g_lerr, sizeof g_lerr, "grouped tiled2 %dx%d: %d groups need %zu B of LDS", BM, BN, Sk, lds);
         return -2;
@@ -1790,6 +1802,21 @@ int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s) {
     }
     hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(1024), lds, s, *p, mtiles, mtiles * ntiles, gp);
     return 0;
+}
+
+template <int KIND, int BM, int BN>
+int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s) {
+    const int Sk = p->K / gp.G;
+    const size_t sc = (size_t)((BM * Sk * 4 + 1023) / 1024 + (Sk * BN * 4 + 1023) / 1024) * 1024; // the tile's scales
+    constexpr int KD = t2g_ks<KIND, BM, BN>(), K1 = t2_ks<KIND, BM, BN>();
+    const bool whole = gp.G % KT<KIND>::KPB == 0;
+    if constexpr (KD != K1) {
+        if (whole && T2<KIND, BM, BN, KD>::LDS + sc <= 163840) return launch_tiled2g_k<KIND, BM, BN, KD>(p, gp, s, sc);
+    }
+    if constexpr (KD > 2 && K1 < 2) {
+        if (whole && T2<KIND, BM, BN, 2>::LDS + sc <= 163840) return launch_tiled2g_k<KIND, BM, BN, 2>(p, gp, s, sc);
+    }
+    return launch_tiled2g_k<KIND, BM, BN, K1>(p, gp, s, sc);
 }
 
 template <int KIND>

@@ -421,9 +421,10 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
  * K is never split. Few rows: k_grouped streams each 16-column panel (and re-reads A per panel). With more
  * rows, int8 and uniform int4 take the LDS-ring kernel at the unsplit 64-row tile (64x192 or 64x64) the time
  * model prices lowest, when the tile's scales fit in LDS beside its ring (else 64x64, else k_grouped):
- *   from 32 rows when every group is whole 128-k stages (G % 128 == 0: the stage runs as in the plain kernel
- *   and a group closes between stages; e.g. W4A4 K=N=4096 G=128: 42.9 -> 21.6 us at M=256);
- *   from 128 rows otherwise (groups end inside stages and the kernel walks them K-block by K-block).
+ *   from 32 rows when every group is whole 128-k spans (G % 128 == 0: the stage runs as in the plain kernel and a
+ *   group closes after the K-block that ends it; e.g. W4A4 K=N=4096 G=128: 42.9 -> 21.6 us at M=256, since 18.5
+ *   with deeper stages);
+ *   from 128 rows otherwise (groups can end inside K-blocks and the kernel walks them K-block by K-block).
  * NF4 stays on k_grouped (its codebook decode would repeat in every wave row).
  * ORK_PLAN=stream|tiled forces either (tests, A/B). */
 #define ORKI_GROUPED_TILED_M 32
