@@ -509,6 +509,29 @@ def test_run_errors(npu):
 
 
 @pytest.mark.parametrize("tile", ["256x256", "128x128", "128x96", "64x192", "64x64", "32x64", "32x32", "16x64", "16x32"])
+def test_nf4_ring_short_k(npu, tile):
+    """NF4 on every LDS-ring tile with rings of one to three stages (K = 32, 128, 160, 288: one K-block, one, two and
+    three, the last ones ending mid-block): the stage decode runs a stage ahead where the tile has room for two decode
+    buffers, so the first and last stages are its edges. Exact against the oracle, M = 70 and 5 (row tails)."""
+    _say("nf4 short-K ring", tile)
+    rng = np.random.default_rng(141 + int(tile.split("x")[0]) + int(tile.split("x")[1]))
+    N = 224
+    for K in (32, 128, 160, 288):
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        with _env(ORK_NF4=1):
+            w, _ = npu.pack_i4a8(W)
+        _, _, codes = O.pack_i4a8(W, nf4=True)
+        for M in (70, 5):
+            A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            with _env(ORK_TILE=tile):
+                rc, C = npu.run_i8(w, A)
+                name = npu.plan_name(w, M)
+            assert name.startswith("tiled2_nf4_" + tile), name
+            assert rc == 0 and np.array_equal(C, O.gemm_i32(A, codes)), (name, K, M)
+        ork.free(w)
+
+
+@pytest.mark.parametrize("tile", ["256x256", "128x128", "128x96", "64x192", "64x64", "32x64", "32x32", "16x64", "16x32"])
 @pytest.mark.parametrize("ks", [1, 3])
 @pytest.mark.parametrize("aline", [0, 1])
 def test_lds_ring_tiles_all_kinds(npu, tile, ks, aline):
