@@ -687,10 +687,13 @@ template <int KIND, int BM, int BN, int KS, int XG = 0> struct T2 {
     static constexpr int DEC1 = KIND == ORKH_NF4 ? NIB * T::STEPS * 1024 : 0;
     static constexpr bool DEC2 = KIND == ORKH_NF4 && (163840 - 2 * DEC1) / SLOT >= 3;
     static constexpr int DEC = DEC2 ? 2 * DEC1 : DEC1;
-    // ring within 160 KiB: 4 slots, 8 for the small stages of the K-group tiles (more bytes in flight per CU);
-    // 8 slots for the 12-16 KiB stages of the other tiles measured slower (int8 M=128 64 x 64 8.5 -> 9.4 us,
-    // fp16 M=512 13.0 -> 14.0, grouped W4A4 M=256 21.9 -> 22.7)
-    static constexpr int RMAX = WK > 1 ? 8 : 4;
+    // ring within 160 KiB: 4 slots. More bytes in flight per CU delay a stage's last lines (a CU's deliveries
+    // interleave across the stages it has asked for) more than they feed the loop: 8 slots on the K-group tiles
+    // measured slower (us: W4A8 M=64 K=2048 N=6144 32 x 64 6.12 -> 7.14, NF4 7.57 -> 8.61, int8 M=128 K=N=2048
+    // 32 x 32 5.35 -> 6.34, fp16 8.26 -> 8.79), and so did 8 slots for the 12-16 KiB stages of the other tiles (int8
+    // M=128 64 x 64 8.5 -> 9.4, fp16 M=512 13.0 -> 14.0); 3 slots lose too (W4A8 M=64 6.12 -> 6.48, fp16 M=512
+    // 64 x 64 12.86 -> 14.68), and 2 lose badly
+    static constexpr int RMAX = 4;
     static constexpr int R = ((163840 - DEC) / SLOT) < RMAX ? ((163840 - DEC) / SLOT) : RMAX;
     static constexpr size_t LDS = (size_t)R * SLOT + DEC;
     static constexpr size_t RED = (size_t)(WK - 1) * WM * WN * MTW * NTW * 1024; // K-group partial tiles

@@ -173,19 +173,19 @@ static double stream_us(const ork_npu *c, int rkind, int M, int N, int KB, int c
  * kernel / tile / split candidates in all (tests/golden/nf4_plan_sweep.json),
  *   t = a + rounds * (b + c * KiB) + [ks > 1] (d + e * ks * M * N * 4 / 1e6)   us,
  * KiB being the A and B bytes one workgroup loads (the streaming kernel: the form of stream_us). The fits are
- * within 3-7% rms per candidate; over the 45 shapes the picks total 639 us against 633 for the fastest timed
- * candidate of each (the row-count rules they replace: 687 -- e.g. K=6144 N=2048 M=64 15.6 -> 10.9 us, K=2048
- * N=12288 M=64 14.9 -> 10.2, K=N=2048 M=192 9.8 -> 8.0). */
+ * within 3-7% rms per candidate; over the 45 shapes the picks total 627 us against 621 for the fastest timed
+ * candidate of each (the row-count rules they replaced totalled 687 on the kernels of the time, against 633 for
+ * the fastest: e.g. K=6144 N=2048 M=64 15.6 -> 10.9 us, K=2048 N=12288 M=64 14.9 -> 10.2, K=N=2048 M=192 9.8 -> 8.0). */
 static const struct nf4_fit {
     int algo, bm, bn, ksmax;
     double a, b, c, d, e;
 } nf4_fits[] = {
-    {ORKH_ALGO_TILED2, 128, 128, 4, 4.3789, 0.0, 0.0301, 2.3617, 0.4960},
-    {ORKH_ALGO_TILED2, 64, 64, 4, 4.6225, 0.0, 0.0289, 1.8197, 0.5224},
-    {ORKH_ALGO_TILED2, 32, 64, 4, 1.4873, 2.5357, 0.0320, 2.6686, 0.2686},
-    {ORKH_ALGO_TILED, 128, 128, 8, 5.3888, 3.6819, 0.0342, 2.9385, 0.4929},
-    {ORKH_ALGO_TILED, 128, 96, 8, 3.8799, 3.9957, 0.0294, 2.9103, 0.4592},
-    {ORKH_ALGO_TILED, 64, 64, 8, 3.5871, 1.4189, 0.0256, 2.7677, 0.4113},
+    {ORKH_ALGO_TILED2, 128, 128, 4, 4.3479, 0.0, 0.0301, 2.3639, 0.4989},
+    {ORKH_ALGO_TILED2, 64, 64, 4, 4.5624, 0.0, 0.0290, 1.8830, 0.5202},
+    {ORKH_ALGO_TILED2, 32, 64, 4, 1.3497, 2.0597, 0.0297, 2.7524, 0.4021},
+    {ORKH_ALGO_TILED, 128, 128, 8, 5.4417, 3.5824, 0.0342, 2.9230, 0.4990},
+    {ORKH_ALGO_TILED, 128, 96, 8, 3.8645, 3.9671, 0.0295, 2.9059, 0.4594},
+    {ORKH_ALGO_TILED, 64, 64, 8, 3.5684, 1.4132, 0.0256, 2.7887, 0.4122},
 };
 
 static void nf4_best(const ork_npu *c, int M, int N, int KB, int cu, orkh_plan *q) {
@@ -204,8 +204,8 @@ static void nf4_best(const ork_npu *c, int M, int N, int KB, int cu, orkh_plan *
             const double per = (double)((wgs + cu - 1) / cu);
             const double kib = ((double)M * 128 * g.kbs + pp * (1024.0 * g.kbs + 64.0 * M)) / 1024;
             const double mmac = (double)pp * g.mt * 16 * 16 * g.kbs * 128 / 1e6;
-            double t = 2.0935 + per * (0.0245 * kib + 0.2674 * mmac);
-            if (ks > 1) t += 2.0600 + 0.6076 * ks * part;
+            double t = 2.0835 + per * (0.0241 * kib + 0.2942 * mmac);
+            if (ks > 1) t += 2.0516 + 0.6116 * ks * part;
             if (best < 0 || t < best - 1e-9) {
                 best = t;
                 *q = g;
