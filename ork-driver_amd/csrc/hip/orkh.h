@@ -121,6 +121,8 @@ typedef struct orkh_plan {
     /* TILED2: 1 = load A stages as whole 128-byte row lines into a swizzled LDS image where the stage's rows
      * are one line each (else, and with 0, in MFMA fragment order) */
     int aline;
+    /* TILED2: 2 = a two-slot ring (two workgroups per CU on the tiles whose 4-slot ring fills one), else 0 */
+    int ring;
     /* STREAM: np = 2 pairs panels: npg workgroups, the first N/16 - npg owning two adjacent panels each */
     int np, npg;
     /* GEMV and STREAM: 1 = half a panel (8 columns) per workgroup, grid (N/8, ksplit) (k_gemv_half, k_stream's
@@ -188,6 +190,9 @@ typedef struct orkh_row {
 int orkh_row_launch(const orkh_row *p, void *stream);
 /* Bytes of LDS the stage ring of k_tiled2 takes for (kind, bm x bn); -1 for a tile that is not built. */
 int orkh_tiled2_ring_lds(int kind, int bm, int bn);
+/* 1 where the LDS-ring kernel has a two-slot ring for the tile (plan.ring = 2): tiles whose ring of up to 4 slots
+ * leaves room for one workgroup per CU, and two with 2 slots; never NF4 */
+int orkh_tiled2_ring2_ok(int kind, int bm, int bn);
 /* Names of the compiled kernel variants, for diagnostics ("stream_i8_mt1_w4", ...). */
 const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *plan);
 

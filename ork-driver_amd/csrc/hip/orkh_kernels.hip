@@ -669,7 +669,7 @@ template <int VM> __device__ __forceinline__ void wait_vmcnt() {
 // Waves across a tile's block columns: all of them up to 4, else 4 when they divide evenly, else 2.
 constexpr int t2_wn(int nb) { return nb < 4 ? nb : (nb % 4 == 0 ? 4 : 2); }
 
-template <int KIND, int BM, int BN, int KS, int XG = 0> struct T2 {
+template <int KIND, int BM, int BN, int KS, int XG = 0, int RC = 0> struct T2 {
     using T = KT<KIND>;
     static constexpr int MB = BM / 16, NB = BN / 16, NW = 16;
     // 16 waves: WM x WN over the tile's 16 x 16 blocks and, on tiles of fewer than 16 blocks (32- and 16-row tiles)
@@ -685,7 +685,7 @@ template <int KIND, int BM, int BN, int KS, int XG = 0> struct T2 {
     // WM waves that read a block (the codebook decode is ~8x the VALU work of the uniform-int4 one)
     // Two stages of them where a ring of 3 slots still fits (the decode then runs a stage ahead: tiled2_body)
     static constexpr int DEC1 = KIND == ORKH_NF4 ? NIB * T::STEPS * 1024 : 0;
-    static constexpr bool DEC2 = KIND == ORKH_NF4 && (163840 - 2 * DEC1) / SLOT >= 3;
+    static constexpr bool DEC2 = KIND == ORKH_NF4 && RC == 0 && (163840 - 2 * DEC1) / SLOT >= 3;
     static constexpr int DEC = DEC2 ? 2 * DEC1 : DEC1;
     // ring within 160 KiB: 4 slots. More bytes in flight per CU delay a stage's last lines (a CU's deliveries
     // interleave across the stages it has asked for) more than they feed the loop: 8 slots on the K-group tiles
@@ -694,7 +694,8 @@ template <int KIND, int BM, int BN, int KS, int XG = 0> struct T2 {
     // M=128 64 x 64 8.5 -> 9.4, fp16 M=512 13.0 -> 14.0); 3 slots lose too (W4A8 M=64 6.12 -> 6.48, fp16 M=512
     // 64 x 64 12.86 -> 14.68), and 2 lose badly
     static constexpr int RMAX = 4;
-    static constexpr int R = ((163840 - DEC) / SLOT) < RMAX ? ((163840 - DEC) / SLOT) : RMAX;
+    // RC: a ring of RC slots instead (k_tiled2's two-workgroups-per-CU form, launch_tiled2_v)
+    static constexpr int R = RC ? RC : ((163840 - DEC) / SLOT) < RMAX ? ((163840 - DEC) / SLOT) : RMAX;
     static constexpr size_t LDS = (size_t)R * SLOT + DEC;
     static constexpr size_t RED = (size_t)(WK - 1) * WM * WN * MTW * NTW * 1024; // K-group partial tiles
     // A stage whose rows are one 128-byte line each is loaded a line at a time (8 rows x 128 B per instruction)
@@ -763,12 +764,12 @@ struct T2Group {
 
 // bid, nT: this workgroup's index among the launch's nT workgroups of this matmul (blockIdx.x and gridDim.x, or a
 // task's share of a grouped launch, which starts at a multiple of 8 so that bid % 8 is still the XCD)
-template <int KIND, int BM, int BN, int KS, int GR, bool AL>
+template <int KIND, int BM, int BN, int KS, int GR, bool AL, int RC = 0>
 __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int ntiles_all, int kbs, void *ws,
                                             const T2Group &gp, int bid, int nT) {
 #pragma clang fp contract(off)
     using T = KT<KIND>;
-    using P = T2<KIND, BM, BN, KS, t2_xg<KIND, BM, BN, GR>()>;
+    using P = T2<KIND, BM, BN, KS, t2_xg<KIND, BM, BN, GR>(), RC>;
     constexpr int R = P::R;
     constexpr bool LINE = AL && P::LINE_OK; // A stage as whole row lines (a_lds), else in fragment order
     typedef typename T::acc_t acc_t;
@@ -1165,10 +1166,10 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         }
 }
 
-template <int KIND, int BM, int BN, int KS, bool AL>
+template <int KIND, int BM, int BN, int KS, bool AL, int RC = 0>
 __global__ __launch_bounds__(1024) void k_tiled2(orkh_mm p, int mtiles, int ntiles_all, int kbs, void *ws) {
-    tiled2_body<KIND, BM, BN, KS, 0, AL>(p, mtiles, ntiles_all, kbs, ws, T2Group{0, nullptr, nullptr}, (int)blockIdx.x,
-                                         (int)gridDim.x);
+    tiled2_body<KIND, BM, BN, KS, 0, AL, RC>(p, mtiles, ntiles_all, kbs, ws, T2Group{0, nullptr, nullptr},
+                                             (int)blockIdx.x, (int)gridDim.x);
 }
 
 // k_tiled2m: up to ORKH_TGROUP_MAX matmuls of one kind, M and K in one launch (the multi-matmul submit): task t's
@@ -1537,13 +1538,36 @@ template <int KIND, int BM, int BN, int XG = 0> constexpr int t2_ks() {
     return base > wk ? base : wk;
 }
 
+template <int KIND, int BM, int BN, int RC>
+int launch_tiled2_r(const orkh_mm *p, const orkh_plan *q, hipStream_t s);
+
+// Two-slot ring (plan.ring == 2): for the tiles whose ring of up to 4 slots holds the CU's LDS for one workgroup, a
+// ring of two fits two workgroups on a CU, so on a grid of several rounds one's set-up and epilogue overlap the other's
+// loop. Not built for NF4 (its decode runs a stage ahead and needs 3 slots).
+template <int KIND, int BM, int BN, int XG, int KS>
+constexpr bool t2_ring2_ok() {
+    return KIND != ORKH_NF4 && T2<KIND, BM, BN, KS, XG>::LDS > 81920 && T2<KIND, BM, BN, KS, XG, 2>::LDS <= 81920;
+}
+
 template <int KIND, int BM, int BN>
 int launch_tiled2_v(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
     constexpr int XG = t2_xg<KIND, BM, BN, 0>();
     constexpr int KS = t2_ks<KIND, BM, BN, XG>();
-    using P = T2<KIND, BM, BN, KS, XG>;
+    if (q->ring == 2) {
+        if constexpr (t2_ring2_ok<KIND, BM, BN, XG, KS>()) return launch_tiled2_r<KIND, BM, BN, 2>(p, q, s);
+        snprintf(g_lerr, sizeof g_lerr, "tiled2 plan: no two-slot ring for %dx%d of this kind", BM, BN);
+        return -2;
+    }
+    return launch_tiled2_r<KIND, BM, BN, 0>(p, q, s);
+}
+
+template <int KIND, int BM, int BN, int RC>
+int launch_tiled2_r(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
+    constexpr int XG = t2_xg<KIND, BM, BN, 0>();
+    constexpr int KS = t2_ks<KIND, BM, BN, XG>();
+    using P = T2<KIND, BM, BN, KS, XG, RC>;
     const bool al = q->aline && P::LINE_OK;
-    auto kern = al ? k_tiled2<KIND, BM, BN, KS, true> : k_tiled2<KIND, BM, BN, KS, false>;
+    auto kern = al ? k_tiled2<KIND, BM, BN, KS, true, RC> : k_tiled2<KIND, BM, BN, KS, false, RC>;
     static lds_flags attr[2]; // per instantiation: allow more than the default 64 KiB of dynamic LDS
     if (lds_limit((const void *)kern, (int)P::LDS, attr[al])) return -1;
     const int mtiles = (p->M + BM - 1) / BM;
@@ -1831,6 +1855,24 @@ int launch_tiled2g(const orkh_mm *p, const orkh_plan *q, const T2Group &gp, hipS
 }
 } // namespace
 
+extern "C" int orkh_tiled2_ring2_ok(int kind, int bm, int bn) {
+#define ORKH_RING2(KIND)                                                                                     \
+    if (bm == 128 && bn == 128) return (int)t2_ring2_ok<KIND, 128, 128, t2_xg<KIND, 128, 128, 0>(),            \
+                                                        t2_ks<KIND, 128, 128, t2_xg<KIND, 128, 128, 0>()>()>(); \
+    if (bm == 128 && bn == 96) return (int)t2_ring2_ok<KIND, 128, 96, t2_xg<KIND, 128, 96, 0>(),               \
+                                                       t2_ks<KIND, 128, 96, t2_xg<KIND, 128, 96, 0>()>()>();    \
+    if (bm == 64 && bn == 192) return (int)t2_ring2_ok<KIND, 64, 192, t2_xg<KIND, 64, 192, 0>(),               \
+                                                       t2_ks<KIND, 64, 192, t2_xg<KIND, 64, 192, 0>()>()>();    \
+    return 0;
+    switch (kind) {
+    case ORKH_I8: ORKH_RING2(ORKH_I8)
+    case ORKH_I4U: ORKH_RING2(ORKH_I4U)
+    case ORKH_F16: ORKH_RING2(ORKH_F16)
+    default: return 0;
+    }
+#undef ORKH_RING2
+}
+
 extern "C" int orkh_tiled2_ring_lds(int kind, int bm, int bn) {
 #define ORKH_RING(KIND)                                                                                      \
     if (bm == 64 && bn == 64) return (int)T2<KIND, 64, 64, t2_ks<KIND, 64, 64>()>::LDS;                       \
@@ -1921,10 +1963,11 @@ extern "C" const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *q) {
         snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d%s", k, q->mt, q->wpg, q->kbw, q->ksplit,
                  q->np == 2 ? "_p2" : q->half ? "_h" : "");
     else if (q->ksplit > 1)
-        snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
-                 q->ksplit, q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");
+        snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d%s%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
+                 q->ksplit, q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "",
+                 q->algo == ORKH_ALGO_TILED2 && q->ring == 2 ? "_r2" : "");
     else
-        snprintf(b, sizeof b, "%s_%s_%dx%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
-                 q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");
+        snprintf(b, sizeof b, "%s_%s_%dx%d%s%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
+                 q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "", q->algo == ORKH_ALGO_TILED2 && q->ring == 2 ? "_r2" : "");
     return b;
 }

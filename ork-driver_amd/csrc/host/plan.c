@@ -306,6 +306,20 @@ static int aline_rule(const ork_npu *c, int rkind, const orkh_plan *q) {
 int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes) {
     const int rc = plan_core(c, rkind, M, K, N, KB, q, ws_bytes);
     if (q->algo == ORKH_ALGO_TILED2) q->aline = aline_rule(c, rkind, q);
+    /* The LDS-ring kernel's two-slot ring (two workgroups per CU, where the kernel has it for the tile) on grids of
+     * more than one round of the CUs: one workgroup's set-up, first stage and epilogue overlap the other's loop.
+     * Measured against the 4-slot ring (graph-timed, us; K=2048 N=6144 unless given): int8 64x192 M=768 22.95 ->
+     * 18.87, M=1024 24.76 -> 21.78; int8 128x128 K=N=4096 M=2048 50.34 -> 45.79, K=N=2048 M=4096 31.6 -> 26.32;
+     * fp16 64x192 M=768 41.16 -> 33.48, 128x128 K=N=2048 M=4096 54.95 -> 45.98; uniform int4 128x128 M=2048
+     * 43.14 -> 33.87. On one round it loses (int8 64x192 M=512 13.38 -> 14.72, 128x128 K=N=4096 M=1024 25.41 ->
+     * 29.11). ORK_RING=0/2 forces either (tests, A/B). */
+    if (q->algo == ORKH_ALGO_TILED2) {
+        const char *fr = knob(c, "ORK_RING");
+        const int cu = (c && c->cores > 0) ? c->cores : 256;
+        const long wgs = (long)cdiv(M, q->bm) * cdiv(N / 16, q->bn / 16) * (q->ksplit > 1 ? q->ksplit : 1);
+        if (fr) q->ring = atoi(fr) == 2 ? 2 : 0;
+        else if (wgs > cu && orkh_tiled2_ring2_ok(rkind, q->bm, q->bn)) q->ring = 2;
+    }
     return rc;
 }
 

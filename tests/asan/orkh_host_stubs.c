@@ -55,4 +55,5 @@ int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *q, int G, const fl
 int orkh_mm_launch_group(const orkh_group *g, int wpg, void *s) { (void)g; (void)wpg; (void)s; return 0; }
 int orkh_mm_launch_tgroup(const orkh_mm *p, int n, const orkh_plan *q, void *s) { (void)p; (void)n; (void)q; (void)s; return 0; }
 int orkh_tiled2_ring_lds(int kind, int bm, int bn) { (void)kind; (void)bm; (void)bn; return 65536; }
+int orkh_tiled2_ring2_ok(int kind, int bm, int bn) { (void)kind; (void)bm; (void)bn; return 0; }
 const char *orkh_mm_variant(const orkh_mm *p, const orkh_plan *q) { (void)p; (void)q; return "stub"; }

@@ -12,6 +12,16 @@ int orkh_tiled2_ring_lds(int kind, int bm, int bn) {
     return 163840;
 }
 
+/* the LDS-ring kernel's two-slot ring: the tiles the kernel builds it for (its LDS arithmetic, restated: int8 and
+ * fp16 on 64 x 192, 128 x 128 and 128 x 96; uniform int4 on 128 x 128 only, its 64 x 192 and 128 x 96 stages being
+ * 41 and 45 KiB; never NF4) */
+int orkh_tiled2_ring2_ok(int kind, int bm, int bn) {
+    const int big = (bm == 128 && (bn == 128 || bn == 96)) || (bm == 64 && bn == 192);
+    if (kind == ORKH_I8 || kind == ORKH_F16) return big;
+    if (kind == ORKH_I4U) return bm == 128 && bn == 128;
+    return 0;
+}
+
 static const char *name(int kind, const orkh_plan *q) {
     static char b[96];
     static const char *kn[] = {"i8", "i4u", "nf4", "f16"};
@@ -22,11 +32,12 @@ static const char *name(int kind, const orkh_plan *q) {
         snprintf(b, sizeof b, "stream_%s_mt%d_w%d_kbw%d_ks%d%s", k, q->mt, q->wpg, q->kbw, q->ksplit,
                  q->np == 2 ? "_p2" : q->half ? "_h" : "");
     else if (q->ksplit > 1)
-        snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
-                 q->ksplit, q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");
+        snprintf(b, sizeof b, "%s_%s_%dx%d_ks%d%s%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
+                 q->ksplit, q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "",
+                 q->algo == ORKH_ALGO_TILED2 && q->ring == 2 ? "_r2" : "");
     else
-        snprintf(b, sizeof b, "%s_%s_%dx%d%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
-                 q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "");
+        snprintf(b, sizeof b, "%s_%s_%dx%d%s%s", q->algo == ORKH_ALGO_TILED2 ? "tiled2" : "tiled", k, q->bm, q->bn,
+                 q->algo == ORKH_ALGO_TILED2 && q->aline ? "_al" : "", q->algo == ORKH_ALGO_TILED2 && q->ring == 2 ? "_r2" : "");
     return b;
 }
 

@@ -508,6 +508,44 @@ def test_run_errors(npu):
     assert L.ork_io_failures() == 0
 
 
+@pytest.mark.parametrize("kind,tile", [("i8", "64x192"), ("i8", "128x128"), ("i8", "128x96"), ("f16", "64x192"),
+                                       ("f16", "128x128"), ("f16", "128x96"), ("i4a8", "128x128"), ("w4a4", "128x128")])
+def test_lds_ring_two_slots(npu, kind, tile):
+    """The LDS-ring kernel's two-slot ring (two workgroups per CU), forced (ORK_RING=2) on every tile it is built
+    for: rows and columns with tails, K tails (one stage, a few, many), a K split, and a grid of several rounds of
+    the CUs (M=1100, N=1536). Exact for the integer kinds, within the fp16 bar for fp16."""
+    _say("lds ring two slots", kind, tile)
+    rng = np.random.default_rng(151 + len(kind) + int(tile.split("x")[1]))
+    for (M, K, N, ks) in [(70, 1056, 224, 1), (300, 160, 224, 1), (130, 2080, 320, 2), (1100, 1056, 1536, 1)]:
+        if kind == "w4a4":
+            N = (N + 63) // 64 * 64
+            B = rng.integers(-8, 8, size=(K, N), dtype=np.int8)
+            A = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+            w, run, ref = npu.pack_i4(B), npu.run_i4, O.gemm_i32(A, B)
+        elif kind == "f16":
+            B = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+            A = rng.standard_normal((M, K)).astype(np.float16)
+            w, run, ref = npu.pack_f16(B), npu.run_f16, O.gemm_f16_f64acc(A, B)
+        elif kind == "i8":
+            B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+            A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            w, run, ref = npu.pack_i8(B), npu.run_i8, O.gemm_i32(A, B)
+        else:
+            W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+            w, _ = npu.pack_i4a8(W)
+            A = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            run, ref = npu.run_i8, O.gemm_i32(A, O.pack_i4a8(W)[2])
+        with _env(ORK_TILE=tile, ORK_RING=2, ORK_KSPLIT=ks):
+            rc, C = run(w, A)
+            name = npu.plan_name(w, M)
+        assert rc == 0 and name.endswith("_r2") and tile in name, name
+        if kind == "f16":
+            assert O.fp16_err(C, ref) <= FP16_TOL, (name, M, K, N)
+        else:
+            assert np.array_equal(C, ref), (name, M, K, N)
+        ork.free(w)
+
+
 @pytest.mark.parametrize("tile", ["256x256", "128x128", "128x96", "64x192", "64x64", "32x64", "32x32", "16x64", "16x32"])
 def test_nf4_ring_short_k(npu, tile):
     """NF4 on every LDS-ring tile with rings of one to three stages (K = 32, 128, 160, 288: one K-block, one, two and

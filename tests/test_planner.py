@@ -69,3 +69,13 @@ def test_stream_half_panels_offered(planner):
     assert got[1].startswith("stream_i8_") and got[1].endswith("_h"), got
     assert not got[2].endswith("_h") and got[3].endswith("_p2"), got
     assert not got[4].endswith("_h") and not got[5].endswith("_h"), got
+
+
+def test_two_slot_ring_picks(planner):
+    """The LDS-ring kernel's two-slot ring: taken on grids of more than one round where the tile has it (int8
+    K=2048 N=6144 M=768 and 1024 on 64 x 192; fp16 K=N=2048 M=4096 and uniform int4 K=2048 N=6144 M=2048 on
+    128 x 128), not on one round (M=512), never on 256 x 256 nor for NF4."""
+    got = planner([(0, 768, 2048, 6144), (0, 1024, 2048, 6144), (3, 4096, 2048, 2048), (1, 2048, 2048, 6144),
+                   (0, 512, 2048, 6144), (0, 4096, 4096, 4096), (2, 1024, 2048, 6144)])
+    assert all(g.endswith("_r2") for g in got[:4]), got
+    assert not any(g.endswith("_r2") for g in got[4:]), got
