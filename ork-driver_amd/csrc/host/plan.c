@@ -316,7 +316,17 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
     if (q->algo == ORKH_ALGO_TILED2) {
         const char *fr = knob(c, "ORK_RING");
         const int cu = (c && c->cores > 0) ? c->cores : 256;
-        const long wgs = (long)cdiv(M, q->bm) * cdiv(N / 16, q->bn / 16) * (q->ksplit > 1 ? q->ksplit : 1);
+        long wgs = (long)cdiv(M, q->bm) * cdiv(N / 16, q->bn / 16) * (q->ksplit > 1 ? q->ksplit : 1);
+        /* uniform int4's 64 x 192 tile has no two-slot form (41 KiB stages): where its grid and 128 x 128's both
+         * exceed one round, 128 x 128 with two slots (us, W4A8 K=2048: N=6144 M=768 21.74 -> 19.96, M=1024 22.61
+         * -> 20.36; N=12288 M=512 22.43 -> 20.06, M=768 32.23 -> 29.71) */
+        const long w128 = (long)cdiv(M, 128) * cdiv(N / 16, 8);
+        if (rkind == ORKH_I4U && !fr && !knob(c, "ORK_TILE") && q->bm == 64 && q->bn == 192 && q->ksplit <= 1 &&
+            wgs > cu && w128 > cu && orkh_tiled2_ring2_ok(rkind, 128, 128)) {
+            q->bm = q->bn = 128;
+            q->aline = aline_rule(c, rkind, q);
+            wgs = w128;
+        }
         if (fr) q->ring = atoi(fr) == 2 ? 2 : 0;
         else if (wgs > cu && orkh_tiled2_ring2_ok(rkind, q->bm, q->bn)) q->ring = 2;
     }

@@ -79,3 +79,7 @@ def test_two_slot_ring_picks(planner):
                    (0, 512, 2048, 6144), (0, 4096, 4096, 4096), (2, 1024, 2048, 6144)])
     assert all(g.endswith("_r2") for g in got[:4]), got
     assert not any(g.endswith("_r2") for g in got[4:]), got
+    # uniform int4, whose 64 x 192 tile has no two-slot form, moves to 128 x 128 with two slots where both grids
+    # exceed one round (K=2048 N=6144 M=768: 21.74 -> 19.96 us), not where 64 x 192 fills one (K=N=4096 M=512)
+    got = planner([(1, 768, 2048, 6144), (1, 512, 4096, 4096)])
+    assert got[0] == "tiled2_i4u_128x128_al_r2" and got[1].startswith("tiled2_i4u_64x192") and "_r2" not in got[1], got
