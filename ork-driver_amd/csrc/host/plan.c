@@ -257,6 +257,10 @@ static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force,
             /* the model underprices several rounds of the K-group tiles (W4A8 M=256 K=2048 N=6144 32x64: 18.2 us
              * measured, 14.3 modelled; int8 M=128 N=6144 32x32: 16.4 vs 12.2), so they are offered for one round */
             if (bm <= 32 && wgs > cu) continue;
+            /* nor split 8 ways: both such picks ran 24-30% above the model (fp16 K=6144 N=2048 M=16 16 x 64: 12.05 us
+             * measured, 9.18 modelled; M=32 32 x 64: 12.03 against 32 x 32 split 4 ways at 11.56), where splits of
+             * up to 4 sit at 0.93-0.98 of it */
+            if (bm <= 32 && ks > 4) continue;
             const double per = (double)((wgs + cu - 1) / cu);
             const double busy = (double)(wgs < cu ? wgs : cu) / cu;
             const double kib = ((double)bm * abpk * kbs + (double)bn / 16 * 1024 * kbs + (double)bm * bn * 4) / 1024;
