@@ -661,6 +661,18 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t vof
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
+// Non-temporal vector stores (global_store_* ... nt). Written as asm because the compiler merges a store that
+// carries the non-temporal hint with an otherwise identical plain store on the other side of a branch, and drops
+// the hint.
+__device__ __forceinline__ void store_nt(int *p, int v) {
+    asm volatile("global_store_dword %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_nt(float *p, float v) {
+    asm volatile("global_store_dword %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_nt4(void *p, v4i v) {
+    asm volatile("global_store_dwordx4 %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
+}
 template <int VM> __device__ __forceinline__ void wait_vmcnt() {
     static_assert(VM >= 0 && VM < 64, "vmcnt");
     __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
@@ -1114,10 +1126,15 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
             c_t *dst = Cb + (size_t)m * ldc + n;
             if (vec) {
                 typedef c_t v4c __attribute__((ext_vector_type(4)));
-                *(v4c *)dst = v4c{finish<KIND>(v[0]), finish<KIND>(v[1]), finish<KIND>(v[2]), finish<KIND>(v[3])};
+                const v4c o = v4c{finish<KIND>(v[0]), finish<KIND>(v[1]), finish<KIND>(v[2]), finish<KIND>(v[3])};
+                if (p.c_nt) store_nt4(dst, __builtin_bit_cast(v4i, o));
+                else *(v4c *)dst = o;
             } else {
 #pragma unroll
-                for (int u = 0; u < 4; u++) dst[u] = finish<KIND>(v[u]);
+                for (int u = 0; u < 4; u++) {
+                    if (p.c_nt) store_nt(&dst[u], finish<KIND>(v[u]));
+                    else dst[u] = finish<KIND>(v[u]);
+                }
             }
         }
         return;
@@ -1161,6 +1178,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                 if (mr0 + i * 16 + r >= p.M) continue;
                 const uint32_t off = (uint32_t)(i * 16 + r) * (uint32_t)ldc + (uint32_t)(jn * 16);
                 if constexpr (GR) Cl[off] = cacc[i][jn][r];
+                else if (p.c_nt) store_nt(&Cl[off], finish<KIND>(acc[i][jn][r]));
                 else Cl[off] = finish<KIND>(acc[i][jn][r]);
             }
         }
@@ -1578,7 +1596,9 @@ int launch_tiled2_r(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
         snprintf(g_lerr, sizeof g_lerr, "tiled2: %ld workgroups", (long)mtiles * ntiles * ksplit);
         return -2;
     }
-    hipLaunchKernelGGL(kern, dim3(mtiles * ntiles * ksplit), dim3(1024), P::LDS, s, *p, mtiles, mtiles * ntiles, kbs,
+    orkh_mm pc = *p;
+    pc.c_nt = q->cnt;
+    hipLaunchKernelGGL(kern, dim3(mtiles * ntiles * ksplit), dim3(1024), P::LDS, s, pc, mtiles, mtiles * ntiles, kbs,
                        q->ws);
     return 0;
 }
