@@ -314,6 +314,14 @@ def sweep_configs(npu, hip, L, ws_c1, dA, dC, codes1, A512, cpu_s, only=None):
         rec("C1 w8a8 K=2048 N=6144", npu.plan_name(ws_c1[0], 16), 16, g, K * N + 16 * K + 4 * 16 * N, 2 * 16 * N * K, "hbm",
             (lambda r: gemm(A512[:r], codes1), gkind, gwhat))
 
+    if only is not None and "m512" in only:
+        # ---- the metric's M=512 GEMM on the headline weights, for profiler runs only (--eager-only passes its
+        # kernel to the counters with no graph or event calls from Python; the bench line's m512 entry times it in
+        # a graph)
+        g, _ = measure(npu, hip, ws_c1, 512, dA, dC, 480, 48)
+        rec("int8 GEMM M=512 K=2048 N=6144", npu.plan_name(ws_c1[0], 512), 512, g, K * N + 512 * K + 4 * 512 * N,
+            2 * 512 * N * K, "mfma_int8")
+
     if want("shard"):
         # ---- one GPU's share of config 1 split 8 ways over N (output channels), the natural split of the path
         # across GPUs: K=2048, N=768, M=1 and 16. 336 rotated copies of the 1.57 MB share (528 MB > 2x the MALL).
@@ -711,7 +719,8 @@ def main():
                          "config sweep's sections named by --configs)")
     ap.add_argument("--configs", default="c1,shard,c2,c3,c4,grouped",
                     help="with --only configs: comma-separated sections of the config sweep (c1 shard c2 c3 c4 "
-                         "grouped; shard = one GPU's share of config 1 split 8 ways over N)")
+                         "grouped; shard = one GPU's share of config 1 split 8 ways over N; m512, only when named: "
+                         "the M=512 int8 GEMM of the bench line, for profiler runs)")
     ap.add_argument("--eager-only", action="store_true",
                     help="profiling: time eager launches by the host clock only (no graphs, events or HIP calls "
                          "from Python); with --only configs")

@@ -107,7 +107,7 @@ typedef struct orkh_mm {
     void *C;
     int ldc;
     uint32_t lut[4];      /* ORKH_NF4 codebook, entry e in byte e%4 of lut[e/4] */
-    int c_nt;             /* k_tiled2: 1 = store C with non-temporal stores (set by the launcher from plan.cnt) */
+    int c_wt;             /* k_tiled2: 1 = store C with write-through stores (set by the launcher from plan.cwt) */
 } orkh_mm;
 
 /* Launch plan chosen by the host planner (ork-driver_amd/csrc/host/plan.c). */
@@ -124,8 +124,8 @@ typedef struct orkh_plan {
     int aline;
     /* TILED2: 2 = a two-slot ring (two workgroups per CU on the tiles whose 4-slot ring fills one), else 0 */
     int ring;
-    /* TILED2: 1 = non-temporal C stores (a grid of one round of the CUs), else write-back */
-    int cnt;
+    /* TILED2: 1 = write-through C stores, else write-back */
+    int cwt;
     /* STREAM: np = 2 pairs panels: npg workgroups, the first N/16 - npg owning two adjacent panels each */
     int np, npg;
     /* GEMV and STREAM: 1 = half a panel (8 columns) per workgroup, grid (N/8, ksplit) (k_gemv_half, k_stream's

@@ -661,17 +661,18 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t vof
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
-// Non-temporal vector stores (global_store_* ... nt). Written as asm because the compiler merges a store that
-// carries the non-temporal hint with an otherwise identical plain store on the other side of a branch, and drops
-// the hint.
-__device__ __forceinline__ void store_nt(int *p, int v) {
-    asm volatile("global_store_dword %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
+// Write-through vector stores at device scope (global_store_* ... sc1): the L2 passes the data on to memory as it
+// comes instead of holding it dirty until the end of the kernel. Written as asm because the compiler merges a store
+// that carries a cache-policy modifier with an otherwise identical plain store on the other side of a branch, and
+// drops the modifier.
+__device__ __forceinline__ void store_wt(int *p, int v) {
+    asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
-__device__ __forceinline__ void store_nt(float *p, float v) {
-    asm volatile("global_store_dword %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
+__device__ __forceinline__ void store_wt(float *p, float v) {
+    asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
-__device__ __forceinline__ void store_nt4(void *p, v4i v) {
-    asm volatile("global_store_dwordx4 %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
+__device__ __forceinline__ void store_wt4(void *p, v4i v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
 template <int VM> __device__ __forceinline__ void wait_vmcnt() {
     static_assert(VM >= 0 && VM < 64, "vmcnt");
@@ -1127,12 +1128,12 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
             if (vec) {
                 typedef c_t v4c __attribute__((ext_vector_type(4)));
                 const v4c o = v4c{finish<KIND>(v[0]), finish<KIND>(v[1]), finish<KIND>(v[2]), finish<KIND>(v[3])};
-                if (p.c_nt) store_nt4(dst, __builtin_bit_cast(v4i, o));
+                if (p.c_wt) store_wt4(dst, __builtin_bit_cast(v4i, o));
                 else *(v4c *)dst = o;
             } else {
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    if (p.c_nt) store_nt(&dst[u], finish<KIND>(v[u]));
+                    if (p.c_wt) store_wt(&dst[u], finish<KIND>(v[u]));
                     else dst[u] = finish<KIND>(v[u]);
                 }
             }
@@ -1177,8 +1178,10 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
             for (int r = 0; r < 4; r++) {
                 if (mr0 + i * 16 + r >= p.M) continue;
                 const uint32_t off = (uint32_t)(i * 16 + r) * (uint32_t)ldc + (uint32_t)(jn * 16);
-                if constexpr (GR) Cl[off] = cacc[i][jn][r];
-                else if (p.c_nt) store_nt(&Cl[off], finish<KIND>(acc[i][jn][r]));
+                if constexpr (GR) {
+                    if (p.c_wt) store_wt(&Cl[off], cacc[i][jn][r]);
+                    else Cl[off] = cacc[i][jn][r];
+                } else if (p.c_wt) store_wt(&Cl[off], finish<KIND>(acc[i][jn][r]));
                 else Cl[off] = finish<KIND>(acc[i][jn][r]);
             }
         }
@@ -1597,7 +1600,7 @@ int launch_tiled2_r(const orkh_mm *p, const orkh_plan *q, hipStream_t s) {
         return -2;
     }
     orkh_mm pc = *p;
-    pc.c_nt = q->cnt;
+    pc.c_wt = q->cwt;
     hipLaunchKernelGGL(kern, dim3(mtiles * ntiles * ksplit), dim3(1024), P::LDS, s, pc, mtiles, mtiles * ntiles, kbs,
                        q->ws);
     return 0;
@@ -1949,6 +1952,7 @@ extern "C" int orkh_mm_launch_grouped(const orkh_mm *p, const orkh_plan *q, int 
         orkh_mm pc = *p;
         pc.C = C;
         pc.ldc = ldc;
+        pc.c_wt = q->cwt;
         const T2Group gp = {G, aS, bS};
         const int rc = p->kind == ORKH_I8 ? launch_tiled2g<ORKH_I8>(&pc, q, gp, s) : launch_tiled2g<ORKH_I4U>(&pc, q, gp, s);
         if (rc) return rc;

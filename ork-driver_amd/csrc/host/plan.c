@@ -333,16 +333,16 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
         }
         if (fr) q->ring = atoi(fr) == 2 ? 2 : 0;
         else if (wgs > cu && orkh_tiled2_ring2_ok(rkind, q->bm, q->bn)) q->ring = 2;
-        /* C stored non-temporally by the 64-row tiles where the grid is one round: every workgroup stores at about the
-         * same time, after all the loads, and the stores write through instead of leaving 4-13 MB of C dirty in the
-         * L2s for the end of the kernel. Measured against write-back stores (graph-timed, us): int8 M=512 K=2048
-         * N=6144 64 x 192 14.19 -> 13.82, W4A4 M=256 K=N=4096 64 x 64 12.54 -> 12.36, fp16 M=512 K=N=2048 64 x 64
-         * 12.87 -> 12.76. Not on the others: 256 x 256 at M=K=N=4096 (one round, 64 MB of C) 67.83 -> 72.97, int8
-         * M=128 K=N=2048 32 x 32 5.60 -> 5.67, W4A8 M=64 32 x 64 within 0.3%; nor on grids of several rounds, where
-         * they compete with the later workgroups' loads (int8 M=1024 two-slot 22.67 -> 24.90). ORK_CNT=0/1 forces
-         * either. */
-        const char *fc = knob(c, "ORK_CNT");
-        q->cnt = fc ? atoi(fc) != 0 : (wgs <= cu && q->bm == 64);
+        /* C stored write-through (device scope) where the grid is one round of the CUs: every workgroup stores at
+         * about the same time, after all the loads, and the L2s pass C on to memory as it comes instead of holding
+         * up to 64 MB of it dirty for the end of the kernel. Graph-timed against write-back stores (us): int8 K=2048
+         * N=6144 M=512 64 x 192 14.56 -> 13.45, M=256 12.89 -> 12.52; uniform int4 M=512 64 x 192 13.96 -> 12.60;
+         * W4A4 K=N=4096 M=256 64 x 64 12.55 -> 12.21; fp16 K=N=2048 M=512 64 x 64 13.00 -> 12.65; int8 M=K=N=4096
+         * 256 x 256 67.72 -> 66.35; int8 K=N=2048 M=128 32 x 32 5.66 -> 5.57; W4A8 M=64 32 x 64 6.25 -> 6.06. On
+         * grids of several rounds the early writes compete with the later workgroups' loads: int8 M=1024 two-slot
+         * 23.37 -> 25.80, fp16 M=768 32.84 -> 36.11. ORK_CWT=0/1 forces either. */
+        const char *fc = knob(c, "ORK_CWT");
+        q->cwt = fc ? atoi(fc) != 0 : wgs <= cu;
     }
     return rc;
 }
@@ -492,6 +492,9 @@ void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB,
             if (ring > 0 && ring + sc <= 163840) {
                 q->ksplit = 1;
                 q->kbs = KB;
+                /* write-through C stores on a grid of one round, as for the plain runs */
+                const char *fc = knob(c, "ORK_CWT");
+                q->cwt = fc ? atoi(fc) != 0 : (long)cdiv(M, q->bm) * cdiv(N / 16, q->bn / 16) <= cu;
                 return;
             }
             if (q->bm == 64 && q->bn == 64) break;

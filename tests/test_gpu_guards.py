@@ -138,9 +138,9 @@ CASES = [
     ("i8", 200, 1024, 4128, {"ORK_TILE": "128x128"}, "128x128"),
     ("i8", 300, 1024, 544, {"ORK_TILE": "256x256"}, "256x256"),
     ("i8", 1100, 1056, 3072, {"ORK_TILE": "64x192"}, "64x192_al_r2"),
-    ("i8", 300, 1024, 4128, {"ORK_TILE": "64x192", "ORK_CNT": 1}, "64x192"),
-    ("f16", 130, 1024, 80, {"ORK_TILE": "64x64", "ORK_CNT": 1}, "tiled2_f16_64x64"),
-    ("w4a4", 150, 1024, 320, {"ORK_TILE": "64x64", "ORK_CNT": 1}, "tiled2_i4u_64x64"),
+    ("i8", 300, 1024, 4128, {"ORK_TILE": "64x192", "ORK_CWT": 0}, "64x192"),
+    ("f16", 130, 1024, 80, {"ORK_TILE": "64x64", "ORK_CWT": 0}, "tiled2_f16_64x64"),
+    ("w4a4", 150, 1024, 320, {"ORK_TILE": "64x64", "ORK_CWT": 0}, "tiled2_i4u_64x64"),
     ("f16", 300, 1024, 544, {"ORK_TILE": "128x128", "ORK_RING": 2}, "128x128_al_r2"),
     ("i8", 70, 2048, 96, {"ORK_TILE": "64x64", "ORK_KSPLIT": 4}, "64x64_ks4"),
     ("i8", 40, 2048, 96, {"ORK_TILE": "32x64"}, "32x64"),
