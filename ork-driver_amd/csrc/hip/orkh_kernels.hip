@@ -655,9 +655,12 @@ __global__ __launch_bounds__(256) void k_grouped(orkh_mm p, int G, const float *
 // clobber of that reserved register is safe and its warning is silenced here.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
+// SITE only numbers the call site in an asm comment: identical asm at several sites lets the compiler merge them
+// through a phi it may place in a VGPR, which the "s" operand cannot take.
+template <int SITE = 0>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_byte), "v"(voff),
-                 "s"(r)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds ; site %3" ::"s"(lds_byte),
+                 "v"(voff), "s"(r), "i"(SITE)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -734,6 +737,26 @@ template <int KIND, int BM, int BN, int GR> constexpr int t2_xg() {
     if (KIND == ORKH_I4U && BM == 64 && BN == 192) return 1;
     if (KIND == ORKH_I4U && BM == 64 && BN == 64) return 2;
     return 0;
+}
+
+// Where in a stage the waves of the LDS-ring kernel issue the loads of the stage R - 1 ahead: before K-block t2_issue_at
+// of their stage work (0: right after the stage's barrier; KPW: after their last K-block). Every wave still issues each
+// stage once, in stage order, inside the iteration, so the waits count as before. Issuing right after the barrier
+// holds every wave of a SIMD on the issue of loads into a full memory pipeline at once with no MFMA ready behind
+// them; later, the MFMAs of the waves not held go on. Graph-timed against right after the barrier (one build each,
+// alternated twice on one box; int8 and fp16 through bench.py's config section too; exact): int8 64 x 192 M=512
+// K=2048 N=6144 13.56-13.68 -> 13.15-13.28 us (after the first of two K-blocks; after both: -0.4 to -0.9%); NF4
+// 128 x 128 M=512 16.62 -> 15.46 (after its one K-block); grouped W4A4 K=N=4096 G=128 64 x 64 M=256 18.33 -> 17.08
+// (after the first of four); uniform int4 64 x 192 W4A4 M=512 18.54 -> 17.95, W4A8 M=512 12.67 -> 12.54, 32 x 64
+// W4A8 M=64 6.03 -> 5.94 (after their one); int8 32 x 64 (four chained M=256 runs) 13.92 -> 13.32-13.80. No gain, so
+// right after the barrier: fp16 64 x 64 M=512 (-0.3 to +0.6% either way), uniform int4 on the 2 x 2 x 4 wave grid
+// (64 x 64, W4A4 M=256: +0.4 to +0.8%) and NF4 on the K-group tiles (its decode runs a stage ahead; -0.1 to -0.6%);
+// the two-slot rings, whose second workgroup per CU already overlaps one's loads with the other's MFMAs, keep it too.
+template <int KIND, int BM, int BN, class P> constexpr int t2_issue_at() {
+    if (P::R <= 2 || (KIND == ORKH_NF4 && P::WK > 1) || (KIND == ORKH_F16 && BM == 64 && BN == 64) ||
+        (KIND == ORKH_I4U && BM == 64 && BN == 64 && P::WK > 1)) // the 2 x 2 x 4 grid; grouped runs keep 4 x 4
+        return 0;
+    return 1;
 }
 
 // Index (in 16-byte units) within a stage's A image of lane `lane`'s operand of fragment (mb, kbl, st).
@@ -837,7 +860,8 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         }
     }
     const int nst = (kb_hi - kb_lo + KS - 1) / KS;
-    auto issue = [&](int st) {
+    auto issue = [&](int st, auto site) { // site: std::integral_constant numbering the call site (lds_dma16)
+        constexpr int SA = 2 * decltype(site)::value, SB = SA + 1;
         const uint32_t slot = lds0 + (uint32_t)(st % R) * P::SLOT;
         const int kb0 = kb_lo + st * KS;
 #pragma unroll
@@ -845,11 +869,11 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
             const int i = wv + q * P::NW;
             if (i < P::NIA) {
                 const int k = kb0 * T::KPB + kof[q];
-                lds_dma16(Ar, (voff[q] != OOB && k < k_hi) ? voff[q] + (uint32_t)kb0 * T::KPB * T::ESZ : OOB,
+                lds_dma16<SA>(Ar, (voff[q] != OOB && k < k_hi) ? voff[q] + (uint32_t)kb0 * T::KPB * T::ESZ : OOB,
                           slot + i * 1024);
             } else {
                 const int kb = kb0 + kof[q];
-                lds_dma16(Br, (i < P::NI && voff[q] != OOB && kb < kb_hi) ? voff[q] + (uint32_t)kb * 1024u : OOB,
+                lds_dma16<SB>(Br, (i < P::NI && voff[q] != OOB && kb < kb_hi) ? voff[q] + (uint32_t)kb * 1024u : OOB,
                           slot + (i < P::NI ? i : P::NI) * 1024);
             }
         }
@@ -910,11 +934,11 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         const __amdgpu_buffer_rsrc_t Sb = make_rsrc(gp.bS, (uint32_t)Sk * p.N * 4u);
         for (int i = wv; i < sca_kib + scb_kib; i += P::NW) {
             if (i < sca_kib) {
-                lds_dma16(Sa, (uint32_t)m0 * Sk * 4u + (uint32_t)i * 1024u + lane * 16u, scl + i * 1024);
+                lds_dma16<8>(Sa, (uint32_t)m0 * Sk * 4u + (uint32_t)i * 1024u + lane * 16u, scl + i * 1024);
             } else {
                 const int f = (i - sca_kib) * 256 + lane * 4; // first float of this lane within the Sk x BN tile
                 const int g = f / BN, c = f - g * BN;
-                lds_dma16(Sb, g < Sk ? ((uint32_t)g * p.N + nb0 * 16 + c) * 4u : OOB, scl + i * 1024);
+                lds_dma16<9>(Sb, g < Sk ? ((uint32_t)g * p.N + nb0 * 16 + c) * 4u : OOB, scl + i * 1024);
             }
         }
     }
@@ -976,8 +1000,11 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         }
     };
 
+    // where in a stage the waves issue the loads of the stage R - 1 ahead (t2_issue_at; grouped runs whose groups
+    // close inside K-blocks walk the stage in another loop: right after the barrier)
+    constexpr int IA = GR == 1 ? 0 : t2_issue_at<KIND, BM, BN, P>() < P::KPW ? t2_issue_at<KIND, BM, BN, P>() : P::KPW;
 #pragma unroll
-    for (int st = 0; st < R - 1; st++) issue(st);
+    for (int st = 0; st < R - 1; st++) issue(st, std::integral_constant<int, 0>{});
     if constexpr (PIPE) {
         if (nst > 0) {
             wait_vmcnt<(R - 2) * P::IPW>(); // stage 0 (every wave's share: the barrier below)
@@ -992,7 +1019,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         __syncthreads();
         // into the slot of stage s - 1, which every wave finished before the barrier (NF4: its blocks were decoded
         // in iteration s - 2)
-        issue(s + R - 1);
+        if constexpr (IA == 0) issue(s + R - 1, std::integral_constant<int, 1>{});
         const v4i *As = sm + (s % R) * (P::SLOT / 16);
         const v4i *Bs = As + P::NIA * 64;
         if constexpr (GR) {
@@ -1009,6 +1036,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         if constexpr (GR != 1) {
 #pragma unroll
             for (int kk = 0; kk < P::KPW; kk++) {
+                if (kk > 0 && kk == IA) issue(s + R - 1, std::integral_constant<int, 2>{});
                 const int kbl = wk * P::KPW + kk; // this wave's K-blocks of the stage
                 v4i op[P::NTW][T::STEPS];
 #pragma unroll
@@ -1038,6 +1066,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                     }
                 }
             }
+            if constexpr (IA > 0 && IA == P::KPW) issue(s + R - 1, std::integral_constant<int, 3>{});
         }
         if constexpr (PIPE && !EARLY) {
             if (s + 1 < nst) decode_stage(s + 1);
