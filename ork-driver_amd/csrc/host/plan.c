@@ -168,24 +168,27 @@ static double stream_us(const ork_npu *c, int rkind, int M, int N, int KB, int c
 }
 
 /* NF4 above one row. Its codebook decode shifts each kernel's balance of operand delivery and VALU work differently
- * per tile, so every candidate has its own least-squares fit (relative error) to graph-timed launches on MI355X:
- * 45 shapes (K x N = 2048 x 6144, 6144 x 2048, 4096 x 4096, 2048 x 2048, 2048 x 12288; M = 32..1024), 896
- * kernel / tile / split candidates in all (tests/golden/nf4_plan_sweep.json),
+ * per tile, so every candidate has its own least-squares fit (relative error, non-negative terms) to graph-timed
+ * launches on MI355X: 45 shapes (K x N = 2048 x 6144, 6144 x 2048, 4096 x 4096, 2048 x 2048, 2048 x 12288;
+ * M = 32..1024), 1007 kernel / tile / split candidates in all (tests/golden/nf4_plan_sweep.json),
  *   t = a + rounds * (b + c * KiB) + [ks > 1] (d + e * ks * M * N * 4 / 1e6)   us,
  * KiB being the A and B bytes one workgroup loads (the streaming kernel: the form of stream_us). The fits are
- * within 3-7% rms per candidate; over the 45 shapes the picks total 627 us against 621 for the fastest timed
- * candidate of each (the row-count rules they replaced totalled 687 on the kernels of the time, against 633 for
- * the fastest: e.g. K=6144 N=2048 M=64 15.6 -> 10.9 us, K=2048 N=12288 M=64 14.9 -> 10.2, K=N=2048 M=192 9.8 -> 8.0). */
+ * within 4-7% rms per candidate; over the 45 shapes the picks total within 0.6% of the fastest timed candidate of
+ * each. Refitted after the LDS-ring kernel's stage loads moved behind the first K-block of stage work (128 x 128
+ * and 64 x 64 ran 2-7% faster) and with its 128 x 96 tile offered: the earlier fits, without it, totalled 2.2%
+ * above the fastest on the same launches (K=4096 N=4096 M=384 24.1 us against 22.8 on 128 x 96, K=2048 N=6144
+ * M=128 10.0 on k_tiled against 9.5 on the LDS ring's 64 x 64). */
 static const struct nf4_fit {
     int algo, bm, bn, ksmax;
     double a, b, c, d, e;
 } nf4_fits[] = {
-    {ORKH_ALGO_TILED2, 128, 128, 4, 4.3479, 0.0, 0.0301, 2.3639, 0.4989},
-    {ORKH_ALGO_TILED2, 64, 64, 4, 4.5624, 0.0, 0.0290, 1.8830, 0.5202},
-    {ORKH_ALGO_TILED2, 32, 64, 4, 1.3497, 2.0597, 0.0297, 2.7524, 0.4021},
-    {ORKH_ALGO_TILED, 128, 128, 8, 5.4417, 3.5824, 0.0342, 2.9230, 0.4990},
-    {ORKH_ALGO_TILED, 128, 96, 8, 3.8645, 3.9671, 0.0295, 2.9059, 0.4594},
-    {ORKH_ALGO_TILED, 64, 64, 8, 3.5684, 1.4132, 0.0256, 2.7887, 0.4122},
+    {ORKH_ALGO_TILED2, 128, 128, 4, 4.1310, 0.6805, 0.0272, 1.7563, 0.4771},
+    {ORKH_ALGO_TILED2, 128, 96, 4, 2.4251, 2.0721, 0.0268, 2.2542, 0.5308},
+    {ORKH_ALGO_TILED2, 64, 64, 4, 3.9420, 0.0000, 0.0287, 2.0167, 0.5399},
+    {ORKH_ALGO_TILED2, 32, 64, 4, 1.0803, 2.1819, 0.0297, 2.6830, 0.3840},
+    {ORKH_ALGO_TILED, 128, 128, 8, 5.3951, 3.6657, 0.0342, 2.9489, 0.4949},
+    {ORKH_ALGO_TILED, 128, 96, 8, 3.8782, 3.9816, 0.0295, 2.9108, 0.4612},
+    {ORKH_ALGO_TILED, 64, 64, 8, 3.5590, 1.4223, 0.0257, 2.7922, 0.4108},
 };
 
 static void nf4_best(const ork_npu *c, int M, int N, int KB, int cu, orkh_plan *q) {

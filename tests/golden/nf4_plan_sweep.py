@@ -19,7 +19,7 @@ SHAPES = {(2048, 6144): (32, 48, 64, 96, 128, 192, 256, 384, 512, 1024),
           (2048, 12288): (32, 64, 96, 128, 192, 256, 512)}
 PLANS = [{}] + [{"ORK_PLAN": "stream", "ORK_KSPLIT": k} for k in (1, 2, 4)] \
     + [{"ORK_PLAN": "tiled", "ORK_TILE": t, "ORK_KSPLIT": k} for t in ("64x64", "128x96", "128x128") for k in (1, 2, 4, 8)] \
-    + [{"ORK_TILE": t, "ORK_KSPLIT": k} for t in ("32x64", "64x64", "128x128") for k in (1, 2, 4)]
+    + [{"ORK_TILE": t, "ORK_KSPLIT": k} for t in ("32x64", "64x64", "128x96", "128x128") for k in (1, 2, 4)]
 
 
 def sweep():
