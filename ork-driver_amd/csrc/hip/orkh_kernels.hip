@@ -759,6 +759,23 @@ template <int KIND, int BM, int BN, class P> constexpr int t2_issue_at() {
     return 1;
 }
 
+// How many of the 16 waves issue a stage's loads (the others only compute: they never wait on the issue of a load
+// into a full memory pipeline, so the matrix cores keep them). Wave wv < LW issues loads wv, wv + LW, ...; the
+// stage's load count must divide evenly. Graph-timed against every wave issuing (one build each, alternated twice
+// on one box; exact): 8 loader waves on uniform int4's 64 x 192 tile (2 x 4 x 2 grid): W4A4 K=N=4096 M=512 18.04 ->
+// 16.80 us, W4A8 K=2048 N=6144 M=512 12.23 -> 11.70, M=256 12.07 -> 11.45; 4 on the NF4 K-group tiles (32 x 64, C3
+// NF4 M=64 7.36 -> 6.98) and on 256 x 256 (M=K=N=4096 int8 67.1 -> 65.6, fp16 134.3 -> 126.0). Elsewhere no gain
+// (int8 64 x 192 M=512: 8 loaders -0.2 to -0.8%, 4 +2.6 to +3.0%; two-slot rings +4 to +9%; uniform int4 32 x 64 with
+// 8: +3.5%), so every wave issues.
+template <int KIND, int BM, int BN, class P> constexpr int t2_loaders() {
+    int lw = P::NW;
+    if (P::R <= 2) return lw;
+    if (KIND == ORKH_I4U && BM == 64 && BN == 192) lw = 8;
+    else if (KIND == ORKH_NF4 && P::WK > 1) lw = 4;
+    else if ((KIND == ORKH_I8 || KIND == ORKH_F16) && BM == 256 && BN == 256) lw = 4;
+    return P::NI % lw == 0 ? lw : P::NW;
+}
+
 // Index (in 16-byte units) within a stage's A image of lane `lane`'s operand of fragment (mb, kbl, st).
 // Fragment order: fragment f = (mb, kbl, st) is 1 KiB at f, lane-major, as mma() takes it.
 // Line order: 8-row groups of 1 KiB; row r's 128-byte line holds its 16-byte chunk c at slot
@@ -833,12 +850,17 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)sm;
     const Lut L = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
 
-    // this wave's loads: i = wv + q * NW; A fragment (mb, kbl, step) or B block (nbl, kbl)
-    uint32_t voff[P::IPW];
-    int kof[P::IPW];
+    // this wave's loads: i = wv + q * LW (waves wv >= LW issue none; grouped runs: every wave); A fragment (mb, kbl,
+    // step) or B block (nbl, kbl)
+    constexpr int LW = GR == 0 ? t2_loaders<KIND, BM, BN, P>() : P::NW;
+    constexpr int IPW = LW == P::NW ? P::IPW : P::NI / LW;
+    static_assert(LW == P::NW || P::NI % LW == 0, "loader waves");
+    static_assert((R - 2) * IPW < 64, "vmcnt");
+    uint32_t voff[IPW];
+    int kof[IPW];
 #pragma unroll
-    for (int q = 0; q < P::IPW; q++) {
-        const int i = wv + q * P::NW;
+    for (int q = 0; q < IPW; q++) {
+        const int i = wv + q * LW;
         voff[q] = OOB;
         kof[q] = 0;
         if (i < P::NIA && LINE) {
@@ -864,9 +886,10 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         constexpr int SA = 2 * decltype(site)::value, SB = SA + 1;
         const uint32_t slot = lds0 + (uint32_t)(st % R) * P::SLOT;
         const int kb0 = kb_lo + st * KS;
+        if (LW < P::NW && wv >= LW) return;
 #pragma unroll
-        for (int q = 0; q < P::IPW; q++) {
-            const int i = wv + q * P::NW;
+        for (int q = 0; q < IPW; q++) {
+            const int i = wv + q * LW;
             if (i < P::NIA) {
                 const int k = kb0 * T::KPB + kof[q];
                 lds_dma16<SA>(Ar, (voff[q] != OOB && k < k_hi) ? voff[q] + (uint32_t)kb0 * T::KPB * T::ESZ : OOB,
@@ -1007,7 +1030,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     for (int st = 0; st < R - 1; st++) issue(st, std::integral_constant<int, 0>{});
     if constexpr (PIPE) {
         if (nst > 0) {
-            wait_vmcnt<(R - 2) * P::IPW>(); // stage 0 (every wave's share: the barrier below)
+            wait_vmcnt<(R - 2) * IPW>(); // stage 0 (every wave's share: the barrier below)
             __syncthreads();
             decode_stage(0);
         }
@@ -1015,7 +1038,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
     for (int s = 0; s < nst; s++) {
         // stage s has landed (NF4: stage s + 1, whose blocks this iteration decodes); the barrier also publishes
         // the decode of stage s
-        wait_vmcnt<(PIPE ? R - 3 : R - 2) * P::IPW>();
+        wait_vmcnt<(PIPE ? R - 3 : R - 2) * IPW>();
         __syncthreads();
         // into the slot of stage s - 1, which every wave finished before the barrier (NF4: its blocks were decoded
         // in iteration s - 2)
