@@ -721,14 +721,15 @@ template <int KIND, int BM, int BN, int KS, int XG = 0, int RC = 0> struct T2 {
     static constexpr int R = RC ? RC : ((163840 - DEC) / SLOT) < RMAX ? ((163840 - DEC) / SLOT) : RMAX;
     static constexpr size_t LDS = (size_t)R * SLOT + DEC;
     static constexpr size_t RED = (size_t)(WK - 1) * WM * WN * MTW * NTW * 1024; // K-group partial tiles
-    // A stage whose rows are one 128-byte line each is loaded a line at a time (8 rows x 128 B per instruction)
-    // instead of in MFMA fragment order (16 rows x 64 B: every line fetched by two instructions), and read from
-    // a swizzled image (a_lds)
-    static constexpr bool LINE_OK = KS * T::KPB * T::ESZ == 128;
+    // A stage whose rows are whole 128-byte lines (ALN of them a row: 1, 2 or 4) is loaded a line at a time (8 rows
+    // x 128 B per instruction) instead of in MFMA fragment order (16 rows x 64 B: every line fetched by two
+    // instructions), and read from a swizzled image (a_lds)
+    static constexpr int ALN = KS * T::KPB * T::ESZ / 128;
+    static constexpr bool LINE_OK = KS * T::KPB * T::ESZ % 128 == 0;
     static_assert(MB % WM == 0 && NB % WN == 0 && WM * WN * WK == NW && KS % WK == 0 && R >= 2 && (R - 2) * IPW < 64,
                   "tile");
     static_assert(RED <= (size_t)R * SLOT, "K-group partials must fit the ring");
-    static_assert(!LINE_OK || NIA * 8 == BM, "line-loaded A: one instruction per 8 rows");
+    static_assert(!LINE_OK || NIA * 8 == BM * ALN, "line-loaded A: one instruction per 8 row lines");
 };
 
 // Wave grids other than 4 x 4 (grouped runs always keep it):
@@ -785,17 +786,18 @@ template <int KIND, int BM, int BN, class P> constexpr int t2_loaders() {
 
 // Index (in 16-byte units) within a stage's A image of lane `lane`'s operand of fragment (mb, kbl, st).
 // Fragment order: fragment f = (mb, kbl, st) is 1 KiB at f, lane-major, as mma() takes it.
-// Line order: 8-row groups of 1 KiB; row r's 128-byte line holds its 16-byte chunk c at slot
-// c ^ (r & 7) ^ ((r >> 3) & 1). The swizzle puts the chunks that any 16 consecutive lanes of a fragment read
-// (16 rows, one chunk) in 16 distinct bank groups, so the 128-bit LDS reads stay conflict-free; the loads
-// write each instruction's 8 lines with the same permutation (lane l of instruction j: row 8j + l/8, slot l % 8).
-template <int KIND, int KS, bool LINE>
+// Line order: 1 KiB per (line li of the stage row, 8-row group g8), at li * BM8 + g8 (BM8 = the tile's 8-row
+// groups); row r's 128-byte line li holds its 16-byte chunk c at slot c ^ (r & 7) ^ ((r >> 3) & 1). The swizzle
+// puts the chunks that any 16 consecutive lanes of a fragment read (16 rows, one chunk) in 16 distinct bank
+// groups, so the 128-bit LDS reads stay conflict-free; the loads write each instruction's 8 lines with the same
+// permutation (lane l of instruction li * BM8 + g8: row 8 g8 + l/8, slot l % 8).
+template <int KIND, int KS, bool LINE, int BM8>
 __device__ __forceinline__ int a_lds(int mb, int kbl, int st, int lane) {
     using T = KT<KIND>;
     if constexpr (LINE) {
-        const int c = (kbl * T::KPB + a_koff<KIND>(st, lane >> 4)) * T::ESZ / 16;
+        const int c = (kbl * T::KPB + a_koff<KIND>(st, lane >> 4)) * T::ESZ / 16; // chunk within the stage row
         const int r7 = lane & 7, h = (lane >> 3) & 1;
-        return (mb * 2 + h) * 64 + r7 * 8 + (c ^ r7 ^ h);
+        return ((c >> 3) * BM8 + mb * 2 + h) * 64 + r7 * 8 + ((c & 7) ^ r7 ^ h);
     } else {
         return ((mb * KS + kbl) * T::STEPS + st) * 64 + lane;
     }
@@ -879,10 +881,11 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
         voff[q] = OOB;
         kof[q] = 0;
         if (i < P::NIA && LINE) {
-            // rows 8i .. 8i+7, each a whole 128-byte line; lane l fills slot l % 8 of row 8i + l / 8
+            // line li of rows 8 g8 .. 8 g8 + 7 (i = li * BM / 8 + g8); lane l fills slot l % 8 of row 8 g8 + l / 8
+            const int li = i / (BM / 8), g8 = i % (BM / 8);
             const int rr = lane >> 3, slot = lane & 7;
-            const int row = m0 + i * 8 + rr;
-            kof[q] = (slot ^ rr ^ (i & 1)) * 16 / T::ESZ;
+            const int row = m0 + g8 * 8 + rr;
+            kof[q] = (li * 128 + (slot ^ rr ^ (g8 & 1)) * 16) / T::ESZ;
             if (row < p.M) voff[q] = (uint32_t)row * lda_b + (uint32_t)kof[q] * T::ESZ;
         } else if (i < P::NIA) {
             const int mb = i / (KS * T::STEPS), rest = i % (KS * T::STEPS);
@@ -1091,7 +1094,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                 for (int st = 0; st < T::STEPS; st++)
 #pragma unroll
                     for (int i = 0; i < P::MTW; i++) {
-                        const v4i a = As[a_lds<KIND, KS, LINE>(wm * P::MTW + i, kbl, st, lane)];
+                        const v4i a = As[a_lds<KIND, KS, LINE, BM / 8>(wm * P::MTW + i, kbl, st, lane)];
 #pragma unroll
                         for (int jn = 0; jn < P::NTW; jn++) acc[i][jn] = mma(a, op[jn][st], acc[i][jn]);
                     }
@@ -1122,7 +1125,7 @@ __device__ __forceinline__ void tiled2_body(const orkh_mm &p, int mtiles, int nt
                 for (int st = 0; st < T::STEPS; st++)
 #pragma unroll
                     for (int i = 0; i < P::MTW; i++)
-                        afr[kbl][st][i] = As[a_lds<KIND, KS, LINE>(wm * P::MTW + i, kbl, st, lane)];
+                        afr[kbl][st][i] = As[a_lds<KIND, KS, LINE, BM / 8>(wm * P::MTW + i, kbl, st, lane)];
             }
 #pragma unroll
             for (int kbl = 0; kbl < KS; kbl++) {

@@ -285,16 +285,26 @@ static double tiled2_best(int rkind, int M, int N, int KB, int cu, int ks_force,
 
 static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes);
 
-/* A-stage layout of the LDS-ring kernel: whole 128-byte row lines (swizzled LDS image) or MFMA fragment
- * order. Measured on MI355X, graph-timed, both layouts in one run (us, fragment -> line):
- *   int8 K=2048 N=6144: M=512 64x192 14.9 -> 14.5, 128x128 15.5 -> 14.5; M=1024 64x192 27.4 -> 26.6,
- *                       128x128 29.4 -> 27.7; M=256 64x192 13.1 -> 12.6; M=128 64x64 8.54 -> 8.63
- *   fp16 K=N=2048:      M=512 64x64 13.1 -> 13.3, 128x128 23.7 -> 21.7, 64x192 21.1 -> 20.0
- *   W4A4 K=N=4096:      M=256 64x64 13.7 -> 14.4, 64x192 21.5 -> 23.0, 128x128 23.0 -> 21.5
- * so lines everywhere except the 64x64 tile and the nibble kinds' 64-row tiles. ORK_ALINE=0/1 forces it
- * (tests, A/B timing). */
-static int aline_rule(const ork_npu *c, int rkind, const orkh_plan *q) {
-    /* the kernel has the line layout only where a stage row is one 128-byte line: K-blocks per stage as
+/* A-stage layout of the LDS-ring kernel: whole 128-byte row lines (swizzled LDS image; a stage row of 1, 2 or 4
+ * lines) or MFMA fragment order. Measured on MI355X, graph-timed, both layouts alternated three times in one run,
+ * exact (us, fragment -> line):
+ *   one line a stage row:  int8 64x64 K=2048 N=6144 M=128 8.25 -> 7.95, M=256 13.44 -> 11.73, K=N=2048 M=128 7.87 ->
+ *                          7.68, M=512 7.88 -> 7.83; int8 64x192 M=256 12.62 -> 11.95, M=512 13.09 -> 12.91; int8
+ *                          32x64 M=96 10.90 -> 10.51; int8 128x96 M=512 14.64 -> 12.36; fp16 64x64 K=N=2048 M=128
+ *                          12.64 -> 13.05, M=512 12.41 -> 13.18, K=2048 N=6144 M=128 13.83 -> 13.27, M=256 22.92 ->
+ *                          20.12; fp16 32x64 M=96 K=N=2048 11.29 -> 11.48, M=256 11.19 -> 11.39; NF4 64x64 M=128
+ *                          9.57 -> 9.68, M=256 14.26 -> 14.69
+ *   2-4 lines a stage row: W4A4 K=N=4096 64x64 M=256 11.98 -> 10.07, 32x32 M=64 8.19 -> 6.83, 16x32 M=32 6.17 ->
+ *                          5.64; W4A8 K=2048 N=6144 64x64 M=128 8.01 -> 7.33, 64x192 M=512 11.78 -> 11.57, 32x64
+ *                          M=64 5.84 -> 5.90 (W4A4 M=128 7.91 -> 8.06, M=96 8.40 -> 8.10); NF4 32x64 M=64 6.98 ->
+ *                          7.04, M=96 12.43 -> 12.57, 16x64 M=48 11.57 -> 11.65, 32x32 K=N=2048 M=64 5.69 -> 5.55;
+ *                          NF4 128x96 M=256 14.29 -> 14.26, M=512 14.96 -> 14.92; int8 32x32 K=N=2048 M=128 5.68 ->
+ *                          5.55, 16x32 M=32 5.56 -> 5.34; fp16 32x32 M=128 8.06 -> 7.64, 16x32 M=48 7.35 -> 6.87,
+ *                          16x64 M=64 9.49 -> 9.21
+ * so lines except: fp16 32x64, and fp16 64x64 unless N > 4096; the nibble kinds' 32x64 tile; NF4's 64x64, 128x96
+ * (no gain) and 16-row tiles. ORK_ALINE=0/1 forces it (tests, A/B timing). */
+static int aline_rule(const ork_npu *c, int rkind, const orkh_plan *q, int N) {
+    /* the kernel has the line layout only where a stage row is whole 128-byte lines: K-blocks per stage as
      * k_tiled2's t2_ks (1 for int4 kinds, 1 for 256 x 256, else 2; at least the tile's K groups of waves) */
     /* k_tiled2's wave grid (t2_xg, t2_wn): 2 x 4 on the uniform-int4 64 x 192 tile, 2 x 2 on its 64 x 64 tile */
     const int xg = (rkind == ORKH_I4U && q->bm == 64) ? (q->bn == 192 ? 1 : q->bn == 64 ? 2 : 0) : 0;
@@ -302,17 +312,22 @@ static int aline_rule(const ork_npu *c, int rkind, const orkh_plan *q) {
     const int nb = xg == 2 ? 2 : (nbt < 4 ? nbt : (nbt % 4 == 0 ? 4 : 2)), wk = 16 / (mb * nb);
     const int base = (rkind == ORKH_I4U || rkind == ORKH_NF4) ? 1 : (q->bm * q->bn >= 65536 ? 1 : 2);
     const int ks = base > wk ? base : wk;
-    if (ks * a_bytes_per_kb(rkind) != 128) return 0;
+    const int row_bytes = ks * a_bytes_per_kb(rkind);
+    if (row_bytes % 128) return 0;
     const char *e = knob(c, "ORK_ALINE");
     if (e) return atoi(e) != 0;
-    if (q->bm == 64 && q->bn == 64) return 0;
-    if ((rkind == ORKH_I4U || rkind == ORKH_NF4) && q->bm == 64) return 0;
+    if (rkind == ORKH_F16) {
+        if (q->bm == 32 && q->bn == 64) return 0;
+        if (q->bm == 64 && q->bn == 64) return N > 4096;
+    }
+    if ((rkind == ORKH_I4U || rkind == ORKH_NF4) && q->bm == 32 && q->bn == 64) return 0;
+    if (rkind == ORKH_NF4 && ((q->bm == 64 && q->bn == 64) || q->bm == 16 || (q->bm == 128 && q->bn == 96))) return 0;
     return 1;
 }
 
 int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_plan *q, size_t *ws_bytes) {
     const int rc = plan_core(c, rkind, M, K, N, KB, q, ws_bytes);
-    if (q->algo == ORKH_ALGO_TILED2) q->aline = aline_rule(c, rkind, q);
+    if (q->algo == ORKH_ALGO_TILED2) q->aline = aline_rule(c, rkind, q, N);
     /* The LDS-ring kernel's two-slot ring (two workgroups per CU, where the kernel has it for the tile) on grids of
      * more than one round of the CUs: one workgroup's set-up, first stage and epilogue overlap the other's loop.
      * Measured against the 4-slot ring (graph-timed, us; K=2048 N=6144 unless given): int8 64x192 M=768 22.95 ->
@@ -331,7 +346,7 @@ int orki_plan(const ork_npu *c, int rkind, int M, int K, int N, int KB, orkh_pla
         if (rkind == ORKH_I4U && !fr && !knob(c, "ORK_TILE") && q->bm == 64 && q->bn == 192 && q->ksplit <= 1 &&
             wgs > cu && w128 > cu && orkh_tiled2_ring2_ok(rkind, 128, 128)) {
             q->bm = q->bn = 128;
-            q->aline = aline_rule(c, rkind, q);
+            q->aline = aline_rule(c, rkind, q, N);
             wgs = w128;
         }
         if (fr) q->ring = atoi(fr) == 2 ? 2 : 0;

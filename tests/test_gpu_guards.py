@@ -261,7 +261,8 @@ def test_allwave_epilogue_c_alignment_guards(gnpu, shift, M, kind, tile):
         with _env({"ORK_TILE": tile}):
             name = gnpu.plan_name(w, M)
             _say("all-wave epilogue C alignment", kind, M, shift, name)
-            assert name == ("tiled2_i4u_" if kind == "w4a4" else "tiled2_f16_") + tile, name
+            base = ("tiled2_i4u_" if kind == "w4a4" else "tiled2_f16_") + tile
+            assert name in (base, base + "_al"), name   # either A-stage layout: the C stores are the same
             assert run(gnpu.h, w, M, dA, g.c + shift) == 0
         got = g.read()
         g.check(got, name)
