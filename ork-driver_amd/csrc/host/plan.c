@@ -236,6 +236,71 @@ static void nf4_best(const ork_npu *c, int M, int N, int KB, int cu, orkh_plan *
     }
 }
 
+/* int8, fp16 and uniform int4 above 64 rows: like NF4, every LDS-ring tile has its own least-squares fit (relative
+ * error, non-negative terms) to graph-timed launches on MI355X, in the form of nf4_fits, KiB being the A and B bytes
+ * one workgroup loads (tests/golden/mma_plan_sweep.json: every tile and K split of 1, 2 and 4 on offer at
+ * K x N = 2048 x 6144, 2048 x 2048, 4096 x 4096, 6144 x 2048, 2048 x 12288 and M = 96..2048; the 32- and 16-row
+ * tiles for one round of the CUs only). A tile is priced only where its rows are at most twice M, as timed. */
+static const struct mma_fit {
+    int rkind, bm, bn, ksmax; /* ksmax: the largest K split timed (and offered) */
+    double a, b, c, d, e;
+} mma_fits[] = { /* kind, tile, ksmax, a..e; then the launches fitted and the fit's rms relative error */
+    {ORKH_I8, 256, 256, 4, 3.7521, 1.6705, 0.0216, 3.8711, 0.3643}, /* 93, 6.8% */
+    {ORKH_I8, 128, 128, 4, 3.0448, 0.5465, 0.0158, 2.6331, 0.4416}, /* 108, 7.3% */
+    {ORKH_I8, 128, 96, 4, 3.8213, 0.7067, 0.0158, 2.3114, 0.4399}, /* 108, 6.5% */
+    {ORKH_I8, 64, 192, 4, 3.7419, 0.0000, 0.0151, 2.2078, 0.4775}, /* 108, 7.3% */
+    {ORKH_I8, 64, 64, 4, 2.9950, 0.5352, 0.0159, 2.6431, 0.3938}, /* 108, 4.9% */
+    {ORKH_I8, 32, 64, 2, 2.7075, 0.0000, 0.0223, 2.1784, 0.4903}, /* 14, 0.6% */
+    {ORKH_I8, 32, 32, 1, 0.0000, 2.8325, 0.0182, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_I8, 16, 64, 1, 0.0000, 2.6976, 0.0192, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_F16, 256, 256, 4, 0.0000, 5.3384, 0.0214, 3.3097, 0.3464}, /* 93, 7.7% */
+    {ORKH_F16, 128, 128, 4, 4.0513, 0.2838, 0.0157, 1.9461, 0.4494}, /* 108, 6.7% */
+    {ORKH_F16, 128, 96, 4, 4.9447, 0.7181, 0.0152, 1.2865, 0.4347}, /* 108, 5.9% */
+    {ORKH_F16, 64, 192, 4, 5.3544, 0.0000, 0.0149, 0.9560, 0.4698}, /* 108, 6.9% */
+    {ORKH_F16, 64, 64, 4, 3.1972, 0.0000, 0.0183, 2.6696, 0.4227}, /* 108, 5.1% */
+    {ORKH_F16, 32, 64, 2, 0.0000, 2.6337, 0.0224, 2.4172, 0.4000}, /* 14, 1.6% */
+    {ORKH_F16, 32, 32, 1, 0.0000, 3.1949, 0.0173, 0.0000, 0.0000}, /* 4, 0.1% */
+    {ORKH_F16, 16, 64, 1, 0.0000, 3.4350, 0.0176, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_I4U, 128, 128, 4, 4.2411, 0.0000, 0.0223, 2.3879, 0.4292}, /* 108, 5.9% */
+    {ORKH_I4U, 128, 96, 4, 1.9526, 2.9686, 0.0192, 2.5525, 0.3956}, /* 108, 6.5% */
+    {ORKH_I4U, 64, 192, 4, 1.3771, 3.4293, 0.0180, 2.6350, 0.3642}, /* 108, 7.1% */
+    {ORKH_I4U, 64, 64, 4, 0.5591, 3.0326, 0.0157, 3.5336, 0.2572}, /* 108, 5.7% */
+    {ORKH_I4U, 32, 64, 2, 2.8548, 0.0000, 0.0197, 2.2861, 0.4331}, /* 14, 0.7% */
+    {ORKH_I4U, 32, 32, 1, 0.0000, 3.1149, 0.0173, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_I4U, 16, 64, 1, 0.0000, 2.9924, 0.0176, 0.0000, 0.0000}, /* 4, 0.2% */
+};
+
+static double mma_fit_best(int rkind, int M, int N, int KB, int cu, int ks_force, orkh_plan *q) {
+    const int NB = N / 16;
+    const double part = (double)M * N * 4 / 1e6;
+    double best = -1;
+    for (size_t i = 0; i < sizeof mma_fits / sizeof mma_fits[0]; i++) {
+        const struct mma_fit *f = &mma_fits[i];
+        if (f->rkind != rkind || f->bm > 2 * M) continue;
+        for (int ks = 1; ks <= f->ksmax; ks *= 2) {
+            if (ks_force > 0 && ks != ks_force) continue;
+            const int kbs = cdiv(KB, ks);
+            if (cdiv(KB, kbs) != ks || (ks > 1 && kbs < 4)) continue;
+            const long wgs = (long)cdiv(M, f->bm) * cdiv(NB, f->bn / 16) * ks;
+            if (f->bm <= 32 && wgs > cu) continue;
+            const double rounds = (double)((wgs + cu - 1) / cu);
+            const double kib = ((double)f->bm * a_bytes_per_kb(rkind) + (double)f->bn * 64) * kbs / 1024;
+            double t = f->a + rounds * (f->b + f->c * kib);
+            if (ks > 1) t += f->d + f->e * ks * part;
+            if (best < 0 || t < best - 1e-9) {
+                best = t;
+                memset(q, 0, sizeof *q);
+                q->algo = ORKH_ALGO_TILED2;
+                q->bm = f->bm;
+                q->bn = f->bn;
+                q->ksplit = ks;
+                q->kbs = kbs;
+            }
+        }
+    }
+    return best;
+}
+
 /* The LDS-ring kernel (k_tiled2): every tile and split on offer priced by the model above; A counts the
  * whole tile height, since rows past M still issue (zero-filled) loads. Returns the modelled time of
  * the best and fills q with it. */
@@ -434,8 +499,10 @@ static int plan_core(const ork_npu *c, int rkind, int M, int K, int N, int KB, o
 
     /* (NF4 reaches here only with ORK_KSPLIT forced: k_tiled up to 128 rows, the LDS-ring kernel above) */
     if ((rkind != ORKH_NF4 || M > 128) && !f_tiled) {
-        /* uniform int4 skips the 256 x 256 tile: with the nibble decode its registers spill (20 B per lane) */
-        tiled2_best(rkind, M, N, KB, cu, ks_force, rkind == ORKH_I4U, q);
+        /* int8, fp16 and uniform int4: the per-tile fits (uniform int4 has no 256 x 256 fit: with the nibble decode
+         * its registers spill, 20 B per lane); a forced split they were not timed at takes the shared model */
+        if (rkind == ORKH_NF4 || mma_fit_best(rkind, M, N, KB, cu, ks_force, q) < 0)
+            tiled2_best(rkind, M, N, KB, cu, ks_force, rkind == ORKH_I4U, q);
         if (q->ksplit > 1) *ws_bytes = (size_t)q->ksplit * M * N * 4;
         return 0;
     }

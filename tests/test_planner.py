@@ -83,3 +83,26 @@ def test_two_slot_ring_picks(planner):
     # exceed one round (K=2048 N=6144 M=768: 21.74 -> 19.96 us), not where 64 x 192 fills one (K=N=4096 M=512)
     got = planner([(1, 768, 2048, 6144), (1, 512, 4096, 4096)])
     assert got[0] == "tiled2_i4u_128x128_al_r2" and got[1].startswith("tiled2_i4u_64x192") and "_r2" not in got[1], got
+
+
+@pytest.mark.parametrize("kind", ["int8", "i4u", "fp16"])
+def test_mma_picks_against_the_sweep(planner, kind):
+    """int8, fp16 and uniform int4 above 64 rows (tests/golden/mma_plan_sweep.json: graph-timed launches of every
+    LDS-ring tile and K split on offer at 30-40 shapes per kind): each pick is a timed candidate within 15% of the
+    fastest at its shape, and the picks total within 2% of the fastest candidates' total."""
+    data = json.load(open(os.path.join(ROOT, "tests", "golden", "mma_plan_sweep.json")))
+    shapes = [s for s in data["shapes"] if s["kind"] == kind]
+    if not shapes:
+        pytest.skip(f"no {kind} launches in the sweep")
+    rk = {"int8": 0, "i4u": 1, "fp16": 3}[kind]
+    picks = planner([(rk, s["M"], s["K"], s["N"]) for s in shapes])
+    tot_pick = tot_best = 0.0
+    worst = []
+    for s, p in zip(shapes, picks):
+        best = min(s["us"].values())
+        assert p in s["us"], (s["K"], s["N"], s["M"], p)
+        worst.append((s["us"][p] / best, s["K"], s["N"], s["M"], p))
+        tot_pick += s["us"][p]
+        tot_best += best
+    assert max(worst)[0] <= 1.15, max(worst)
+    assert tot_pick <= 1.02 * tot_best, (tot_pick, tot_best, sorted(worst)[-3:])
