@@ -1902,18 +1902,20 @@ template <int KIND, int BM, int BN> constexpr int t2g_ks() {
 }
 
 template <int KIND, int BM, int BN, int KS>
-int launch_tiled2g_k(const orkh_mm *p, const T2Group &gp, hipStream_t s, size_t sc) {
+int launch_tiled2g_k(const orkh_mm *p, const T2Group &gp, hipStream_t s, size_t sc, bool aline) {
     using P = T2<KIND, BM, BN, KS>;
     const bool whole = gp.G % KT<KIND>::KPB == 0;
-    auto kern = whole ? k_tiled2g<KIND, BM, BN, KS, 2, false> : k_tiled2g<KIND, BM, BN, KS, 1, false>;
+    const bool al = aline && P::LINE_OK;
+    auto kern = whole ? (al ? k_tiled2g<KIND, BM, BN, KS, 2, true> : k_tiled2g<KIND, BM, BN, KS, 2, false>)
+                      : (al ? k_tiled2g<KIND, BM, BN, KS, 1, true> : k_tiled2g<KIND, BM, BN, KS, 1, false>);
     const size_t lds = P::LDS + sc;
     const int Sk = p->K / gp.G;
     if (lds > 163840) {
         snprintf(g_lerr, sizeof g_lerr, "grouped tiled2 %dx%d: %d groups need %zu B of LDS", BM, BN, Sk, lds);
         return -2;
     }
-    static lds_flags attr[2]; // per instantiation: allow up to 160 KiB of dynamic LDS
-    if (lds_limit((const void *)kern, 163840, attr[whole])) return -1;
+    static lds_flags attr[2][2]; // per instantiation: allow up to 160 KiB of dynamic LDS
+    if (lds_limit((const void *)kern, 163840, attr[whole][al])) return -1;
     const int mtiles = (p->M + BM - 1) / BM;
     const int ntiles = (p->N / 16 + P::NB - 1) / P::NB;
     if ((long)mtiles * ntiles >= (1L << 24)) { // the kernel's tile-index division is exact below 2^24
@@ -1925,24 +1927,24 @@ int launch_tiled2g_k(const orkh_mm *p, const T2Group &gp, hipStream_t s, size_t 
 }
 
 template <int KIND, int BM, int BN>
-int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s) {
+int launch_tiled2g_v(const orkh_mm *p, const T2Group &gp, hipStream_t s, bool al) {
     const int Sk = p->K / gp.G;
     const size_t sc = (size_t)((BM * Sk * 4 + 1023) / 1024 + (Sk * BN * 4 + 1023) / 1024) * 1024; // the tile's scales
     constexpr int KD = t2g_ks<KIND, BM, BN>(), K1 = t2_ks<KIND, BM, BN>();
     const bool whole = gp.G % KT<KIND>::KPB == 0;
     if constexpr (KD != K1) {
-        if (whole && T2<KIND, BM, BN, KD>::LDS + sc <= 163840) return launch_tiled2g_k<KIND, BM, BN, KD>(p, gp, s, sc);
+        if (whole && T2<KIND, BM, BN, KD>::LDS + sc <= 163840) return launch_tiled2g_k<KIND, BM, BN, KD>(p, gp, s, sc, al);
     }
     if constexpr (KD > 2 && K1 < 2) {
-        if (whole && T2<KIND, BM, BN, 2>::LDS + sc <= 163840) return launch_tiled2g_k<KIND, BM, BN, 2>(p, gp, s, sc);
+        if (whole && T2<KIND, BM, BN, 2>::LDS + sc <= 163840) return launch_tiled2g_k<KIND, BM, BN, 2>(p, gp, s, sc, al);
     }
-    return launch_tiled2g_k<KIND, BM, BN, K1>(p, gp, s, sc);
+    return launch_tiled2g_k<KIND, BM, BN, K1>(p, gp, s, sc, al);
 }
 
 template <int KIND>
 int launch_tiled2g(const orkh_mm *p, const orkh_plan *q, const T2Group &gp, hipStream_t s) {
-    if (q->bm == 64 && q->bn == 192) return launch_tiled2g_v<KIND, 64, 192>(p, gp, s);
-    if (q->bm == 64 && q->bn == 64) return launch_tiled2g_v<KIND, 64, 64>(p, gp, s);
+    if (q->bm == 64 && q->bn == 192) return launch_tiled2g_v<KIND, 64, 192>(p, gp, s, q->aline);
+    if (q->bm == 64 && q->bn == 64) return launch_tiled2g_v<KIND, 64, 64>(p, gp, s, q->aline);
     snprintf(g_lerr, sizeof g_lerr, "grouped tiled2 plan: %dx%d unsupported", q->bm, q->bn);
     return -2;
 }

@@ -577,6 +577,9 @@ void orki_plan_grouped(const ork_npu *c, int rkind, int M, int K, int N, int KB,
             if (ring > 0 && ring + sc <= 163840) {
                 q->ksplit = 1;
                 q->kbs = KB;
+                /* A stages as whole row lines where the stage row is whole lines (the kernel checks) */
+                const char *fa = knob(c, "ORK_ALINE");
+                q->aline = fa ? atoi(fa) != 0 : 1;
                 /* write-through C stores on a grid of one round, as for the plain runs */
                 const char *fc = knob(c, "ORK_CWT");
                 q->cwt = fc ? atoi(fc) != 0 : (long)cdiv(M, q->bm) * cdiv(N / 16, q->bn / 16) <= cu;
