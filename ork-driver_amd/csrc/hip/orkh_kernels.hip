@@ -772,15 +772,25 @@ template <int KIND, int BM, int BN, class P> constexpr int t2_issue_at() {
 // stage's load count must divide evenly. Graph-timed against every wave issuing (one build each, alternated twice
 // on one box; exact): 8 loader waves on uniform int4's 64 x 192 tile (2 x 4 x 2 grid): W4A4 K=N=4096 M=512 18.04 ->
 // 16.80 us, W4A8 K=2048 N=6144 M=512 12.23 -> 11.70, M=256 12.07 -> 11.45; 4 on the NF4 K-group tiles (32 x 64, C3
-// NF4 M=64 7.36 -> 6.98) and on 256 x 256 (M=K=N=4096 int8 67.1 -> 65.6, fp16 134.3 -> 126.0). Elsewhere no gain
-// (int8 64 x 192 M=512: 8 loaders -0.2 to -0.8%, 4 +2.6 to +3.0%; two-slot rings +4 to +9%; uniform int4 32 x 64 with
-// 8: +3.5%), so every wave issues.
+// NF4 M=64 7.36 -> 6.98) and on 256 x 256 (M=K=N=4096 int8 67.1 -> 65.6, fp16 134.3 -> 126.0). Once A stages were
+// line-loaded (rows of 2 and 4 lines included), 8 loader waves also on: uniform int4's 2 x 2 x 4 64 x 64 tile (W4A4
+// K=N=4096 M=256 9.97 -> 9.14, W4A8 K=2048 N=6144 M=128 7.33 -> 6.65, M=96 7.03 -> 6.45; 4 loaders 9.66); the 32 x 32
+// and 16 x 32 K-group tiles (fp16 K=N=2048 M=128 7.61 -> 7.25, M=48 6.84 -> 6.32; int8 M=128 5.52 -> 5.27, M=64 5.24
+// -> 4.83, K=6144 N=2048 M=32 8.62 -> 8.05; W4A4 K=N=4096 M=64 6.90 -> 6.35; W4A8 K=N=2048 M=64 4.03 -> 3.87); int8
+// 64 x 64 (K=2048 N=6144 M=128 7.89 -> 7.59, K=N=2048 M=512 7.85 -> 7.40); 128 x 128 (W4A8 K=2048 N=6144 M=512 13.28
+// -> 12.46, fp16 21.85 -> 21.26, int8 K=N=4096 M=512 20.31 -> 19.83, K=2048 N=6144 12.51 -> 12.45). Elsewhere no gain
+// (int8 64 x 192 M=512: 8 loaders -0.2 to -0.8%, 4 +2.6 to +3.0%; the two-slot rings +4 to +9%; the 32 x 64 tiles
+// -0.3 to +1.6%; 128 x 96 and fp16 64 x 64 within 0.5%), so there every wave issues.
 template <int KIND, int BM, int BN, class P> constexpr int t2_loaders() {
     int lw = P::NW;
     if (P::R <= 2) return lw;
     if (KIND == ORKH_I4U && BM == 64 && BN == 192) lw = 8;
     else if (KIND == ORKH_NF4 && P::WK > 1) lw = 4;
     else if ((KIND == ORKH_I8 || KIND == ORKH_F16) && BM == 256 && BN == 256) lw = 4;
+    else if (KIND != ORKH_NF4 && BM == 128 && BN == 128) lw = 8;
+    else if (KIND == ORKH_I4U && BM == 64 && BN == 64 && P::WK > 1) lw = 8;
+    else if (KIND == ORKH_I8 && BM == 64 && BN == 64) lw = 8;
+    else if (KIND != ORKH_NF4 && BN == 32 && (BM == 32 || BM == 16)) lw = 8;
     return P::NI % lw == 0 ? lw : P::NW;
 }
 

@@ -245,29 +245,29 @@ static const struct mma_fit {
     int rkind, bm, bn, ksmax; /* ksmax: the largest K split timed (and offered) */
     double a, b, c, d, e;
 } mma_fits[] = { /* kind, tile, ksmax, a..e; then the launches fitted and the fit's rms relative error */
-    {ORKH_I8, 256, 256, 4, 3.7521, 1.6705, 0.0216, 3.8711, 0.3643}, /* 93, 6.8% */
-    {ORKH_I8, 128, 128, 4, 3.0448, 0.5465, 0.0158, 2.6331, 0.4416}, /* 108, 7.3% */
-    {ORKH_I8, 128, 96, 4, 3.8213, 0.7067, 0.0158, 2.3114, 0.4399}, /* 108, 6.5% */
-    {ORKH_I8, 64, 192, 4, 3.7419, 0.0000, 0.0151, 2.2078, 0.4775}, /* 108, 7.3% */
-    {ORKH_I8, 64, 64, 4, 2.9950, 0.5352, 0.0159, 2.6431, 0.3938}, /* 108, 4.9% */
-    {ORKH_I8, 32, 64, 2, 2.7075, 0.0000, 0.0223, 2.1784, 0.4903}, /* 14, 0.6% */
-    {ORKH_I8, 32, 32, 1, 0.0000, 2.8325, 0.0182, 0.0000, 0.0000}, /* 4, 0.2% */
-    {ORKH_I8, 16, 64, 1, 0.0000, 2.6976, 0.0192, 0.0000, 0.0000}, /* 4, 0.2% */
-    {ORKH_F16, 256, 256, 4, 0.0000, 5.3384, 0.0214, 3.3097, 0.3464}, /* 93, 7.7% */
-    {ORKH_F16, 128, 128, 4, 4.0513, 0.2838, 0.0157, 1.9461, 0.4494}, /* 108, 6.7% */
-    {ORKH_F16, 128, 96, 4, 4.9447, 0.7181, 0.0152, 1.2865, 0.4347}, /* 108, 5.9% */
-    {ORKH_F16, 64, 192, 4, 5.3544, 0.0000, 0.0149, 0.9560, 0.4698}, /* 108, 6.9% */
-    {ORKH_F16, 64, 64, 4, 3.1972, 0.0000, 0.0183, 2.6696, 0.4227}, /* 108, 5.1% */
-    {ORKH_F16, 32, 64, 2, 0.0000, 2.6337, 0.0224, 2.4172, 0.4000}, /* 14, 1.6% */
-    {ORKH_F16, 32, 32, 1, 0.0000, 3.1949, 0.0173, 0.0000, 0.0000}, /* 4, 0.1% */
-    {ORKH_F16, 16, 64, 1, 0.0000, 3.4350, 0.0176, 0.0000, 0.0000}, /* 4, 0.2% */
-    {ORKH_I4U, 128, 128, 4, 4.2411, 0.0000, 0.0223, 2.3879, 0.4292}, /* 108, 5.9% */
-    {ORKH_I4U, 128, 96, 4, 1.9526, 2.9686, 0.0192, 2.5525, 0.3956}, /* 108, 6.5% */
-    {ORKH_I4U, 64, 192, 4, 1.3771, 3.4293, 0.0180, 2.6350, 0.3642}, /* 108, 7.1% */
-    {ORKH_I4U, 64, 64, 4, 0.5591, 3.0326, 0.0157, 3.5336, 0.2572}, /* 108, 5.7% */
-    {ORKH_I4U, 32, 64, 2, 2.8548, 0.0000, 0.0197, 2.2861, 0.4331}, /* 14, 0.7% */
-    {ORKH_I4U, 32, 32, 1, 0.0000, 3.1149, 0.0173, 0.0000, 0.0000}, /* 4, 0.2% */
-    {ORKH_I4U, 16, 64, 1, 0.0000, 2.9924, 0.0176, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_I8, 256, 256, 4, 6.2092, 0.0000, 0.0238, 0.0000, 0.3870}, /* 16, 3.4% */
+    {ORKH_I8, 128, 128, 4, 2.3737, 1.4808, 0.0156, 2.4375, 0.4353}, /* 81, 7.1% */
+    {ORKH_I8, 128, 96, 4, 3.5225, 1.2820, 0.0153, 2.0808, 0.4438}, /* 76, 5.9% */
+    {ORKH_I8, 64, 192, 4, 3.6932, 0.4577, 0.0147, 1.9325, 0.4694}, /* 75, 7.4% */
+    {ORKH_I8, 64, 64, 4, 2.4845, 0.4706, 0.0160, 2.5196, 0.4344}, /* 79, 4.8% */
+    {ORKH_I8, 32, 64, 2, 2.6937, 0.0000, 0.0224, 2.0809, 0.5510}, /* 14, 0.8% */
+    {ORKH_I8, 32, 32, 1, 0.0000, 2.2326, 0.0188, 0.0000, 0.0000}, /* 4, 0.3% */
+    {ORKH_I8, 16, 64, 1, 0.0000, 2.6750, 0.0193, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_F16, 256, 256, 4, 0.5834, 5.7930, 0.0228, 0.0000, 0.3646}, /* 38, 4.9% */
+    {ORKH_F16, 128, 128, 4, 4.2727, 0.2246, 0.0158, 1.6127, 0.4546}, /* 92, 6.3% */
+    {ORKH_F16, 128, 96, 4, 5.2291, 0.6159, 0.0151, 1.1021, 0.4404}, /* 94, 6.0% */
+    {ORKH_F16, 64, 192, 4, 6.0050, 0.0000, 0.0145, 0.6227, 0.4643}, /* 87, 7.3% */
+    {ORKH_F16, 64, 64, 4, 3.1675, 0.0000, 0.0182, 2.6459, 0.4374}, /* 89, 5.4% */
+    {ORKH_F16, 32, 64, 2, 2.6285, 0.0000, 0.0224, 2.4098, 0.3979}, /* 13, 1.7% */
+    {ORKH_F16, 32, 32, 1, 0.0000, 2.7870, 0.0174, 0.0000, 0.0000}, /* 4, 0.4% */
+    {ORKH_F16, 16, 64, 1, 0.0000, 3.4548, 0.0176, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_I4U, 128, 128, 4, 2.2998, 1.7452, 0.0209, 2.5598, 0.4145}, /* 57, 5.8% */
+    {ORKH_I4U, 128, 96, 4, 0.7049, 4.8868, 0.0178, 2.3325, 0.3942}, /* 44, 4.9% */
+    {ORKH_I4U, 64, 192, 4, 0.2553, 4.8169, 0.0173, 2.5279, 0.3592}, /* 57, 5.6% */
+    {ORKH_I4U, 64, 64, 4, 0.3743, 3.0064, 0.0137, 2.3628, 0.4714}, /* 61, 3.8% */
+    {ORKH_I4U, 32, 64, 2, 2.8688, 0.0000, 0.0196, 2.2564, 0.4203}, /* 14, 0.8% */
+    {ORKH_I4U, 32, 32, 1, 0.0000, 2.7450, 0.0157, 0.0000, 0.0000}, /* 4, 0.1% */
+    {ORKH_I4U, 16, 64, 1, 0.0000, 2.9825, 0.0176, 0.0000, 0.0000}, /* 4, 0.2% */
 };
 
 static double mma_fit_best(int rkind, int M, int N, int KB, int cu, int ks_force, orkh_plan *q) {

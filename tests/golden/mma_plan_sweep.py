@@ -11,7 +11,9 @@ kernels as W4A8.
 
 The fit of each candidate (kind, tile, split or not) is the form plan.c evaluates,
     t = a + rounds * (b + c * KiB) + [ks > 1] (d + e * ks * M * N * 4 / 1e6)   us,
-KiB being the A and B bytes one workgroup loads, by least squares on the relative error with non-negative terms.
+KiB being the A and B bytes one workgroup loads, by least squares on the relative error with non-negative terms,
+over the candidate's launches that ran within twice the fastest candidate at their shape (where the planner's choice
+is made; the far slower ones, e.g. 4-way splits of many rounds, would otherwise pull the fit away from it).
 """
 import json
 import os
@@ -140,11 +142,16 @@ def fit(rows):
 def reduce(lines):
     """per shape, the fastest exact time of each plan name; per candidate, its fit"""
     shapes, groups = {}, {}
+    lines = [r for r in lines if r["exact"] and r["us"]]
+    fastest = {}
     for r in lines:
-        if not r["exact"] or not r["us"]:
-            continue
+        k = (r["kind"], r["K"], r["N"], r["M"])
+        fastest[k] = min(fastest.get(k, 1e9), min(r["us"]))
+    for r in lines:
         s = shapes.setdefault((r["kind"], r["K"], r["N"], r["M"]), {})
         s[r["plan"]] = min(s.get(r["plan"], 1e9), min(r["us"]))
+        if min(r["us"]) > 2 * fastest[(r["kind"], r["K"], r["N"], r["M"])]:
+            continue
         groups.setdefault((r["kind"], r["tile"]), []).append(
             (features(r["kind"], r["tile"], r["ks"], r["M"], r["K"], r["N"]), min(r["us"]), r["ks"]))
     fits = {}
