@@ -780,12 +780,14 @@ template <int KIND, int BM, int BN, class P> constexpr int t2_issue_at() {
 // 64 x 64 (K=2048 N=6144 M=128 7.89 -> 7.59, K=N=2048 M=512 7.85 -> 7.40); 128 x 128 (W4A8 K=2048 N=6144 M=512 13.28
 // -> 12.46, fp16 21.85 -> 21.26, int8 K=N=4096 M=512 20.31 -> 19.83, K=2048 N=6144 12.51 -> 12.45). Elsewhere no gain
 // (int8 64 x 192 M=512: 8 loaders -0.2 to -0.8%, 4 +2.6 to +3.0%; the two-slot rings +4 to +9%; the 32 x 64 tiles
-// -0.3 to +1.6%; 128 x 96 and fp16 64 x 64 within 0.5%), so there every wave issues.
+// -0.3 to +1.6%; 128 x 96 and fp16 64 x 64 within 0.5%), so there every wave issues. NF4's 64 x 64 tile takes 4 (K=2048
+// N=6144 M=128 9.58 -> 9.41, K=6144 N=2048 M=128 split 4 ways 12.66 -> 12.30; 8 loaders no gain); its 128 x 96 and
+// 128 x 128 tiles gain nothing from 4 or 8.
 template <int KIND, int BM, int BN, class P> constexpr int t2_loaders() {
     int lw = P::NW;
     if (P::R <= 2) return lw;
     if (KIND == ORKH_I4U && BM == 64 && BN == 192) lw = 8;
-    else if (KIND == ORKH_NF4 && P::WK > 1) lw = 4;
+    else if (KIND == ORKH_NF4 && (P::WK > 1 || (BM == 64 && BN == 64))) lw = 4;
     else if ((KIND == ORKH_I8 || KIND == ORKH_F16) && BM == 256 && BN == 256) lw = 4;
     else if (KIND != ORKH_NF4 && BM == 128 && BN == 128) lw = 8;
     else if (KIND == ORKH_I4U && BM == 64 && BN == 64 && P::WK > 1) lw = 8;
