@@ -782,7 +782,9 @@ template <int KIND, int BM, int BN, class P> constexpr int t2_issue_at() {
 // (int8 64 x 192 M=512: 8 loaders -0.2 to -0.8%, 4 +2.6 to +3.0%; the two-slot rings +4 to +9%; the 32 x 64 tiles
 // -0.3 to +1.6%; 128 x 96 and fp16 64 x 64 within 0.5%), so there every wave issues. NF4's 64 x 64 tile takes 4 (K=2048
 // N=6144 M=128 9.58 -> 9.41, K=6144 N=2048 M=128 split 4 ways 12.66 -> 12.30; 8 loaders no gain); its 128 x 96 and
-// 128 x 128 tiles gain nothing from 4 or 8.
+// 128 x 128 tiles gain nothing from 4 or 8. 4 loader waves on int8 128 x 96 (K=N=4096 M=512 18.97-19.01 -> 18.23-18.27,
+// K=2048 N=6144 M=384 11.98 -> 11.65-11.72, M=512 12.76-12.86 -> 12.69-12.78; 8 measured no gain) and fp16 64 x 64
+// (C2 M=512 12.39-12.44 -> 12.26-12.27); fp16 128 x 96 with 4: +0.6%.
 template <int KIND, int BM, int BN, class P> constexpr int t2_loaders() {
     int lw = P::NW;
     if (P::R <= 2) return lw;
@@ -790,6 +792,7 @@ template <int KIND, int BM, int BN, class P> constexpr int t2_loaders() {
     else if (KIND == ORKH_NF4 && (P::WK > 1 || (BM == 64 && BN == 64))) lw = 4;
     else if ((KIND == ORKH_I8 || KIND == ORKH_F16) && BM == 256 && BN == 256) lw = 4;
     else if (KIND != ORKH_NF4 && BM == 128 && BN == 128) lw = 8;
+    else if ((KIND == ORKH_I8 && BM == 128 && BN == 96) || (KIND == ORKH_F16 && BM == 64 && BN == 64)) lw = 4;
     else if (KIND == ORKH_I4U && BM == 64 && BN == 64 && P::WK > 1) lw = 8;
     else if (KIND == ORKH_I8 && BM == 64 && BN == 64) lw = 8;
     else if (KIND != ORKH_NF4 && BN == 32 && (BM == 32 || BM == 16)) lw = 8;
