@@ -245,29 +245,29 @@ static const struct mma_fit {
     int rkind, bm, bn, ksmax; /* ksmax: the largest K split timed (and offered) */
     double a, b, c, d, e;
 } mma_fits[] = { /* kind, tile, ksmax, a..e; then the launches fitted and the fit's rms relative error */
-    {ORKH_I8, 256, 256, 4, 6.2092, 0.0000, 0.0238, 0.0000, 0.3870}, /* 16, 3.4% */
-    {ORKH_I8, 128, 128, 4, 2.3737, 1.4808, 0.0156, 2.4375, 0.4353}, /* 81, 7.1% */
-    {ORKH_I8, 128, 96, 4, 3.5225, 1.2820, 0.0153, 2.0808, 0.4438}, /* 76, 5.9% */
-    {ORKH_I8, 64, 192, 4, 3.6932, 0.4577, 0.0147, 1.9325, 0.4694}, /* 75, 7.4% */
-    {ORKH_I8, 64, 64, 4, 2.4845, 0.4706, 0.0160, 2.5196, 0.4344}, /* 79, 4.8% */
-    {ORKH_I8, 32, 64, 2, 2.6937, 0.0000, 0.0224, 2.0809, 0.5510}, /* 14, 0.8% */
-    {ORKH_I8, 32, 32, 1, 0.0000, 2.2326, 0.0188, 0.0000, 0.0000}, /* 4, 0.3% */
-    {ORKH_I8, 16, 64, 1, 0.0000, 2.6750, 0.0193, 0.0000, 0.0000}, /* 4, 0.2% */
-    {ORKH_F16, 256, 256, 4, 0.5834, 5.7930, 0.0228, 0.0000, 0.3646}, /* 38, 4.9% */
-    {ORKH_F16, 128, 128, 4, 4.2727, 0.2246, 0.0158, 1.6127, 0.4546}, /* 92, 6.3% */
-    {ORKH_F16, 128, 96, 4, 5.2291, 0.6159, 0.0151, 1.1021, 0.4404}, /* 94, 6.0% */
-    {ORKH_F16, 64, 192, 4, 6.0050, 0.0000, 0.0145, 0.6227, 0.4643}, /* 87, 7.3% */
-    {ORKH_F16, 64, 64, 4, 3.1675, 0.0000, 0.0182, 2.6459, 0.4374}, /* 89, 5.4% */
-    {ORKH_F16, 32, 64, 2, 2.6285, 0.0000, 0.0224, 2.4098, 0.3979}, /* 13, 1.7% */
-    {ORKH_F16, 32, 32, 1, 0.0000, 2.7870, 0.0174, 0.0000, 0.0000}, /* 4, 0.4% */
-    {ORKH_F16, 16, 64, 1, 0.0000, 3.4548, 0.0176, 0.0000, 0.0000}, /* 4, 0.2% */
-    {ORKH_I4U, 128, 128, 4, 2.2998, 1.7452, 0.0209, 2.5598, 0.4145}, /* 57, 5.8% */
-    {ORKH_I4U, 128, 96, 4, 0.7049, 4.8868, 0.0178, 2.3325, 0.3942}, /* 44, 4.9% */
-    {ORKH_I4U, 64, 192, 4, 0.2553, 4.8169, 0.0173, 2.5279, 0.3592}, /* 57, 5.6% */
-    {ORKH_I4U, 64, 64, 4, 0.3743, 3.0064, 0.0137, 2.3628, 0.4714}, /* 61, 3.8% */
-    {ORKH_I4U, 32, 64, 2, 2.8688, 0.0000, 0.0196, 2.2564, 0.4203}, /* 14, 0.8% */
-    {ORKH_I4U, 32, 32, 1, 0.0000, 2.7450, 0.0157, 0.0000, 0.0000}, /* 4, 0.1% */
-    {ORKH_I4U, 16, 64, 1, 0.0000, 2.9825, 0.0176, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_I8, 256, 256, 4, 5.8440, 0.0000, 0.0241, 0.0000, 0.3994}, /* 16, 3.1% */
+    {ORKH_I8, 128, 128, 4, 2.1719, 1.6437, 0.0156, 2.4427, 0.4431}, /* 82, 7.2% */
+    {ORKH_I8, 128, 96, 4, 2.9512, 2.1169, 0.0143, 2.2673, 0.4083}, /* 75, 5.9% */
+    {ORKH_I8, 64, 192, 4, 3.4918, 0.7902, 0.0145, 2.0294, 0.4527}, /* 74, 7.5% */
+    {ORKH_I8, 64, 64, 4, 2.4453, 0.5219, 0.0160, 2.5433, 0.4340}, /* 79, 4.6% */
+    {ORKH_I8, 32, 64, 2, 2.7092, 0.0000, 0.0223, 2.3342, 0.4118}, /* 14, 0.6% */
+    {ORKH_I8, 32, 32, 1, 0.0000, 2.2276, 0.0188, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_I8, 16, 64, 1, 0.0000, 2.6950, 0.0192, 0.0000, 0.0000}, /* 4, 0.1% */
+    {ORKH_F16, 256, 256, 4, 0.0880, 6.1768, 0.0227, 0.0000, 0.3771}, /* 38, 4.7% */
+    {ORKH_F16, 128, 128, 4, 4.0377, 0.2295, 0.0161, 1.6667, 0.4677}, /* 92, 6.6% */
+    {ORKH_F16, 128, 96, 4, 5.2807, 0.7426, 0.0150, 0.9779, 0.4447}, /* 91, 6.2% */
+    {ORKH_F16, 64, 192, 4, 5.9856, 0.0000, 0.0145, 0.6252, 0.4682}, /* 89, 7.1% */
+    {ORKH_F16, 64, 64, 4, 2.8047, 0.0000, 0.0180, 2.8555, 0.4211}, /* 92, 6.4% */
+    {ORKH_F16, 32, 64, 2, 2.6572, 0.0000, 0.0223, 2.4686, 0.3812}, /* 13, 1.6% */
+    {ORKH_F16, 32, 32, 1, 0.0000, 2.7401, 0.0175, 0.0000, 0.0000}, /* 4, 0.2% */
+    {ORKH_F16, 16, 64, 1, 0.0000, 3.4902, 0.0175, 0.0000, 0.0000}, /* 4, 0.3% */
+    {ORKH_I4U, 128, 128, 4, 2.1327, 1.8768, 0.0211, 2.5510, 0.4127}, /* 57, 5.8% */
+    {ORKH_I4U, 128, 96, 4, 0.7882, 4.7886, 0.0180, 2.3200, 0.4005}, /* 46, 4.9% */
+    {ORKH_I4U, 64, 192, 4, 0.1933, 4.9232, 0.0174, 2.4635, 0.3617}, /* 57, 5.8% */
+    {ORKH_I4U, 64, 64, 4, 0.3768, 3.0260, 0.0137, 2.3979, 0.4614}, /* 60, 3.8% */
+    {ORKH_I4U, 32, 64, 2, 0.0000, 2.8698, 0.0196, 2.1311, 0.5144}, /* 14, 0.5% */
+    {ORKH_I4U, 32, 32, 1, 0.0000, 2.7500, 0.0158, 0.0000, 0.0000}, /* 4, 0.1% */
+    {ORKH_I4U, 16, 64, 1, 0.0000, 3.0075, 0.0175, 0.0000, 0.0000}, /* 4, 0.1% */
 };
 
 static double mma_fit_best(int rkind, int M, int N, int KB, int cu, int ks_force, orkh_plan *q) {

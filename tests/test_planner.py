@@ -90,7 +90,7 @@ def test_two_slot_ring_picks(planner):
 def test_mma_picks_against_the_sweep(planner, kind):
     """int8, fp16 and uniform int4 above 64 rows (tests/golden/mma_plan_sweep.json: graph-timed launches of every
     LDS-ring tile and K split on offer at 36-39 shapes per kind): each pick is a timed candidate within 20% of the
-    fastest at its shape (the worst: fp16 K=N=4096 M=256, 24.4 us on 64 x 64 against 20.6 on 128 x 128 split 4 ways,
+    fastest at its shape (the worst: fp16 K=N=4096 M=256, 23.9 us on 64 x 64 against 20.9 on 128 x 128 split 4 ways,
     where both fits are off by ~10%), and the picks total within 2% of the fastest candidates' total."""
     data = json.load(open(os.path.join(ROOT, "tests", "golden", "mma_plan_sweep.json")))
     shapes = [s for s in data["shapes"] if s["kind"] == kind]
